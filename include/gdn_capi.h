@@ -1,0 +1,191 @@
+/*
+ * gdn_capi.h -- C ABI of the MI355X (gfx950) Gated DeltaNet library.
+ *
+ * One shared library, libgdn_mi355x.so, exports the functions below with C
+ * linkage.  They are what the reference's Python kernel boundary would bind
+ * through ctypes (the reference has no compiled code of its own: its GDN
+ * entry points are Python functions in engine/kernels/ that dispatch to
+ * Helion/Triton/third-party kernels).  Each declaration names the reference
+ * interface it replaces.
+ *
+ * Conventions shared by every entry point
+ *   - Pointers are device pointers unless stated otherwise.  Nothing here
+ *     allocates device memory, synchronises the device or the stream, or
+ *     keeps state between calls: every kernel is enqueued on `stream`
+ *     (a hipStream_t passed as void*; NULL is the null stream), so calls are
+ *     safe to record into a HIP graph.
+ *   - The return value is a gdn_status_t.  On failure nothing was launched
+ *     and gdn_last_error_string() (thread-local) says why.
+ *   - Token-major activations: element (token t, head h, dim d) of q/k/v lives
+ *     at base + t*stride_t + h*D + d, so strided views of a packed
+ *     [tokens, 2*Hk*K + Hv*V] projection can be passed without a copy.
+ *     Batched inputs [B, T, ...] are addressed as token b*T + t.
+ *   - State tensors are fp32 [*, Hv, K, V] with V contiguous.  A slot index
+ *     array (int64, one entry per sequence) selects rows of a pool; a NULL
+ *     index array means row n for sequence n.  A negative slot id means
+ *     "no slot": the initial state is taken as zero and no state is written.
+ *     Non-negative slot ids must be distinct within one call (duplicates
+ *     race).
+ *   - v-head j uses q/k head j / (Hv / Hk) (HF's repeat_interleave GQA).
+ */
+#ifndef GDN_CAPI_H
+#define GDN_CAPI_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GDN_ABI_VERSION 1
+
+typedef enum {
+  GDN_OK = 0,
+  GDN_ERR_INVALID_ARGUMENT = 1,  /* bad shape, null pointer, bad dtype   */
+  GDN_ERR_UNSUPPORTED = 2,       /* valid but not implemented (e.g. K!=128) */
+  GDN_ERR_WORKSPACE = 3,         /* workspace missing or too small       */
+  GDN_ERR_LAUNCH = 4             /* hipLaunchKernel / hipGetLastError failed */
+} gdn_status_t;
+
+typedef enum {
+  GDN_DTYPE_F32 = 0,
+  GDN_DTYPE_BF16 = 1,
+  GDN_DTYPE_F16 = 2
+} gdn_dtype_t;
+
+/* Library ABI version (GDN_ABI_VERSION of the build). */
+int gdn_abi_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *gdn_last_error_string(void);
+
+/*
+ * Token recurrence: decode (T = 1), speculative verify (T > 1 with
+ * snapshots) and small-T prefill.
+ *
+ * Replaces fla's fused_recurrent_gated_delta_rule, reached from HF's GDN
+ * decode branch (transformers modeling_qwen3_5_moe.py:503-515) and held by
+ * the reference as the torch path at engine/runtime/cuda_graphs.py:126-135,
+ * 201-203; together with the reference cache's gather/scatter around it
+ * (engine/runtime/kv_cache.py:189-208), which the slot indices make
+ * unnecessary.
+ *
+ *   q, k      [tokens, Hk, K] (qkv_dtype, token stride q_stride_t/k_stride_t)
+ *   v         [tokens, Hv, V] (qkv_dtype, token stride v_stride_t)
+ *   g         [tokens, Hv] fp32 log-decay;  beta [tokens, Hv] (beta_dtype)
+ *   state_in  fp32 pool, rows selected by state_in_idx (may be NULL: zero state)
+ *   state_out fp32 pool, rows selected by state_out_idx (may be NULL: not
+ *             written).  state_out == state_in updates the pool in place.
+ *   o         [tokens, Hv, V] (o_dtype, contiguous)
+ *   snapshots fp32 [n_seqs, T, Hv, K, V] or NULL; snapshot t = state after
+ *             token t (requires cu_seqlens == NULL)
+ *   cu_seqlens int32 [n_seqs + 1] (device) or NULL for n_seqs x T tokens
+ *   scale     multiplier of q after the optional l2norm (K^-1/2 by default)
+ * Requires K == V == 128.
+ */
+int gdn_recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
+                      int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
+                      const float *g, const void *beta, int beta_dtype,
+                      const float *state_in, const int64_t *state_in_idx,
+                      float *state_out, const int64_t *state_out_idx,
+                      void *o, int o_dtype, float *snapshots,
+                      const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
+                      int32_t Hk, int32_t Hv, int32_t K, int32_t V,
+                      float scale, int l2norm_qk, void *stream);
+
+/*
+ * Chunk-64 prefill (WY/UT form).
+ *
+ * Replaces engine/kernels/delta_rule.py:352-438 (chunk_gated_delta_rule, the
+ * fla-compatible entry) and the kernels behind it: the Helion kernel
+ * (delta_rule.py:128-263), the torch fallback (:286-349) and fla's Triton
+ * chunk kernels.  Unlike the reference entry, cu_seqlens is honoured.
+ *
+ *   q, k, v, g, beta as for gdn_recurrent_fwd; tokens = n_seqs*T, or
+ *   cu_seqlens[n_seqs] when cu_seqlens (int32, device) is given.
+ *   h0  fp32 initial states (rows by h0_idx) or NULL for zero
+ *   hT  fp32 final states (rows by hT_idx) or NULL; hT may equal h0.
+ *   o   [tokens, Hv, V] o_dtype, contiguous
+ *   workspace  device scratch of at least gdn_chunk_workspace_bytes(...)
+ * Requires K == V == 128 and q/k/v in bf16.
+ */
+int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
+                  int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
+                  const float *g, const void *beta, int beta_dtype,
+                  const float *h0, const int64_t *h0_idx,
+                  float *hT, const int64_t *hT_idx,
+                  void *o, int o_dtype,
+                  const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
+                  int32_t Hk, int32_t Hv, int32_t K, int32_t V,
+                  float scale, int l2norm_qk,
+                  void *workspace, size_t workspace_bytes, void *stream);
+
+/* Workspace bytes gdn_chunk_fwd needs for `total_tokens` tokens in `n_seqs`
+ * sequences (an upper bound that needs no knowledge of the lengths). */
+size_t gdn_chunk_workspace_bytes(int32_t n_seqs, int64_t total_tokens,
+                                 int32_t Hv, int32_t K, int32_t V);
+
+/*
+ * Causal depthwise conv, prefill.
+ *
+ * Replaces causal-conv1d's causal_conv1d_fn as HF's GDN prefill calls it
+ * (transformers modeling_qwen3_5_moe.py:462-478 and :220-240; reference pool
+ * layout engine/runtime/kv_cache.py:142-156), including the cache update HF
+ * does before it (cache_utils.py:1032-1068).
+ *
+ *   x      [tokens, C] (dtype, token stride x_stride_t, channels contiguous)
+ *   w      [C, width] (dtype);  bias [C] (dtype) or NULL
+ *   y      [tokens, C] (dtype, token stride y_stride_t)
+ *   state_in  [*, C, state_len] (dtype) history rows by state_in_idx, or NULL
+ *             for zero history
+ *   state_out [*, C, state_len] (dtype) rows by state_out_idx, or NULL: the
+ *             last state_len inputs of cat(history, x) per sequence
+ *   cu_seqlens int32 [n_seqs+1] or NULL for n_seqs x T tokens
+ * Requires width <= state_len + 1, state_len <= 8, C % 8 == 0.
+ */
+int causal_conv1d_fwd(const void *x, int64_t x_stride_t, const void *w, const void *bias,
+                      void *y, int64_t y_stride_t,
+                      const void *state_in, const int64_t *state_in_idx,
+                      void *state_out, const int64_t *state_out_idx,
+                      const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
+                      int32_t C, int32_t width, int32_t state_len,
+                      int silu, int dtype, void *stream);
+
+/*
+ * Causal depthwise conv, decode / verify step (T new tokens per sequence,
+ * window updated in place).
+ *
+ * Replaces causal-conv1d's causal_conv1d_update as HF's GDN decode calls it
+ * (transformers modeling_qwen3_5_moe.py:452-461, :200-217), on the
+ * reference's slot pool [slots, C, state_len] (engine/runtime/kv_cache.py:
+ * 142-146) addressed by slot index instead of gathered.
+ *
+ *   x [n_seqs*T, C] (token stride x_stride_t), y likewise (y_stride_t)
+ *   conv_state [*, C, state_len], rows by state_idx (NULL: row n); updated
+ *   in place.  Negative slot ids: zero window, nothing written.
+ */
+int causal_conv1d_update(const void *x, int64_t x_stride_t, void *conv_state,
+                         const int64_t *state_idx, const void *w, const void *bias,
+                         void *y, int64_t y_stride_t, int32_t n_seqs, int32_t T,
+                         int32_t C, int32_t width, int32_t state_len,
+                         int silu, int dtype, void *stream);
+
+/*
+ * Speculative-verify commit: pool[slot_ids[b]] = snapshots[b, accepted_len[b]-1].
+ * accepted_len[b] <= 0 or slot_ids[b] < 0 leaves the slot untouched.
+ *
+ * No reference implementation exists; engine/runtime/spec_decode.py:81-87
+ * and :99-103 document the missing GDN rollback this provides.
+ *   pool fp32 [*, H, K, V];  snapshots fp32 [n_seqs, T, H, K, V]
+ *   slot_ids int64 [n_seqs];  accepted_len int32 [n_seqs]
+ */
+int gdn_state_commit(float *pool, const int64_t *slot_ids, const float *snapshots,
+                     const int32_t *accepted_len, int32_t n_seqs, int32_t T,
+                     int32_t H, int32_t K, int32_t V, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_CAPI_H */

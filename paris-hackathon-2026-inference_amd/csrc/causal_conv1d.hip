@@ -1,0 +1,338 @@
+// Causal depthwise conv1d (+ optional SiLU) feeding the GDN q/k/v split.
+//
+// Prefill: each thread owns 8 consecutive channels and walks a tile of
+// tokens of the packed token-major stream, keeping the previous 3 inputs of
+// its channels in registers; a sequence start (from cu_seqlens) reloads the
+// window from the cached history (or zeros).  A second small kernel writes
+// the final windows.  A token row of x is read by
+// one coalesced 16-byte load per thread, so the kernel is one read of x and
+// one write of y (HBM roofline), plus the small state rows.
+// Update: one thread per (sequence, channel) shifts the cached window by
+// the T new tokens in place.
+//
+// Semantics: transformers modeling_qwen3_5_moe.py:200-240 (causal_conv1d_fn
+// and causal_conv1d_update) and cache_utils.py:1032-1068 (cached window).
+#include "gdn_common.h"
+
+namespace gdn {
+namespace {
+
+constexpr int CPT = 8;         // channels per thread
+constexpr int CONV_NT = 256;   // threads per workgroup
+constexpr int TILE_T = 32;     // tokens per workgroup tile
+
+template <typename T> struct Vec8;
+template <> struct Vec8<uint16_t> {
+  static __device__ __forceinline__ void load(const uint16_t *p, float *o) {
+    const uint4 u = *reinterpret_cast<const uint4 *>(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = bf16_bits_to_f32(w[i] & 0xffffu);
+      o[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
+    }
+  }
+  static __device__ __forceinline__ void store(uint16_t *p, const float *x) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = static_cast<uint32_t>(f32_to_bf16_bits(x[2 * i])) |
+             (static_cast<uint32_t>(f32_to_bf16_bits(x[2 * i + 1])) << 16);
+    *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+template <> struct Vec8<float> {
+  static __device__ __forceinline__ void load(const float *p, float *o) {
+    const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  }
+  static __device__ __forceinline__ void store(float *p, const float *x) {
+    reinterpret_cast<float4 *>(p)[0] = make_float4(x[0], x[1], x[2], x[3]);
+    reinterpret_cast<float4 *>(p)[1] = make_float4(x[4], x[5], x[6], x[7]);
+  }
+};
+
+template <typename T> __device__ __forceinline__ float ld1(const T *p);
+template <> __device__ __forceinline__ float ld1<uint16_t>(const uint16_t *p) { return bf16_bits_to_f32(*p); }
+template <> __device__ __forceinline__ float ld1<float>(const float *p) { return *p; }
+template <typename T> __device__ __forceinline__ void st1(T *p, float x);
+template <> __device__ __forceinline__ void st1<uint16_t>(uint16_t *p, float x) { *p = f32_to_bf16_bits(x); }
+template <> __device__ __forceinline__ void st1<float>(float *p, float x) { *p = x; }
+
+__device__ __forceinline__ float silu(float x) { return x / (1.f + expf(-x)); }
+
+struct ConvArgs {
+  const void *x;
+  int64_t xs;
+  const void *w, *bias;
+  void *y;
+  int64_t ys;
+  const void *st_in;
+  const int64_t *in_idx;
+  void *st_out;
+  const int64_t *out_idx;
+  const int32_t *cu;
+  int n_seqs, T, C, width, silu;
+  int64_t total;
+};
+
+constexpr int WIN = 3;  // previous inputs kept in registers (width <= 4)
+
+// History row (SL inputs, oldest first) -> value `d` tokens before the
+// sequence start (d >= 1), or 0 when there is no history.
+template <typename T, int SL>
+__device__ __forceinline__ float history_at(const ConvArgs &a, int64_t row, int c, int d) {
+  if (row < 0 || d > SL) return 0.f;
+  return ld1<T>(static_cast<const T *>(a.st_in) + (row * a.C + c) * SL + (SL - d));
+}
+
+__device__ __forceinline__ int64_t in_row_of(const ConvArgs &a, int n) {
+  return a.st_in ? (a.in_idx ? a.in_idx[n] : n) : -1;
+}
+
+template <typename T, int SL>
+__global__ __launch_bounds__(CONV_NT) void conv_fwd_kernel(ConvArgs a) {
+  const int c0 = (blockIdx.x * CONV_NT + threadIdx.x) * CPT;
+  if (c0 >= a.C) return;
+  const int64_t tbeg = static_cast<int64_t>(blockIdx.y) * TILE_T;
+  if (tbeg >= a.total) return;
+  const int64_t tend = min(tbeg + TILE_T, a.total);
+
+  // sequence containing tbeg: last n with start(n) <= tbeg < end(n)
+  int n;
+  int64_t s_beg, s_end;
+  if (a.cu) {
+    int lo = 0, hi = a.n_seqs;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (a.cu[mid] <= tbeg) lo = mid; else hi = mid;
+    }
+    n = lo;
+    s_beg = a.cu[n];
+    s_end = a.cu[n + 1];
+  } else {
+    n = static_cast<int>(tbeg / a.T);
+    s_beg = static_cast<int64_t>(n) * a.T;
+    s_end = s_beg + a.T;
+  }
+  if (tbeg >= s_end) return;  // tokens past cu_seqlens[n_seqs]
+
+  float wt[4][CPT];
+  {
+    const T *wp = static_cast<const T *>(a.w);
+#pragma unroll
+    for (int i = 0; i < CPT; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wt[j][i] = j < a.width ? ld1<T>(wp + (int64_t)(c0 + i) * a.width + j) : 0.f;
+  }
+  float bias[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) bias[i] = a.bias ? ld1<T>(static_cast<const T *>(a.bias) + c0 + i) : 0.f;
+
+  // win[j] = input at t - WIN + j (oldest first) for the current token t
+  float win[WIN][CPT];
+  {
+    const int64_t hrow = in_row_of(a, n);
+#pragma unroll
+    for (int j = 0; j < WIN; ++j) {
+      const int64_t tt = tbeg - WIN + j;
+      if (tt >= s_beg) {
+        Vec8<T>::load(static_cast<const T *>(a.x) + tt * a.xs + c0, win[j]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) win[j][i] = history_at<T, SL>(a, hrow, c0 + i, static_cast<int>(s_beg - tt));
+      }
+    }
+  }
+
+  for (int64_t t = tbeg; t < tend; ++t) {
+    if (t == s_end) {  // the next sequence starts inside this tile
+      ++n;
+      if (a.cu) {
+        while (n < a.n_seqs && a.cu[n + 1] <= t) ++n;  // skip empty sequences
+        if (n >= a.n_seqs) break;
+        s_beg = a.cu[n];
+        s_end = a.cu[n + 1];
+      } else {
+        s_beg = t;
+        s_end = t + a.T;
+      }
+      const int64_t hrow = in_row_of(a, n);
+#pragma unroll
+      for (int j = 0; j < WIN; ++j)
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) win[j][i] = history_at<T, SL>(a, hrow, c0 + i, WIN - j);
+    }
+    float xv[CPT];
+    Vec8<T>::load(static_cast<const T *>(a.x) + t * a.xs + c0, xv);
+    float out[CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      float acc = bias[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (j < a.width) {
+          const int back = a.width - 1 - j;  // tap j reads x_{t - back}
+          acc += wt[j][i] * (back == 0 ? xv[i] : win[WIN - back][i]);
+        }
+      }
+      out[i] = a.silu ? silu(acc) : acc;
+    }
+    Vec8<T>::store(static_cast<T *>(a.y) + t * a.ys + c0, out);
+
+#pragma unroll
+    for (int j = 0; j < WIN - 1; ++j)
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) win[j][i] = win[j + 1][i];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) win[WIN - 1][i] = xv[i];
+  }
+}
+
+// Final windows: the last SL inputs of cat(history, x) per sequence.  Run
+// after the conv kernel (stream order) so that a pool updated in place is
+// never overwritten while a tile still reads its history; each thread reads
+// all SL values of its (sequence, channel) before writing any.
+template <typename T, int SL>
+__global__ __launch_bounds__(CONV_NT) void conv_final_state_kernel(ConvArgs a) {
+  const int c = blockIdx.x * CONV_NT + threadIdx.x;
+  const int n = blockIdx.y;
+  if (c >= a.C) return;
+  const int64_t row = a.out_idx ? a.out_idx[n] : n;
+  if (row < 0) return;
+  int64_t s_beg, s_end;
+  if (a.cu) {
+    s_beg = a.cu[n];
+    s_end = a.cu[n + 1];
+  } else {
+    s_beg = static_cast<int64_t>(n) * a.T;
+    s_end = s_beg + a.T;
+  }
+  const int64_t hrow = in_row_of(a, n);
+  float vals[SL];
+#pragma unroll
+  for (int j = 0; j < SL; ++j) {
+    const int64_t pos = s_end - SL + j;
+    vals[j] = pos >= s_beg ? ld1<T>(static_cast<const T *>(a.x) + pos * a.xs + c)
+                           : history_at<T, SL>(a, hrow, c, static_cast<int>(s_beg - pos));
+  }
+  T *st = static_cast<T *>(a.st_out) + (row * a.C + c) * SL;
+#pragma unroll
+  for (int j = 0; j < SL; ++j) st1<T>(st + j, vals[j]);
+}
+
+struct UpdArgs {
+  const void *x;
+  int64_t xs;
+  void *st;
+  const int64_t *idx;
+  const void *w, *bias;
+  void *y;
+  int64_t ys;
+  int n_seqs, T, C, width, silu;
+};
+
+template <typename T, int SL>
+__global__ __launch_bounds__(CONV_NT) void conv_update_kernel(UpdArgs a) {
+  const int c = blockIdx.x * CONV_NT + threadIdx.x;
+  const int n = blockIdx.y;
+  if (c >= a.C) return;
+  const int64_t row = a.idx ? a.idx[n] : n;
+  T *st = row >= 0 ? static_cast<T *>(a.st) + (row * a.C + c) * SL : nullptr;
+  float full[SL + 1];  // cached window (oldest first) followed by the new input
+#pragma unroll
+  for (int j = 0; j < SL; ++j) full[j] = st ? ld1<T>(st + j) : 0.f;
+  float wt[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) wt[j] = j < a.width ? ld1<T>(static_cast<const T *>(a.w) + (int64_t)c * a.width + j) : 0.f;
+  const float b = a.bias ? ld1<T>(static_cast<const T *>(a.bias) + c) : 0.f;
+  for (int t = 0; t < a.T; ++t) {
+    const int64_t tok = static_cast<int64_t>(n) * a.T + t;
+    full[SL] = ld1<T>(static_cast<const T *>(a.x) + tok * a.xs + c);
+    float acc = b;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (j < a.width) acc += wt[j] * full[SL + 1 - a.width + j];
+    st1<T>(static_cast<T *>(a.y) + tok * a.ys + c, a.silu ? silu(acc) : acc);
+#pragma unroll
+    for (int j = 0; j < SL; ++j) full[j] = full[j + 1];
+  }
+  if (st) {
+#pragma unroll
+    for (int j = 0; j < SL; ++j) st1<T>(st + j, full[j]);
+  }
+}
+
+template <typename T, int SL>
+int launch_fwd(const ConvArgs &a, hipStream_t s) {
+  const unsigned gx = (a.C / CPT + CONV_NT - 1) / CONV_NT;
+  const unsigned gy = static_cast<unsigned>((a.total + TILE_T - 1) / TILE_T);
+  if (gy > 0) hipLaunchKernelGGL((conv_fwd_kernel<T, SL>), dim3(gx, gy), dim3(CONV_NT), 0, s, a);
+  if (a.st_out)
+    hipLaunchKernelGGL((conv_final_state_kernel<T, SL>), dim3((a.C + CONV_NT - 1) / CONV_NT, a.n_seqs),
+                       dim3(CONV_NT), 0, s, a);
+  return check_launch("causal_conv1d_fwd");
+}
+
+template <typename T, int SL>
+int launch_upd(const UpdArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL((conv_update_kernel<T, SL>), dim3((a.C + CONV_NT - 1) / CONV_NT, a.n_seqs),
+                     dim3(CONV_NT), 0, s, a);
+  return check_launch("causal_conv1d_update");
+}
+
+}  // namespace
+}  // namespace gdn
+
+extern "C" int causal_conv1d_fwd(const void *x, int64_t x_stride_t, const void *w, const void *bias,
+                                 void *y, int64_t y_stride_t,
+                                 const void *state_in, const int64_t *state_in_idx,
+                                 void *state_out, const int64_t *state_out_idx,
+                                 const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
+                                 int32_t C, int32_t width, int32_t state_len,
+                                 int silu, int dtype, void *stream) {
+  using namespace gdn;
+  if (dtype != GDN_DTYPE_BF16 && dtype != GDN_DTYPE_F32)
+    return fail(GDN_ERR_UNSUPPORTED, "causal_conv1d_fwd: dtype must be bf16 or fp32");
+  if (width < 1 || width > 4 || (state_len != 3 && state_len != 4))
+    return fail(GDN_ERR_UNSUPPORTED, "causal_conv1d_fwd: width=%d state_len=%d (need width<=4, state_len in {3,4})",
+                width, state_len);
+  if (C <= 0 || C % CPT || n_seqs < 0 || T < 0 || n_seqs > 65535)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "causal_conv1d_fwd: bad sizes C=%d n_seqs=%d T=%d", C, n_seqs, T);
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) % 16)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "causal_conv1d_fwd: x and y must be 16-byte aligned");
+  if (!x || !w || !y) return fail(GDN_ERR_INVALID_ARGUMENT, "causal_conv1d_fwd: null x/w/y");
+  if (x_stride_t < C || y_stride_t < C || (x_stride_t % CPT) || (y_stride_t % CPT))
+    return fail(GDN_ERR_INVALID_ARGUMENT, "causal_conv1d_fwd: token strides must be >= C and multiples of 8");
+  if (n_seqs == 0) return ok();
+  ConvArgs a{x, x_stride_t, w, bias, y, y_stride_t, state_in, state_in_idx, state_out, state_out_idx,
+             cu_seqlens, n_seqs, T, C, width, silu};
+  a.total = cu_seqlens ? static_cast<int64_t>(T) : static_cast<int64_t>(n_seqs) * T;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == GDN_DTYPE_BF16)
+    return state_len == 4 ? launch_fwd<uint16_t, 4>(a, s) : launch_fwd<uint16_t, 3>(a, s);
+  return state_len == 4 ? launch_fwd<float, 4>(a, s) : launch_fwd<float, 3>(a, s);
+}
+
+extern "C" int causal_conv1d_update(const void *x, int64_t x_stride_t, void *conv_state,
+                                    const int64_t *state_idx, const void *w, const void *bias,
+                                    void *y, int64_t y_stride_t, int32_t n_seqs, int32_t T,
+                                    int32_t C, int32_t width, int32_t state_len,
+                                    int silu, int dtype, void *stream) {
+  using namespace gdn;
+  if (dtype != GDN_DTYPE_BF16 && dtype != GDN_DTYPE_F32)
+    return fail(GDN_ERR_UNSUPPORTED, "causal_conv1d_update: dtype must be bf16 or fp32");
+  if (width < 1 || width > 4 || (state_len != 3 && state_len != 4) || width > state_len + 1)
+    return fail(GDN_ERR_UNSUPPORTED, "causal_conv1d_update: width=%d state_len=%d (need width<=min(4,state_len+1))",
+                width, state_len);
+  if (C <= 0 || n_seqs < 0 || T < 0 || x_stride_t < C || y_stride_t < C)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "causal_conv1d_update: bad sizes");
+  if (!x || !w || !y || !conv_state) return fail(GDN_ERR_INVALID_ARGUMENT, "causal_conv1d_update: null pointer");
+  if (n_seqs == 0) return ok();
+  if (n_seqs > 65535) return fail(GDN_ERR_INVALID_ARGUMENT, "causal_conv1d_update: n_seqs > 65535");
+  UpdArgs a{x, x_stride_t, conv_state, state_idx, w, bias, y, y_stride_t, n_seqs, T, C, width, silu};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == GDN_DTYPE_BF16)
+    return state_len == 4 ? launch_upd<uint16_t, 4>(a, s) : launch_upd<uint16_t, 3>(a, s);
+  return state_len == 4 ? launch_upd<float, 4>(a, s) : launch_upd<float, 3>(a, s);
+}

@@ -1,0 +1,72 @@
+// Shared device helpers and host-side error plumbing for libgdn_mi355x.
+// gfx950 (CDNA4) only: wave64, bf16 MFMA, 160 KiB LDS per CU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "gdn_capi.h"
+
+namespace gdn {
+
+// ---------------------------------------------------------------- host side
+
+// Records a formatted message for gdn_last_error_string() and returns `code`.
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clears the thread's message; returns GDN_OK.
+int ok();
+// Maps a launch error (hipGetLastError after a launch) to a status.
+int check_launch(const char *what);
+
+inline bool valid_dtype(int dt) { return dt == GDN_DTYPE_F32 || dt == GDN_DTYPE_BF16 || dt == GDN_DTYPE_F16; }
+inline size_t dtype_size(int dt) { return dt == GDN_DTYPE_F32 ? 4 : 2; }
+
+// ---------------------------------------------------------------- device side
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits (inputs here are finite).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float load_elem(const void *p, int64_t i, int dt) {
+  if (dt == GDN_DTYPE_F32) return static_cast<const float *>(p)[i];
+  if (dt == GDN_DTYPE_BF16) return bf16_bits_to_f32(static_cast<const uint16_t *>(p)[i]);
+  return static_cast<float>(static_cast<const _Float16 *>(p)[i]);
+}
+
+__device__ __forceinline__ void store_elem(void *p, int64_t i, int dt, float x) {
+  if (dt == GDN_DTYPE_F32) {
+    static_cast<float *>(p)[i] = x;
+  } else if (dt == GDN_DTYPE_BF16) {
+    static_cast<uint16_t *>(p)[i] = f32_to_bf16_bits(x);
+  } else {
+    static_cast<_Float16 *>(p)[i] = static_cast<_Float16>(x);
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+  return x;
+}
+
+// Sequence n's token range: [*t0, *t0 + *len).
+__device__ __forceinline__ void seq_range(const int32_t *cu_seqlens, int n, int T, int64_t *t0, int *len) {
+  if (cu_seqlens) {
+    int a = cu_seqlens[n], b = cu_seqlens[n + 1];
+    *t0 = a;
+    *len = b - a;
+  } else {
+    *t0 = static_cast<int64_t>(n) * T;
+    *len = T;
+  }
+}
+
+}  // namespace gdn

@@ -1,0 +1,223 @@
+// Token recurrence of the gated delta rule (decode / spec-verify / small-T).
+//
+// One workgroup owns a [128 x VT] column slice of one (sequence, v-head)
+// state and keeps it in registers for all of the sequence's tokens: the
+// state is read from HBM once and written once, so decode is a pure stream
+// of the fp32 state (the HBM roofline).  Thread mapping (NT = 2*VT threads):
+//   columns: 4 per thread (float4), TPR = VT/4 threads span the slice;
+//   rows:    8 row groups, thread row group rg owns rows rg + 8r, r < 16.
+// Per token the two K-reductions k~^T S and q~^T S are done together: in
+// registers over 16 rows, xor-shuffles across the row groups of a wave, and
+// LDS across waves when VT > 32.  The output uses
+//   o = q~^T (e^g S + k~ d^T) = e^g (q~^T S) + (q~ . k~) d,
+// so no second reduction is needed after the rank-1 update.
+//
+// Semantics: transformers modeling_qwen3_5_moe.py:331-381 (the torch
+// recurrence the reference imports at engine/runtime/cuda_graphs.py:126-135).
+#include "gdn_common.h"
+
+namespace gdn {
+namespace {
+
+constexpr int KD = 128;  // head dim of k (rows of the state)
+constexpr int VD = 128;  // head dim of v (columns of the state)
+
+struct RecArgs {
+  const void *q, *k, *v;
+  int64_t qs, ks, vs;  // token strides (elements)
+  const float *g;
+  const void *beta;
+  const float *state_in;
+  const int64_t *in_idx;
+  float *state_out;
+  const int64_t *out_idx;
+  void *o;
+  float *snap;
+  const int32_t *cu;
+  int n_seqs, T, Hk, Hv;
+  float scale;
+  int l2norm;
+  int qkv_dt, beta_dt, o_dt;
+};
+
+template <int VT>
+__global__ __launch_bounds__(2 * VT) void recurrent_kernel(RecArgs a) {
+  constexpr int NT = 2 * VT;
+  constexpr int NW = NT / 64;
+  constexpr int TPR = VT / 4;   // threads per state row
+  constexpr int RPT = 16;       // rows per thread (8 row groups)
+  constexpr int NSPLIT = VD / VT;
+
+  __shared__ float qs_l[KD];
+  __shared__ float ks_l[KD];
+  __shared__ float red[NW > 1 ? NW : 1][2][VT];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int c4 = tid % TPR;
+  const int rg = tid / TPR;
+
+  int bid = blockIdx.x;
+  const int vt = bid % NSPLIT;
+  bid /= NSPLIT;
+  const int h = bid % a.Hv;
+  const int n = bid / a.Hv;
+  const int hk = h / (a.Hv / a.Hk);
+  const int col0 = vt * VT + c4 * 4;
+
+  int64_t t0;
+  int len;
+  seq_range(a.cu, n, a.T, &t0, &len);
+
+  const int64_t in_row = a.state_in ? (a.in_idx ? a.in_idx[n] : n) : -1;
+  const int64_t out_row = a.state_out ? (a.out_idx ? a.out_idx[n] : n) : -1;
+
+  float4 s[RPT];
+  if (in_row >= 0) {
+    const float *base = a.state_in + (in_row * a.Hv + h) * (int64_t)(KD * VD) + col0;
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) s[r] = *reinterpret_cast<const float4 *>(base + (rg + 8 * r) * VD);
+  } else {
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) s[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+
+  for (int t = 0; t < len; ++t) {
+    const int64_t tok = t0 + t;
+    // ---- q/k prologue: every wave reduces the full 128-vectors itself
+    const int64_t qoff = tok * a.qs + (int64_t)hk * KD + 2 * lane;
+    const int64_t koff = tok * a.ks + (int64_t)hk * KD + 2 * lane;
+    float q0 = load_elem(a.q, qoff, a.qkv_dt), q1 = load_elem(a.q, qoff + 1, a.qkv_dt);
+    float k0 = load_elem(a.k, koff, a.qkv_dt), k1 = load_elem(a.k, koff + 1, a.qkv_dt);
+    const float sqq = wave_sum(q0 * q0 + q1 * q1);
+    const float skk = wave_sum(k0 * k0 + k1 * k1);
+    const float sqk = wave_sum(q0 * k0 + q1 * k1);
+    const float rq = a.l2norm ? rsqrtf(sqq + 1e-6f) : 1.f;
+    const float rk = a.l2norm ? rsqrtf(skk + 1e-6f) : 1.f;
+    const float qsc = rq * a.scale;
+    if (wave == 0) {
+      qs_l[2 * lane] = q0 * qsc;
+      qs_l[2 * lane + 1] = q1 * qsc;
+      ks_l[2 * lane] = k0 * rk;
+      ks_l[2 * lane + 1] = k1 * rk;
+    }
+    const float qk = sqk * qsc * rk;
+    const float eg = expf(a.g[tok * a.Hv + h]);
+    const float bt = load_elem(a.beta, tok * a.Hv + h, a.beta_dt);
+    float vv[4];
+    const int64_t voff = tok * a.vs + (int64_t)h * VD + col0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) vv[c] = load_elem(a.v, voff + c, a.qkv_dt);
+    __syncthreads();
+
+    // ---- partial k~^T S and q~^T S over this thread's rows
+    float pk[4] = {0.f, 0.f, 0.f, 0.f}, pq[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+      const float kk = ks_l[rg + 8 * r], qq = qs_l[rg + 8 * r];
+      pk[0] += kk * s[r].x; pk[1] += kk * s[r].y; pk[2] += kk * s[r].z; pk[3] += kk * s[r].w;
+      pq[0] += qq * s[r].x; pq[1] += qq * s[r].y; pq[2] += qq * s[r].z; pq[3] += qq * s[r].w;
+    }
+#pragma unroll
+    for (int m = TPR; m < 64; m <<= 1) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        pk[c] += __shfl_xor(pk[c], m, 64);
+        pq[c] += __shfl_xor(pq[c], m, 64);
+      }
+    }
+    if constexpr (NW > 1) {
+      if (lane < TPR) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          red[wave][0][c4 * 4 + c] = pk[c];
+          red[wave][1][c4 * 4 + c] = pq[c];
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float sk = 0.f, sq = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          sk += red[w][0][c4 * 4 + c];
+          sq += red[w][1][c4 * 4 + c];
+        }
+        pk[c] = sk;
+        pq[c] = sq;
+      }
+    }
+
+    // ---- delta, rank-1 update, output
+    float d[4], out[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      d[c] = bt * (vv[c] - eg * pk[c]);
+      out[c] = eg * pq[c] + qk * d[c];
+    }
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+      const float kk = ks_l[rg + 8 * r];
+      s[r].x = eg * s[r].x + kk * d[0];
+      s[r].y = eg * s[r].y + kk * d[1];
+      s[r].z = eg * s[r].z + kk * d[2];
+      s[r].w = eg * s[r].w + kk * d[3];
+    }
+    if (rg == 0) {
+      const int64_t ooff = (tok * a.Hv + h) * (int64_t)VD + col0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) store_elem(a.o, ooff + c, a.o_dt, out[c]);
+    }
+    if (a.snap) {
+      float *sb = a.snap + (((int64_t)n * a.T + t) * a.Hv + h) * (int64_t)(KD * VD) + col0;
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) *reinterpret_cast<float4 *>(sb + (rg + 8 * r) * VD) = s[r];
+    }
+    __syncthreads();
+  }
+
+  if (out_row >= 0) {
+    float *base = a.state_out + (out_row * a.Hv + h) * (int64_t)(KD * VD) + col0;
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) *reinterpret_cast<float4 *>(base + (rg + 8 * r) * VD) = s[r];
+  }
+}
+
+}  // namespace
+}  // namespace gdn
+
+extern "C" int gdn_recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
+                                 int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
+                                 const float *g, const void *beta, int beta_dtype,
+                                 const float *state_in, const int64_t *state_in_idx,
+                                 float *state_out, const int64_t *state_out_idx,
+                                 void *o, int o_dtype, float *snapshots,
+                                 const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
+                                 int32_t Hk, int32_t Hv, int32_t K, int32_t V,
+                                 float scale, int l2norm_qk, void *stream) {
+  using namespace gdn;
+  if (K != KD || V != VD)
+    return fail(GDN_ERR_UNSUPPORTED, "gdn_recurrent_fwd: K=%d V=%d; only K=V=128 is built", K, V);
+  if (n_seqs < 0 || T < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_recurrent_fwd: bad sizes n_seqs=%d T=%d Hk=%d Hv=%d",
+                n_seqs, T, Hk, Hv);
+  if (!valid_dtype(qkv_dtype) || !valid_dtype(beta_dtype) || !valid_dtype(o_dtype))
+    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_recurrent_fwd: bad dtype");
+  if (n_seqs == 0) return ok();
+  if (!q || !k || !v || !g || !beta || !o)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_recurrent_fwd: null q/k/v/g/beta/o");
+  if (snapshots && cu_seqlens)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_recurrent_fwd: snapshots need equal-length sequences");
+  if (q_stride_t < Hk * K || k_stride_t < Hk * K || v_stride_t < Hv * V)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_recurrent_fwd: token stride smaller than a row");
+  const int64_t n_blocks = static_cast<int64_t>(n_seqs) * Hv * (VD / 32);
+  if (n_blocks > 0x7fffffff) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_recurrent_fwd: grid too large");
+
+  RecArgs a{q, k, v, q_stride_t, k_stride_t, v_stride_t, g, beta, state_in, state_in_idx,
+            state_out, state_out_idx, o, snapshots, cu_seqlens, n_seqs, T, Hk, Hv,
+            scale, l2norm_qk, qkv_dtype, beta_dtype, o_dtype};
+  hipLaunchKernelGGL(recurrent_kernel<32>, dim3(static_cast<unsigned>(n_blocks)), dim3(64), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch("gdn_recurrent_fwd");
+}

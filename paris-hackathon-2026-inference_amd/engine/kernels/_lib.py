@@ -1,0 +1,166 @@
+"""ctypes binding of libgdn_mi355x.so and the tensor plumbing around it.
+
+The library is loaded after ``torch`` so that its HIP runtime dependency
+(``libamdhip64.so.7``) resolves to the copy torch already mapped: one HIP
+runtime per process, and torch's streams and allocations are valid handles
+inside the library.  There is no fallback: if the library is missing the
+first call raises, naming the build command.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import torch
+
+LIB_NAME = "libgdn_mi355x.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+ABI_VERSION = 1
+
+GDN_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+_c_void_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_f32 = ctypes.c_float
+_size = ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/gdn_capi.h
+SIGNATURES = {
+    "gdn_abi_version": (_int, []),
+    "gdn_last_error_string": (ctypes.c_char_p, []),
+    "gdn_recurrent_fwd": (_int, [
+        _c_void_p, _c_void_p, _c_void_p, _int,      # q k v qkv_dtype
+        _i64, _i64, _i64,                           # token strides
+        _c_void_p, _c_void_p, _int,                 # g beta beta_dtype
+        _c_void_p, _c_void_p,                       # state_in, state_in_idx
+        _c_void_p, _c_void_p,                       # state_out, state_out_idx
+        _c_void_p, _int, _c_void_p,                 # o, o_dtype, snapshots
+        _c_void_p, _i32, _i32,                      # cu_seqlens n_seqs T
+        _i32, _i32, _i32, _i32,                     # Hk Hv K V
+        _f32, _int, _c_void_p]),                    # scale l2norm stream
+    "gdn_chunk_fwd": (_int, [
+        _c_void_p, _c_void_p, _c_void_p, _int,
+        _i64, _i64, _i64,
+        _c_void_p, _c_void_p, _int,
+        _c_void_p, _c_void_p,                       # h0, h0_idx
+        _c_void_p, _c_void_p,                       # hT, hT_idx
+        _c_void_p, _int,                            # o, o_dtype
+        _c_void_p, _i32, _i32,
+        _i32, _i32, _i32, _i32,
+        _f32, _int,
+        _c_void_p, _size, _c_void_p]),              # workspace, bytes, stream
+    "gdn_chunk_workspace_bytes": (_size, [_i32, _i64, _i32, _i32, _i32]),
+    "causal_conv1d_fwd": (_int, [
+        _c_void_p, _i64, _c_void_p, _c_void_p,      # x x_stride w bias
+        _c_void_p, _i64,                            # y y_stride
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, # state_in idx state_out idx
+        _c_void_p, _i32, _i32,                      # cu n_seqs T
+        _i32, _i32, _i32,                           # C width state_len
+        _int, _int, _c_void_p]),                    # silu dtype stream
+    "causal_conv1d_update": (_int, [
+        _c_void_p, _i64, _c_void_p, _c_void_p,      # x x_stride conv_state idx
+        _c_void_p, _c_void_p, _c_void_p, _i64,      # w bias y y_stride
+        _i32, _i32, _i32, _i32, _i32,               # n_seqs T C width state_len
+        _int, _int, _c_void_p]),
+    "gdn_state_commit": (_int, [
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+        _i32, _i32, _i32, _i32, _i32, _c_void_p]),
+}
+
+_LIB: Optional[ctypes.CDLL] = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load (once) and type the shared library; raises if it is missing or stale."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"{LIB_NAME} not found at {path}; build it with "
+            "`python paris-hackathon-2026-inference_amd/build_lib.py` (hipcc, gfx950)")
+    lib = ctypes.CDLL(path, mode=ctypes.RTLD_LOCAL)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    ver = lib.gdn_abi_version()
+    if ver != ABI_VERSION:
+        raise RuntimeError(f"{LIB_NAME} ABI {ver} != expected {ABI_VERSION}; rebuild it")
+    _LIB = lib
+    return lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = load().gdn_last_error_string().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (status {status}): {msg}")
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def require_gpu(*tensors: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError(f"expected a GPU tensor, got one on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    if dev is None:
+        raise ValueError("no tensor given")
+    return dev
+
+
+def dtype_code(t: torch.Tensor, what: str) -> int:
+    try:
+        return GDN_DTYPE[t.dtype]
+    except KeyError:
+        raise TypeError(f"{what}: unsupported dtype {t.dtype}") from None
+
+
+def token_major(x: torch.Tensor, what: str) -> tuple[torch.Tensor, int]:
+    """View [B, T, H, D] as a token-major stream; returns (tensor, token stride).
+
+    Heads and dims must be packed (stride(3) == 1, stride(2) == D) and the
+    batch stride must equal T * token stride; otherwise a contiguous copy is
+    made.
+    """
+    if x.dim() != 4:
+        raise ValueError(f"{what}: expected [B, T, H, D], got shape {tuple(x.shape)}")
+    b, t, h, d = x.shape
+    st = x.stride(1) if t > 1 else h * d
+    ok = (x.stride(3) == 1 and (h == 1 or x.stride(2) == d) and st >= h * d and st % 8 == 0
+          and (b == 1 or x.stride(0) == t * st) and x.storage_offset() % 8 == 0)
+    if not ok:
+        x = x.contiguous()
+        st = h * d
+    return x, st
+
+
+def as_index(idx: Optional[torch.Tensor], device: torch.device) -> Optional[torch.Tensor]:
+    if idx is None:
+        return None
+    if idx.device != device or idx.dtype != torch.int64 or not idx.is_contiguous():
+        idx = idx.to(device=device, dtype=torch.int64).contiguous()
+    return idx
+
+
+def as_cu_seqlens(cu: Optional[torch.Tensor], device: torch.device) -> Optional[torch.Tensor]:
+    if cu is None:
+        return None
+    if cu.device != device or cu.dtype != torch.int32 or not cu.is_contiguous():
+        cu = cu.to(device=device, dtype=torch.int32).contiguous()
+    return cu

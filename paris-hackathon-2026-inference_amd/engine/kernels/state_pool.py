@@ -1,0 +1,70 @@
+"""Slot-indexed GDN state pools and the speculative-verify commit.
+
+The reference keeps one GDN layer's state as two slot pools
+(``_LinearAttentionSlotLayer``, engine/runtime/kv_cache.py:134-212):
+recurrent ``[slots, Hv, K, V]`` fp32 and conv ``[slots, conv_dim, 4]`` bf16,
+gathered with ``index_select(...).clone()`` before each forward and
+scattered back with ``index_copy_`` after it (:189-208).  Here the kernels
+address the pools by slot id, so :class:`LinearAttentionSlotPool` only owns
+the tensors; decode, prefill and the spec-verify commit update them in place.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+
+def gdn_state_commit(pool: torch.Tensor, slot_ids: torch.Tensor, snapshots: torch.Tensor,
+                     accepted_len: torch.Tensor) -> torch.Tensor:
+    """``pool[slot_ids[b]] = snapshots[b, accepted_len[b] - 1]`` on the GPU, in place.
+
+    ``accepted_len[b] <= 0`` or a negative slot leaves that slot untouched;
+    values above T are clamped to T.  There is no reference implementation:
+    engine/runtime/spec_decode.py:81-87 and :99-103 document the missing
+    GDN rollback ("requires saving state snapshots").
+    """
+    dev = _lib.require_gpu(pool, snapshots)
+    if pool.dtype != torch.float32 or snapshots.dtype != torch.float32:
+        raise TypeError("pool and snapshots must be fp32")
+    if not pool.is_contiguous() or not snapshots.is_contiguous():
+        raise ValueError("pool and snapshots must be contiguous")
+    n, t, h, k, v = snapshots.shape
+    if pool.shape[1:] != (h, k, v):
+        raise ValueError(f"pool {tuple(pool.shape)} does not match snapshots {tuple(snapshots.shape)}")
+    idx = _lib.as_index(slot_ids, dev)
+    acc = accepted_len.to(device=dev, dtype=torch.int32).contiguous()
+    if idx.numel() != n or acc.numel() != n:
+        raise ValueError("slot_ids and accepted_len need one entry per sequence")
+    st = _lib.load().gdn_state_commit(_lib.ptr(pool), _lib.ptr(idx), _lib.ptr(snapshots), _lib.ptr(acc),
+                                      n, t, h, k, v, _lib.stream_of(pool))
+    _lib.check(st, "gdn_state_commit")
+    return pool
+
+
+class LinearAttentionSlotPool:
+    """One GDN layer's pooled state, addressed by slot id (no gather/scatter).
+
+    Mirrors the reference's ``_LinearAttentionSlotLayer`` pools and
+    ``reset_slot`` (kv_cache.py:160-212) with the same shapes and dtypes.
+    """
+
+    def __init__(self, num_slots: int, conv_dim: int = 8192, conv_kernel: int = 4,
+                 num_v_heads: int = 32, head_k_dim: int = 128, head_v_dim: int = 128,
+                 device: Optional[torch.device] = None, conv_dtype: torch.dtype = torch.bfloat16):
+        device = device or torch.device("cuda")
+        self.num_slots = num_slots
+        self.conv_states = torch.zeros(num_slots, conv_dim, conv_kernel, dtype=conv_dtype, device=device)
+        self.recurrent_states = torch.zeros(num_slots, num_v_heads, head_k_dim, head_v_dim,
+                                            dtype=torch.float32, device=device)
+
+    def reset_slot(self, slot_id: int) -> None:
+        self.conv_states[slot_id].zero_()
+        self.recurrent_states[slot_id].zero_()
+
+    def commit_spec(self, slot_ids: torch.Tensor, snapshots: torch.Tensor,
+                    accepted_len: torch.Tensor) -> None:
+        """Keep the recurrent state after each sequence's last accepted draft token."""
+        gdn_state_commit(self.recurrent_states, slot_ids, snapshots, accepted_len)

@@ -1,0 +1,136 @@
+"""GPU parity of the causal depthwise conv (prefill fn and decode update)
+with the CPU oracle and with HF's golden vectors, through the C ABI.
+
+fp32 cases are checked to 1e-5; bf16 outputs to the north star's 2e-2 abs
+(bf16 rounding of O(1) values is ~4e-3).  Window/state tensors are copies
+of inputs, so they are checked bit-exactly."""
+import numpy as np
+import pytest
+import torch
+
+from engine import configs
+from engine.kernels import causal_conv1d_fn, causal_conv1d_update
+from oracle import conv
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not torch.cuda.is_available(), reason="needs an MI355X")]
+
+DEV = "cuda"
+
+
+def np64(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fn_matches_hf_golden(golden, dtype):
+    x = torch.from_numpy(golden["conv_fn.x"]).to(DEV, dtype)
+    w = torch.from_numpy(golden["conv_fn.w"]).to(DEV, dtype)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    y = causal_conv1d_fn(x, w, None, activation="silu")
+    assert y.shape == x.shape and y.dtype == dtype
+    assert np.abs(np64(y) - golden["conv_fn.y"]).max() < tol
+    xs = torch.from_numpy(golden["conv_fn_short.x"]).to(DEV, dtype)
+    ys = causal_conv1d_fn(xs, w, None, activation="silu")
+    assert np.abs(np64(ys) - golden["conv_fn_short.y"]).max() < tol
+
+
+def test_update_matches_hf_golden(golden):
+    x = torch.from_numpy(golden["conv_upd.x"]).to(DEV)
+    st = torch.from_numpy(golden["conv_upd.state"]).to(DEV)
+    w = torch.from_numpy(golden["conv_upd.w"]).to(DEV)
+    y = causal_conv1d_update(x, st, w, None, "silu")
+    assert np.abs(np64(y) - golden["conv_upd.y"]).max() < 1e-5
+    assert np.array_equal(st.cpu().numpy(), golden["conv_upd.state_after"])
+
+
+def test_config3_varlen_conv_with_history_and_pool():
+    c = configs.config3()
+    cu = c["cu_seqlens"]
+    n = cu.numel() - 1
+    gen = torch.Generator().manual_seed(33)
+    hist = torch.randn(n, configs.CONV_DIM, 4, generator=gen).to(torch.bfloat16)
+    num_slots = 24
+    slots = torch.randperm(num_slots, generator=gen)[:n]
+    pool0 = torch.randn(num_slots, configs.CONV_DIM, 4, generator=gen).to(torch.bfloat16)
+    pool0[slots] = hist
+    x = c["x"]
+    y_ref, fin_ref = conv.causal_conv1d_varlen(x.float().numpy(), c["conv_w"].float().numpy(), cu.numpy(),
+                                               activation="silu", initial_states=hist.float().numpy(),
+                                               dtype=np.float32)
+    pool = pool0.to(DEV)
+    y = causal_conv1d_fn(x.to(DEV), c["conv_w"].to(DEV), None, activation="silu", cu_seqlens=cu.to(DEV),
+                         conv_states=pool, cache_indices=slots.to(DEV))
+    assert y.shape == x.shape
+    err = np.abs(np64(y) - y_ref)
+    assert err.max() < 2e-2 and err.mean() < 2e-3
+    assert np.array_equal(np64(pool[slots.to(DEV)]), fin_ref)
+    keep = torch.ones(num_slots, dtype=torch.bool)
+    keep[slots] = False
+    assert torch.equal(pool[keep.to(DEV)].cpu(), pool0[keep])
+
+
+def test_varlen_short_and_empty_sequences_fp32():
+    lens = [2, 0, 37, 1, 64, 3]
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32)
+    gen = torch.Generator().manual_seed(2)
+    x = torch.randn(int(cu[-1]), 64, generator=gen)
+    w = torch.randn(64, 4, generator=gen)
+    hist = torch.randn(len(lens), 64, 4, generator=gen)
+    y_ref, fin_ref = conv.causal_conv1d_varlen(x.numpy(), w.numpy(), cu.numpy(), activation="silu",
+                                               initial_states=hist.numpy())
+    y, fin = causal_conv1d_fn(x.to(DEV), w.to(DEV), activation="silu", cu_seqlens=cu.to(DEV),
+                              initial_states=hist.to(DEV), return_final_states=True)
+    assert np.abs(np64(y) - y_ref).max() < 1e-5
+    assert np.array_equal(np64(fin), fin_ref.astype(np.float32).astype(np.float64))
+
+
+def test_has_initial_state_false_starts_from_zeros():
+    gen = torch.Generator().manual_seed(4)
+    x = torch.randn(2, 16, 5, generator=gen).to(torch.bfloat16)
+    w = torch.randn(16, 4, generator=gen).to(torch.bfloat16)
+    pool = torch.randn(2, 16, 4, generator=gen).to(torch.bfloat16).to(DEV)
+    pool_before = pool.clone()
+    y = causal_conv1d_fn(x.to(DEV), w.to(DEV), activation="silu", conv_states=pool,
+                         has_initial_state=torch.tensor([False, True], device=DEV))
+    y0, f0 = conv.causal_conv1d_fn(x[:1].float().numpy(), w.float().numpy())
+    y1, f1 = conv.causal_conv1d_fn(x[1:].float().numpy(), w.float().numpy(),
+                                   initial_state=pool_before[1:].float().cpu().numpy())
+    assert np.abs(np64(y[:1]) - y0).max() < 2e-2 and np.abs(np64(y[1:]) - y1).max() < 2e-2
+    assert np.array_equal(np64(pool[0]), f0[0]) and np.array_equal(np64(pool[1]), f1[0])
+
+
+@pytest.mark.parametrize("t", [1, 2, 4])
+def test_update_pool_indices_and_negative_slot(t):
+    gen = torch.Generator().manual_seed(10 + t)
+    b, c = 4, configs.CONV_DIM
+    x = torch.randn(b, c, t, generator=gen).to(torch.bfloat16)
+    w = torch.randn(c, 4, generator=gen).to(torch.bfloat16)
+    pool0 = torch.randn(6, c, 4, generator=gen).to(torch.bfloat16)
+    idx = torch.tensor([4, -1, 0, 2])
+    states = torch.zeros(b, c, 4)
+    states[[0, 2, 3]] = pool0[[4, 0, 2]].float()
+    y_ref, st_ref = conv.causal_conv1d_update(x.float().numpy(), states.numpy(), w.float().numpy(),
+                                              activation="silu")
+    pool = pool0.to(DEV)
+    y = causal_conv1d_update(x.to(DEV), pool, w.to(DEV), None, "silu", conv_state_indices=idx.to(DEV))
+    assert np.abs(np64(y) - y_ref).max() < 2e-2
+    assert np.array_equal(np64(pool[[4, 0, 2]]), st_ref[[0, 2, 3]])
+    assert torch.equal(pool[[1, 3, 5]].cpu(), pool0[[1, 3, 5]])
+
+
+def test_prefill_then_decode_continuation():
+    """fn over a prompt (pool window written) then update steps == fn over the whole stream."""
+    gen = torch.Generator().manual_seed(6)
+    c, t = 256, 45
+    x = torch.randn(1, c, t + 3, generator=gen)
+    w = torch.randn(c, 4, generator=gen)
+    y_full = causal_conv1d_fn(x.to(DEV), w.to(DEV), activation="silu")
+    pool = torch.zeros(3, c, 4, device=DEV)
+    slot = torch.tensor([1], device=DEV)
+    y_pre = causal_conv1d_fn(x[:, :, :t].to(DEV), w.to(DEV), activation="silu", conv_states=pool,
+                             cache_indices=slot)
+    outs = [causal_conv1d_update(x[:, :, t + i:t + i + 1].to(DEV), pool, w.to(DEV), None, "silu",
+                                 conv_state_indices=slot) for i in range(3)]
+    y_cat = torch.cat([y_pre] + outs, dim=-1)
+    assert torch.allclose(y_cat, y_full, atol=1e-5)
