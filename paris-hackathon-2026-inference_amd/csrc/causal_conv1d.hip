@@ -108,14 +108,15 @@ __global__ __launch_bounds__(CONV_NT) void conv_fwd_kernel(ConvArgs a) {
       if (a.cu[mid] <= tbeg) lo = mid; else hi = mid;
     }
     n = lo;
-    s_beg = a.cu[n];
-    s_end = a.cu[n + 1];
   } else {
     n = static_cast<int>(tbeg / a.T);
-    s_beg = static_cast<int64_t>(n) * a.T;
-    s_end = s_beg + a.T;
   }
-  if (tbeg >= s_end) return;  // tokens past cu_seqlens[n_seqs]
+  {
+    int len;
+    seq_range(a.cu, n, a.T, a.total, &s_beg, &len);
+    s_end = s_beg + len;
+  }
+  if (tbeg < s_beg || tbeg >= s_end) return;  // tokens outside every sequence
 
   float wt[4][CPT];
   {
@@ -151,12 +152,13 @@ __global__ __launch_bounds__(CONV_NT) void conv_fwd_kernel(ConvArgs a) {
       if (a.cu) {
         while (n < a.n_seqs && a.cu[n + 1] <= t) ++n;  // skip empty sequences
         if (n >= a.n_seqs) break;
-        s_beg = a.cu[n];
-        s_end = a.cu[n + 1];
-      } else {
-        s_beg = t;
-        s_end = t + a.T;
       }
+      {
+        int len;
+        seq_range(a.cu, n, a.T, a.total, &s_beg, &len);
+        s_end = s_beg + len;
+      }
+      if (t < s_beg || t >= s_end) break;
       const int64_t hrow = in_row_of(a, n);
 #pragma unroll
       for (int j = 0; j < WIN; ++j)
@@ -200,14 +202,10 @@ __global__ __launch_bounds__(CONV_NT) void conv_final_state_kernel(ConvArgs a) {
   if (c >= a.C) return;
   const int64_t row = a.out_idx ? a.out_idx[n] : n;
   if (row < 0) return;
-  int64_t s_beg, s_end;
-  if (a.cu) {
-    s_beg = a.cu[n];
-    s_end = a.cu[n + 1];
-  } else {
-    s_beg = static_cast<int64_t>(n) * a.T;
-    s_end = s_beg + a.T;
-  }
+  int64_t s_beg;
+  int len;
+  seq_range(a.cu, n, a.T, a.total, &s_beg, &len);
+  const int64_t s_end = s_beg + len;
   const int64_t hrow = in_row_of(a, n);
   float vals[SL];
 #pragma unroll

@@ -57,16 +57,23 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-// Sequence n's token range: [*t0, *t0 + *len).
-__device__ __forceinline__ void seq_range(const int32_t *cu_seqlens, int n, int T, int64_t *t0, int *len) {
+// Sequence n's token range [*t0, *t0 + *len), clamped to the [0, total)
+// tokens the caller passed, so that a malformed device-side cu_seqlens can
+// never move an access outside the tensors.
+__device__ __forceinline__ void seq_range(const int32_t *cu_seqlens, int n, int T, int64_t total,
+                                          int64_t *t0, int *len) {
+  int64_t a, b;
   if (cu_seqlens) {
-    int a = cu_seqlens[n], b = cu_seqlens[n + 1];
-    *t0 = a;
-    *len = b - a;
+    a = cu_seqlens[n];
+    b = cu_seqlens[n + 1];
   } else {
-    *t0 = static_cast<int64_t>(n) * T;
-    *len = T;
+    a = static_cast<int64_t>(n) * T;
+    b = a + T;
   }
+  a = a < 0 ? 0 : (a > total ? total : a);
+  b = b < a ? a : (b > total ? total : b);
+  *t0 = a;
+  *len = static_cast<int>(b - a);
 }
 
 }  // namespace gdn

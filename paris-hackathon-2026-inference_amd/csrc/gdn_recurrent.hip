@@ -19,6 +19,8 @@
 namespace gdn {
 namespace {
 
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+
 constexpr int KD = 128;  // head dim of k (rows of the state)
 constexpr int VD = 128;  // head dim of v (columns of the state)
 
@@ -35,6 +37,7 @@ struct RecArgs {
   float *snap;
   const int32_t *cu;
   int n_seqs, T, Hk, Hv;
+  int64_t total;
   float scale;
   int l2norm;
   int qkv_dt, beta_dt, o_dt;
@@ -68,19 +71,22 @@ __global__ __launch_bounds__(2 * VT) void recurrent_kernel(RecArgs a) {
 
   int64_t t0;
   int len;
-  seq_range(a.cu, n, a.T, &t0, &len);
+  seq_range(a.cu, n, a.T, a.total, &t0, &len);
 
   const int64_t in_row = a.state_in ? (a.in_idx ? a.in_idx[n] : n) : -1;
   const int64_t out_row = a.state_out ? (a.out_idx ? a.out_idx[n] : n) : -1;
 
-  float4 s[RPT];
+  // The state is touched exactly once per launch: non-temporal loads and
+  // stores keep it from displacing reusable lines in the caches.
+  f32x4 s[RPT];
   if (in_row >= 0) {
     const float *base = a.state_in + (in_row * a.Hv + h) * (int64_t)(KD * VD) + col0;
 #pragma unroll
-    for (int r = 0; r < RPT; ++r) s[r] = *reinterpret_cast<const float4 *>(base + (rg + 8 * r) * VD);
+    for (int r = 0; r < RPT; ++r)
+      s[r] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(base + (rg + 8 * r) * VD));
   } else {
 #pragma unroll
-    for (int r = 0; r < RPT; ++r) s[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int r = 0; r < RPT; ++r) s[r] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
   for (int t = 0; t < len; ++t) {
@@ -172,7 +178,8 @@ __global__ __launch_bounds__(2 * VT) void recurrent_kernel(RecArgs a) {
     if (a.snap) {
       float *sb = a.snap + (((int64_t)n * a.T + t) * a.Hv + h) * (int64_t)(KD * VD) + col0;
 #pragma unroll
-      for (int r = 0; r < RPT; ++r) *reinterpret_cast<float4 *>(sb + (rg + 8 * r) * VD) = s[r];
+      for (int r = 0; r < RPT; ++r)
+        __builtin_nontemporal_store(s[r], reinterpret_cast<f32x4 *>(sb + (rg + 8 * r) * VD));
     }
     __syncthreads();
   }
@@ -180,7 +187,8 @@ __global__ __launch_bounds__(2 * VT) void recurrent_kernel(RecArgs a) {
   if (out_row >= 0) {
     float *base = a.state_out + (out_row * a.Hv + h) * (int64_t)(KD * VD) + col0;
 #pragma unroll
-    for (int r = 0; r < RPT; ++r) *reinterpret_cast<float4 *>(base + (rg + 8 * r) * VD) = s[r];
+    for (int r = 0; r < RPT; ++r)
+      __builtin_nontemporal_store(s[r], reinterpret_cast<f32x4 *>(base + (rg + 8 * r) * VD));
   }
 }
 
@@ -216,6 +224,7 @@ extern "C" int gdn_recurrent_fwd(const void *q, const void *k, const void *v, in
 
   RecArgs a{q, k, v, q_stride_t, k_stride_t, v_stride_t, g, beta, state_in, state_in_idx,
             state_out, state_out_idx, o, snapshots, cu_seqlens, n_seqs, T, Hk, Hv,
+            cu_seqlens ? static_cast<int64_t>(T) : static_cast<int64_t>(n_seqs) * T,
             scale, l2norm_qk, qkv_dtype, beta_dtype, o_dtype};
   hipLaunchKernelGGL(recurrent_kernel<32>, dim3(static_cast<unsigned>(n_blocks)), dim3(64), 0,
                      static_cast<hipStream_t>(stream), a);

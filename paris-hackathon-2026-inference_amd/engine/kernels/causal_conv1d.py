@@ -86,7 +86,7 @@ def causal_conv1d_fn(
     w = weight.to(dt).contiguous()
     bb = None if bias is None else bias.to(dt).contiguous()
     xt, xs, b, t, was_bct = _stream_view(x)
-    c = xt.shape[1]
+    c = xt.shape[-1]
     if w.dim() != 2 or w.shape[0] != c:
         raise ValueError(f"weight must be [C={c}, W], got {tuple(weight.shape)}")
     cu = _lib.as_cu_seqlens(cu_seqlens, dev)
