@@ -6,27 +6,33 @@
 //   U = T (beta V),  W = T (beta e^gamma K~)
 //   V' = U - W S ;  O = (e^gamma Q~) S + lower(Q~K~^T * Gamma) V'
 //   S <- e^{gamma_63} S + (e^{gamma_63 - gamma} K~)^T V'
-// is split into three launches:
-//   chunk_table_kernel  chunk -> (sequence, first token) table (cu_seqlens aware)
+// runs as three launches:
+//   chunk_table_kernel  chunk -> sequence table (cu_seqlens aware)
 //   chunk_prep_kernel   one workgroup per (chunk, v-head), all in parallel:
 //                       K K^T and Q K^T on MFMA from the raw bf16 rows (exact
-//                       products; the l2norm and gate factors are applied to
-//                       the fp32 results), T by blocked forward substitution
-//                       in fp32 (LDS), then W = T' K and U = T'' V on MFMA with
-//                       T', T'' split into bf16 hi + lo parts.
-//   chunk_scan_kernel   one wave per (sequence, v-head, 16 state columns), serial
-//                       over the chunks: the state slice lives in MFMA
-//                       accumulators for the whole sequence.
+//                       products; l2norm and gate factors scale the fp32
+//                       results), T by blocked substitution in fp32 (LDS),
+//                       W = T' K and U = T'' V on MFMA with T', T'' split into
+//                       bf16 hi + lo parts.  Every operand the scan needs is
+//                       written pre-swizzled: one 1 KiB block per (MFMA, wave),
+//                       lane l's 16 bytes at offset 16 l.
+//   chunk_scan_kernel   one wave per (sequence, v-head, 16 state columns),
+//                       serial over the chunks; the state slice lives in MFMA
+//                       accumulators for the whole sequence.  The next chunk's
+//                       operand blocks stream into a second LDS buffer with
+//                       buffer_load ... lds while the current chunk computes.
 // Precision (checked against an fp64 restatement at T=4096): the state is fed
-// to MFMA as bf16, U stays fp32 (it initialises the V' accumulator) and the
-// state increment K^T V'' uses V'' split into bf16 hi + lo.
+// to MFMA as bf16, U stays fp32 (it initialises the V' accumulator), the state
+// increment K^T V'' uses V'' split into bf16 hi + lo.
 //
 // MFMA: v_mfma_f32_16x16x32_bf16.  Lane l holds A[l%16][8(l/16)+j] and
-// B[8(l/16)+j][l%16] (j<8) and D[4(l/16)+i][l%16] (i<4).  When an
+// B[8(l/16)+j][l%16] (j<8), and D[4(l/16)+i][l%16] (i<4).  When an
 // accumulator tile pair (rows 0-15, 16-31 of a 32-long reduction) is reused
 // as the B operand of the next product, lane group g = l/16 holds reduction
-// indices {4g..4g+3, 16+4g..16+4g+3}; the matching A operand reads the same
-// index set ("pi" order) with two 8-byte loads.  No LDS round trip.
+// indices {4g..4g+3, 16+4g..16+4g+3} ("pi" order); the scan's A-operand
+// blocks are stored in the same order, so no accumulator goes through LDS.
+#include <type_traits>
+
 #include "gdn_common.h"
 
 namespace gdn {
@@ -37,34 +43,42 @@ typedef __attribute__((ext_vector_type(4))) float f32x4;
 typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
 typedef __attribute__((ext_vector_type(2))) unsigned u32x2;
 
-constexpr int CK = 64;    // chunk length
-constexpr int DK = 128;   // k head dim
-constexpr int DV = 128;   // v head dim
-constexpr int SCAL = 132; // per (chunk, head) scalars: sq[64], sk[64], eL, pad
+constexpr int CK = 64;     // chunk length
+constexpr int DK = 128;    // k head dim
+constexpr int DV = 128;    // v head dim
+constexpr int SCAL = 256;  // per (chunk, v-head) scalars: sq[64], sk[64], eL (1 KiB block)
+
+// Operand blocks (64 lanes x 16 bytes) per chunk, in two contiguous regions
+// so that one chunk's scan operands are two straight copies:
+//   per (chunk, v-head): -W [p 0..3][s 0..3], A [p 0..3][s 0..1] (6 used), scalars
+//   per (chunk, k-head): Q [p 0..3][s 0..3], K^T [i 0..7][s 0..1]
+constexpr int NB_W = 16;
+constexpr int NB_A = 8;
+constexpr int NB_SC = SCAL / 64;  // scalars as blocks (1)
+constexpr int NB_Q = 16;
+constexpr int NB_KT = 16;
+constexpr int VH_W = 0, VH_A = VH_W + NB_W, VH_SC = VH_A + NB_A, NB_VH = VH_SC + NB_SC;
+constexpr int KH_Q = 0, KH_KT = KH_Q + NB_Q, NB_KH = KH_KT + NB_KT;
 
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
-
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 u) { return __builtin_bit_cast(bf16x8, u); }
-
-// 8 consecutive bf16 at p (16-byte aligned)
+__device__ __forceinline__ int64_t uniform64(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(x) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+__device__ __forceinline__ uint16_t bf16_rne(float x) {  // hardware round-to-nearest-even
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
+}
 __device__ __forceinline__ bf16x8 ld8(const uint16_t *p) {
   return as_bf16x8(*reinterpret_cast<const u32x4 *>(p));
-}
-// pi-order operand: p[0..3] and p[16..19] (each 8-byte aligned)
-__device__ __forceinline__ bf16x8 ld_pi(const uint16_t *p) {
-  const u32x2 a = *reinterpret_cast<const u32x2 *>(p);
-  const u32x2 b = *reinterpret_cast<const u32x2 *>(p + 16);
-  u32x4 u = {a.x, a.y, b.x, b.y};
-  return as_bf16x8(u);
 }
 __device__ __forceinline__ bf16x8 zero8() {
   u32x4 u = {0u, 0u, 0u, 0u};
   return as_bf16x8(u);
 }
-
-// two accumulator tiles -> one pi-order B operand (bf16 hi part)
 __device__ __forceinline__ bf16x8 pack_hi(f32x4 a, f32x4 b) {
   bf16x8 r;
 #pragma unroll
@@ -106,11 +120,9 @@ struct ChunkArgs {
   int max_chunks;
   // workspace
   int32_t *chunk_start;  // [n_seqs + 1]
-  uint16_t *W;           // [NC][Hv][64][128]   -W, bf16
-  float *Ut;             // [NC][Hv][128][64]   U transposed, fp32
-  uint16_t *A;           // [NC][Hv][64][64]    lower(Q~K~^T Gamma), bf16
-  uint16_t *Kt;          // [NC][Hk][128][64]   raw K transposed, bf16
-  float *scal;           // [NC][Hv][SCAL]
+  u32x4 *vh;             // [NC][Hv][NB_VH][64]   -W, A, scalars
+  u32x4 *kh;             // [NC][Hk][NB_KH][64]   Q, K^T
+  float *Ut;             // [NC][Hv][128][64]     U transposed, fp32
 };
 
 __device__ __forceinline__ void seq_bounds(const ChunkArgs &a, int n, int64_t *s0, int *len) {
@@ -127,11 +139,9 @@ __global__ __launch_bounds__(256) void chunk_table_kernel(ChunkArgs a) {
     int64_t s0;
     int len = 0;
     if (n < a.n_seqs) seq_bounds(a, n, &s0, &len);
-    const int32_t nc = (len + CK - 1) / CK;
-    part[threadIdx.x] = nc;
+    part[threadIdx.x] = (len + CK - 1) / CK;
     __syncthreads();
-    // inclusive scan (Hillis-Steele) over 256 entries
-    for (int off = 1; off < 256; off <<= 1) {
+    for (int off = 1; off < 256; off <<= 1) {  // inclusive scan
       const int32_t x = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
       __syncthreads();
       part[threadIdx.x] += x;
@@ -144,23 +154,27 @@ __global__ __launch_bounds__(256) void chunk_table_kernel(ChunkArgs a) {
 }
 
 // ------------------------------------------------------------------ phase A
-constexpr int KT_LD = CK + 8;   // LDS row stride (bf16) of the transposed K / V tiles
-constexpr int TF_LD = CK + 4;   // LDS row stride (fp32) of L / T
+constexpr int LT_LD = CK + 4;    // fp32 row stride of L / T (16-byte aligned rows)
+constexpr int WS_LD = DK + 8;    // bf16 row stride of the -W staging tile (same bytes as L / T)
+static_assert(CK * LT_LD * 4 == CK * WS_LD * 2, "W staging reuses the L/T buffer");
+
+// Transposed [128][64] bf16 tiles (K^T, V^T): 16-byte segment seg of row r is
+// stored at segment seg ^ (r & 7) to spread LDS banks.
+__device__ __forceinline__ int tsw(int row, int col) {
+  return row * CK + ((((col >> 3) ^ row) & 7) << 3) + (col & 7);
+}
 
 __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
-  __shared__ __align__(16) uint16_t kt_s[DK * KT_LD];
-  __shared__ __align__(16) uint16_t vt_s[DV * KT_LD];
-  __shared__ __align__(16) float lf[CK * TF_LD];   // L (strict lower)
-  __shared__ __align__(16) float tf[CK * TF_LD];   // T = (I + L)^-1
-  __shared__ __align__(16) float xs[3][16][17];    // block products
+  __shared__ __align__(16) uint16_t kt_s[DK * CK];
+  __shared__ __align__(16) uint16_t vt_s[DV * CK];
+  __shared__ __align__(16) float lt[CK * LT_LD];   // L, then T in place, then -W staging
+  __shared__ __align__(16) float xs[3][16][17];
   __shared__ float gam_s[CK], beta_s[CK], nk_s[CK], nq_s[CK];
 
   const int h = blockIdx.x;
   const int j = blockIdx.y;
-  const int total_chunks = a.chunk_start[a.n_seqs];
-  if (j >= total_chunks) return;
-  // sequence owning chunk j: last n with chunk_start[n] <= j
-  int lo = 0, hi = a.n_seqs;
+  if (j >= a.chunk_start[a.n_seqs]) return;
+  int lo = 0, hi = a.n_seqs;  // sequence owning chunk j: last n with chunk_start[n] <= j
   while (hi - lo > 1) {
     const int mid = (lo + hi) >> 1;
     if (a.chunk_start[mid] <= j) lo = mid; else hi = mid;
@@ -173,247 +187,493 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
   const int64_t t0 = s0 + static_cast<int64_t>(c) * CK;
   const int len = min(CK, slen - c * CK);
   if (len <= 0) return;
-  const int hk = h / (a.Hv / a.Hk);
+  const int ratio = a.Hv / a.Hk;
+  const int hk = h / ratio;
+  const bool khead_writer = (h % ratio) == 0;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int g4 = lane >> 4;   // lane group
+  const int g4 = lane >> 4;
   const int r16 = lane & 15;
+  const size_t ch = static_cast<size_t>(j) * a.Hv + h;
+  const size_t chk = static_cast<size_t>(j) * a.Hk + hk;
 
-  // ---- A.1: K^T and V^T tiles into LDS, row norms, gates
-  for (int i = tid; i < CK * TF_LD; i += 256) tf[i] = 0.f;
+  // ---- issue every global load up front
+  const int seg = tid & 15;
+  u32x4 ku[4], qu[4], vu[4];
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int row = (tid >> 4) + 16 * it;
+    const int64_t tok = t0 + row;
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    ku[it] = row < len ? *reinterpret_cast<const u32x4 *>(a.k + tok * a.ks + (int64_t)hk * DK + seg * 8) : z;
+    qu[it] = row < len ? *reinterpret_cast<const u32x4 *>(a.q + tok * a.qs + (int64_t)hk * DK + seg * 8) : z;
+    vu[it] = row < len ? *reinterpret_cast<const u32x4 *>(a.v + tok * a.vs + (int64_t)h * DV + seg * 8) : z;
+  }
+  // MFMA operands of K K^T / Q K^T for row block p = wave
+  const int p = wave;
+  bf16x8 ak[4], aq[4], bk[4][4];
   {
-    const int seg = tid & 15;         // 8-element column segment
+    const int row = 16 * p + r16;
+    const uint16_t *krow = a.k + (t0 + row) * a.ks + (int64_t)hk * DK + 8 * g4;
+    const uint16_t *qrow = a.q + (t0 + row) * a.qs + (int64_t)hk * DK + 8 * g4;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      ak[s] = row < len ? ld8(krow + 32 * s) : zero8();
+      aq[s] = row < len ? ld8(qrow + 32 * s) : zero8();
+    }
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+      const int col = 16 * cb + r16;
+      const uint16_t *kcol = a.k + (t0 + col) * a.ks + (int64_t)hk * DK + 8 * g4;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) bk[cb][s] = (cb <= p && col < len) ? ld8(kcol + 32 * s) : zero8();
+    }
+  }
+  float gv = 0.f, bv = 0.f;
+  if (wave == 0 && lane < len) {
+    gv = a.g[(t0 + lane) * a.Hv + h];
+    bv = load_elem(a.beta, (t0 + lane) * a.Hv + h, a.beta_dt);
+  }
+
+  // ---- A.1: K^T, V^T into LDS; row norms; chunk-local cumsum of g
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int row = (tid >> 4) + 16 * it;
+    float sk = 0.f, sq = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t kw = ku[it][e], qw = qu[it][e], vw = vu[it][e];
+      const float k0 = bf16_bits_to_f32(kw & 0xffffu), k1 = bf16_bits_to_f32(kw >> 16);
+      const float q0 = bf16_bits_to_f32(qw & 0xffffu), q1 = bf16_bits_to_f32(qw >> 16);
+      sk += k0 * k0 + k1 * k1;
+      sq += q0 * q0 + q1 * q1;
+      const int d0 = seg * 8 + 2 * e;
+      kt_s[tsw(d0, row)] = static_cast<uint16_t>(kw & 0xffffu);
+      kt_s[tsw(d0 + 1, row)] = static_cast<uint16_t>(kw >> 16);
+      vt_s[tsw(d0, row)] = static_cast<uint16_t>(vw & 0xffffu);
+      vt_s[tsw(d0 + 1, row)] = static_cast<uint16_t>(vw >> 16);
+    }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+      sk += __shfl_xor(sk, m, 64);
+      sq += __shfl_xor(sq, m, 64);
+    }
+    if (seg == 0) {
+      nk_s[row] = a.l2norm ? rsqrtf(sk + 1e-6f) : 1.f;
+      nq_s[row] = (a.l2norm ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
+    }
+  }
+  if (wave == 0) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float x = __shfl_up(gv, off, 64);
+      if (lane >= off) gv += x;
+    }
+    gam_s[lane] = gv;
+    beta_s[lane] = bv;
+  }
+  // Q operand blocks for the scan (pi order), straight from the loaded rows
+  if (khead_writer) {
+    u32x4 *qop = a.kh + chk * (NB_KH * 64) + KH_Q * 64;
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       const int row = (tid >> 4) + 16 * it;
-      const bool live = row < len;
-      const int64_t tok = t0 + row;
-      u32x4 ku = {0u, 0u, 0u, 0u}, qu = ku, vu = ku;
-      if (live) {
-        ku = *reinterpret_cast<const u32x4 *>(a.k + tok * a.ks + (int64_t)hk * DK + seg * 8);
-        qu = *reinterpret_cast<const u32x4 *>(a.q + tok * a.qs + (int64_t)hk * DK + seg * 8);
-        vu = *reinterpret_cast<const u32x4 *>(a.v + tok * a.vs + (int64_t)h * DV + seg * 8);
-      }
-      float sk = 0.f, sq = 0.f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t kw = ku[e], qw = qu[e], vw = vu[e];
-        const float k0 = bf16_bits_to_f32(kw & 0xffffu), k1 = bf16_bits_to_f32(kw >> 16);
-        const float q0 = bf16_bits_to_f32(qw & 0xffffu), q1 = bf16_bits_to_f32(qw >> 16);
-        sk += k0 * k0 + k1 * k1;
-        sq += q0 * q0 + q1 * q1;
-        kt_s[(seg * 8 + 2 * e) * KT_LD + row] = static_cast<uint16_t>(kw & 0xffffu);
-        kt_s[(seg * 8 + 2 * e + 1) * KT_LD + row] = static_cast<uint16_t>(kw >> 16);
-        vt_s[(seg * 8 + 2 * e) * KT_LD + row] = static_cast<uint16_t>(vw & 0xffffu);
-        vt_s[(seg * 8 + 2 * e + 1) * KT_LD + row] = static_cast<uint16_t>(vw >> 16);
-      }
-#pragma unroll
-      for (int m = 1; m < 16; m <<= 1) {
-        sk += __shfl_xor(sk, m, 64);
-        sq += __shfl_xor(sq, m, 64);
-      }
-      if (seg == 0) {
-        nk_s[row] = a.l2norm ? rsqrtf(sk + 1e-6f) : 1.f;
-        nq_s[row] = (a.l2norm ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
-      }
-    }
-    if (wave == 0) {
-      const bool live = lane < len;
-      float gv = live ? a.g[(t0 + lane) * a.Hv + h] : 0.f;
-      const float bv = live ? load_elem(a.beta, (t0 + lane) * a.Hv + h, a.beta_dt) : 0.f;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float x = __shfl_up(gv, off, 64);
-        if (lane >= off) gv += x;
-      }
-      gam_s[lane] = gv;
-      beta_s[lane] = bv;
+      const int s = seg >> 2, m = seg & 3;       // columns 32 s + 8 m .. +8
+      const int blk = (row >> 4) * 4 + s;
+      const int half = m >> 1;                   // slots 0-3 or 4-7
+      const int gA = 2 * (m & 1);                // lane group of columns +0..3; +4..7 -> gA + 1
+      u32x2 *base = reinterpret_cast<u32x2 *>(qop + blk * 64);
+      base[2 * ((row & 15) + 16 * gA) + half] = u32x2{qu[it][0], qu[it][1]};
+      base[2 * ((row & 15) + 16 * (gA + 1)) + half] = u32x2{qu[it][2], qu[it][3]};
     }
   }
   __syncthreads();
 
-  // ---- A.2: K K^T and Q K^T (wave w owns row block p = w)
-  const size_t ch = static_cast<size_t>(j) * a.Hv + h;
+  // ---- A.2: K K^T -> L (fp32, LDS), Q K^T -> A (pi-order blocks, global)
   {
-    const int p = wave;
-    const int row = 16 * p + r16;
-    const bool live_r = row < len;
-    const uint16_t *krow = a.k + (t0 + row) * a.ks + (int64_t)hk * DK;
-    const uint16_t *qrow = a.q + (t0 + row) * a.qs + (int64_t)hk * DK;
-    uint16_t *Aout = a.A + ch * (CK * CK);
+    u32x4 *aop = a.vh + ch * (NB_VH * 64) + VH_A * 64;
     for (int cb = 0; cb < 4; ++cb) {
       f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = kk;
       if (cb <= p) {
-        const int col = 16 * cb + r16;
-        const bool live_c = col < len;
-        const uint16_t *kcol = a.k + (t0 + col) * a.ks + (int64_t)hk * DK;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          const int off = 32 * s + 8 * g4;
-          const bf16x8 ak = live_r ? ld8(krow + off) : zero8();
-          const bf16x8 aq = live_r ? ld8(qrow + off) : zero8();
-          const bf16x8 bk = live_c ? ld8(kcol + off) : zero8();
-          kk = mfma(ak, bk, kk);
-          qk = mfma(aq, bk, qk);
+          kk = mfma(ak[s], bk[cb][s], kk);
+          qk = mfma(aq[s], bk[cb][s], qk);
         }
       }
-      const int jj = 16 * cb + r16;  // column (key position) of this lane
+      const int jj = 16 * cb + r16;
+      const int sblk = cb >> 1;
+      const bool a_used = sblk <= (p >= 2 ? 1 : 0);
+      uint16_t *ablk = reinterpret_cast<uint16_t *>(aop + (p * 2 + sblk) * 64);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int ii = 16 * p + 4 * g4 + e;  // row (query position)
+        const int ii = 16 * p + 4 * g4 + e;
         float lval = 0.f, aval = 0.f;
         if (cb <= p && ii >= jj) {
           const float dec = expf(gam_s[ii] - gam_s[jj]);
           aval = nq_s[ii] * nk_s[jj] * qk[e] * dec;
           if (ii > jj) lval = beta_s[ii] * nk_s[ii] * nk_s[jj] * kk[e] * dec;
         }
-        lf[ii * TF_LD + jj] = lval;
-        Aout[ii * CK + jj] = f32_to_bf16_bits(aval);
+        lt[ii * LT_LD + jj] = lval;
+        if (a_used) {
+          // element (row ii, col jj) of block (p, sblk): lane (ii&15) + 16 g, slot
+          const int cc = jj - 32 * sblk;
+          const int lane_op = (ii & 15) + 16 * ((cc & 15) >> 2);
+          ablk[lane_op * 8 + (cc >> 4) * 4 + (cc & 3)] = f32_to_bf16_bits(aval);
+        }
       }
     }
   }
   __syncthreads();
 
-  // ---- A.3: T = (I + L)^-1, blocked (16x16 diagonal blocks by substitution)
-  if (tid < 64) {
-    const int b = tid >> 4, cc = tid & 15;
-    float x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = (i == cc) ? 1.f : 0.f;
-    const float *lb = lf + (16 * b) * TF_LD + 16 * b;
-#pragma unroll
-    for (int i = 1; i < 16; ++i) {
-      if (i > cc) {
-        float s = 0.f;
-#pragma unroll
-        for (int jx = 0; jx < i; ++jx) s += lb[i * TF_LD + jx] * x[jx];
-        x[i] = -s;
-      }
-    }
-    float *tb = tf + (16 * b) * TF_LD + 16 * b;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) tb[i * TF_LD + cc] = x[i];
-  }
-  __syncthreads();
-  for (int ab = 1; ab < 4; ++ab) {
-    // X_b = sum_{kb=b}^{ab-1} L[ab][kb] T[kb][b]   for b < ab
-    for (int e = tid; e < ab * 256; e += 256) {
-      const int b = e >> 8, r = (e >> 4) & 15, cc = e & 15;
-      float s = 0.f;
-      for (int kb = b; kb < ab; ++kb) {
-        const float *lrow = lf + (16 * ab + r) * TF_LD + 16 * kb;
-        const float *tcol = tf + (16 * kb) * TF_LD + 16 * b + cc;
-#pragma unroll
-        for (int qx = 0; qx < 16; ++qx) s += lrow[qx] * tcol[qx * TF_LD];
-      }
-      xs[b][r][cc] = s;
-    }
-    __syncthreads();
-    // T[ab][b] = -T[ab][ab] X_b
-    for (int e = tid; e < ab * 256; e += 256) {
-      const int b = e >> 8, r = (e >> 4) & 15, cc = e & 15;
-      const float *trow = tf + (16 * ab + r) * TF_LD + 16 * ab;
-      float s = 0.f;
-#pragma unroll
-      for (int qx = 0; qx < 16; ++qx) s += trow[qx] * xs[b][qx][cc];
-      tf[(16 * ab + r) * TF_LD + 16 * b + cc] = -s;
-    }
-    __syncthreads();
-  }
-
-  // ---- A.4: W = T diag(beta e^gamma nk) K,  U = T diag(beta) V  (hi + lo T)
+  // ---- A.3: T = (I + L)^-1 in place (16x16 diagonal blocks by substitution)
   {
-    const int p = wave;
+    float x[16];
+    const int b = tid >> 4, cc = tid & 15;
+    if (tid < 64) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[i] = (i == cc) ? 1.f : 0.f;
+      const float *lb = lt + (16 * b) * LT_LD + 16 * b;
+#pragma unroll
+      for (int i = 1; i < 16; ++i) {
+        if (i > cc) {
+          float sacc = 0.f;
+#pragma unroll
+          for (int jx = 0; jx < i; ++jx) sacc += lb[i * LT_LD + jx] * x[jx];
+          x[i] = -sacc;
+        }
+      }
+    }
+    __syncthreads();
+    if (tid < 64) {
+      float *tb = lt + (16 * b) * LT_LD + 16 * b;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) tb[i * LT_LD + cc] = x[i];
+    }
+    __syncthreads();
+  }
+  for (int ab = 1; ab < 4; ++ab) {
+    for (int e = tid; e < ab * 256; e += 256) {  // X_b = sum_{kb=b}^{ab-1} L[ab][kb] T[kb][b]
+      const int b = e >> 8, r = (e >> 4) & 15, cc = e & 15;
+      float sacc = 0.f;
+      for (int kb = b; kb < ab; ++kb) {
+        const float *lrow = lt + (16 * ab + r) * LT_LD + 16 * kb;
+        const float *tcol = lt + (16 * kb) * LT_LD + 16 * b + cc;
+#pragma unroll
+        for (int qx = 0; qx < 16; ++qx) sacc += lrow[qx] * tcol[qx * LT_LD];
+      }
+      xs[b][r][cc] = sacc;
+    }
+    __syncthreads();
+    for (int e = tid; e < ab * 256; e += 256) {  // T[ab][b] = -T[ab][ab] X_b
+      const int b = e >> 8, r = (e >> 4) & 15, cc = e & 15;
+      const float *trow = lt + (16 * ab + r) * LT_LD + 16 * ab;
+      float sacc = 0.f;
+#pragma unroll
+      for (int qx = 0; qx < 16; ++qx) sacc += trow[qx] * xs[b][qx][cc];
+      lt[(16 * ab + r) * LT_LD + 16 * b + cc] = -sacc;
+    }
+    __syncthreads();
+  }
+
+  // ---- A.4: W = T diag(beta e^gamma nk) K,  U = T diag(beta) V  (T split hi + lo)
+  f32x4 wacc[8];
+  {
     const int nsteps = p >= 2 ? 2 : 1;  // T is lower triangular
     bf16x8 wa_hi[2], wa_lo[2], ua_hi[2], ua_lo[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      if (s < nsteps) {
-        const float *trow = tf + (16 * p + r16) * TF_LD + 32 * s + 8 * g4;
+      const float *trow = lt + (16 * p + r16) * LT_LD + 32 * s + 8 * g4;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int col = 32 * s + 8 * g4 + e;
-          const float t = trow[e];
-          const float tb = t * beta_s[col];
-          const float tw = tb * expf(gam_s[col]) * nk_s[col];
-          const __bf16 hw = static_cast<__bf16>(tw), hu = static_cast<__bf16>(tb);
-          wa_hi[s][e] = hw;
-          wa_lo[s][e] = static_cast<__bf16>(tw - static_cast<float>(hw));
-          ua_hi[s][e] = hu;
-          ua_lo[s][e] = static_cast<__bf16>(tb - static_cast<float>(hu));
-        }
+      for (int e = 0; e < 8; ++e) {
+        const int col = 32 * s + 8 * g4 + e;
+        const float t = s < nsteps ? trow[e] : 0.f;
+        const float tb = t * beta_s[col];
+        const float tw = tb * expf(gam_s[col]) * nk_s[col];
+        const __bf16 hw = static_cast<__bf16>(tw), hu = static_cast<__bf16>(tb);
+        wa_hi[s][e] = hw;
+        wa_lo[s][e] = static_cast<__bf16>(tw - static_cast<float>(hw));
+        ua_hi[s][e] = hu;
+        ua_lo[s][e] = static_cast<__bf16>(tb - static_cast<float>(hu));
       }
     }
-    uint16_t *Wout = a.W + ch * (CK * DK);
     float *Uout = a.Ut + ch * (DV * CK);
-#pragma unroll 2
+#pragma unroll
     for (int nb = 0; nb < 8; ++nb) {
       f32x4 w = {0.f, 0.f, 0.f, 0.f}, u = w;
+      const int row = 16 * nb + r16;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         if (s < nsteps) {
-          const bf16x8 bk = ld8(kt_s + (16 * nb + r16) * KT_LD + 32 * s + 8 * g4);
-          const bf16x8 bv = ld8(vt_s + (16 * nb + r16) * KT_LD + 32 * s + 8 * g4);
-          w = mfma(wa_hi[s], bk, w);
-          w = mfma(wa_lo[s], bk, w);
-          u = mfma(ua_hi[s], bv, u);
-          u = mfma(ua_lo[s], bv, u);
+          const bf16x8 bk2 = ld8(kt_s + tsw(row, 32 * s + 8 * g4));
+          const bf16x8 bv2 = ld8(vt_s + tsw(row, 32 * s + 8 * g4));
+          w = mfma(wa_hi[s], bk2, w);
+          w = mfma(wa_lo[s], bk2, w);
+          u = mfma(ua_hi[s], bv2, u);
+          u = mfma(ua_lo[s], bv2, u);
         }
       }
-      // D layout: column 16nb + r16, rows 16p + 4g4 + e
-#pragma unroll
-      for (int e = 0; e < 4; ++e) Wout[(16 * p + 4 * g4 + e) * DK + 16 * nb + r16] = f32_to_bf16_bits(-w[e]);
-      *reinterpret_cast<f32x4 *>(Uout + (16 * nb + r16) * CK + 16 * p + 4 * g4) = u;
+      wacc[nb] = w;
+      *reinterpret_cast<f32x4 *>(Uout + row * CK + 16 * p + 4 * g4) = u;  // U^T[v][pos]
     }
   }
-
-  // ---- A.5: per-position scalars and the transposed raw K tile
-  if (tid < CK) {
-    float *sc = a.scal + ch * SCAL;
-    const float gl = gam_s[CK - 1];
-    sc[tid] = expf(gam_s[tid]) * nq_s[tid];
-    sc[CK + tid] = expf(gl - gam_s[tid]) * nk_s[tid];
-    if (tid == 0) sc[2 * CK] = expf(gl);
+  __syncthreads();  // T no longer read: reuse lt as the -W staging tile [64][WS_LD] bf16
+  {
+    uint16_t *ws = reinterpret_cast<uint16_t *>(lt);
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ws[(16 * p + 4 * g4 + e) * WS_LD + 16 * nb + r16] = f32_to_bf16_bits(-wacc[nb][e]);
   }
-  if (h % (a.Hv / a.Hk) == 0) {
-    uint16_t *kt_out = a.Kt + (static_cast<size_t>(j) * a.Hk + hk) * (DK * CK);
-    for (int e = tid; e < DK * CK / 8; e += 256) {
-      const int row = e >> 3, seg = e & 7;
-      *reinterpret_cast<u32x4 *>(kt_out + row * CK + seg * 8) =
-          *reinterpret_cast<const u32x4 *>(kt_s + row * KT_LD + seg * 8);
+  __syncthreads();
+
+  // ---- A.5: operand blocks (-W, K^T) and per-position scalars
+  {
+    const uint16_t *ws = reinterpret_cast<const uint16_t *>(lt);
+    u32x4 *wop = a.vh + ch * (NB_VH * 64) + VH_W * 64;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int e = tid + 256 * it;          // block e/64, lane e%64
+      const int blk = e >> 6, l = e & 63;
+      const int bp = blk >> 2, bs = blk & 3;
+      const uint16_t *src = ws + (16 * bp + (l & 15)) * WS_LD + 32 * bs + 4 * (l >> 4);
+      const u32x2 x0 = *reinterpret_cast<const u32x2 *>(src);
+      const u32x2 x1 = *reinterpret_cast<const u32x2 *>(src + 16);
+      wop[e] = u32x4{x0.x, x0.y, x1.x, x1.y};
+    }
+    if (khead_writer) {
+      u32x4 *kop = a.kh + chk * (NB_KH * 64) + KH_KT * 64;
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int e = tid + 256 * it;
+        const int blk = e >> 6, l = e & 63;
+        const int bi = blk >> 1, bs = blk & 1;
+        const int row = 16 * bi + (l & 15);
+        const int col = 32 * bs + 4 * (l >> 4);
+        const u32x2 x0 = *reinterpret_cast<const u32x2 *>(kt_s + tsw(row, col));
+        const u32x2 x1 = *reinterpret_cast<const u32x2 *>(kt_s + tsw(row, col + 16));
+        kop[e] = u32x4{x0.x, x0.y, x1.x, x1.y};
+      }
+    }
+    if (tid < CK) {
+      float *sc = reinterpret_cast<float *>(a.vh + ch * (NB_VH * 64) + VH_SC * 64);
+      const float gl = gam_s[CK - 1];
+      sc[tid] = expf(gam_s[tid]) * nq_s[tid];
+      sc[CK + tid] = expf(gl - gam_s[tid]) * nk_s[tid];
+      if (tid == 0) sc[2 * CK] = expf(gl);
     }
   }
 }
 
 // ------------------------------------------------------------------ phase B
-// Workgroup = 4 waves = 64 state columns of one (sequence, v-head); wave w owns
-// columns 16*(4*half + w) .. +16 and all 128 state rows (8 accumulator tiles).
-__global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkArgs a) {
+// LDS stage: one chunk's scan operands for a workgroup of NW waves: the
+// v-head region, the k-head region, then (when U_LDS) U^T for the
+// workgroup's 16*NW columns, 4 blocks per wave.  Without U_LDS each wave
+// prefetches its own U^T rows into registers instead (keeps two stages of an
+// 8-wave workgroup within the 160 KiB of LDS).
+constexpr int ST_W = VH_W * 64;
+constexpr int ST_A = VH_A * 64;
+constexpr int ST_SC = VH_SC * 64;
+constexpr int ST_Q = (NB_VH + KH_Q) * 64;
+constexpr int ST_KT = (NB_VH + KH_KT) * 64;
+constexpr int ST_U = (NB_VH + NB_KH) * 64;
+template <int NW, bool U_LDS> struct Stage {
+  static constexpr int blocks = NB_VH + NB_KH + (U_LDS ? 4 * NW : 0);
+  static constexpr int u4 = blocks * 64;  // size in 16-byte units
+};
+
+constexpr int BUF_DWORD3 = 0x00020000;  // raw (untyped) buffer resource word 3 on CDNA
+
+// Copies nb 1 KiB blocks of a region into LDS with buffer_load ... lds: a
+// uniform base (no per-lane 64-bit address math), 64 lanes x 16 bytes per
+// instruction, hardware bounds check against the region size.  Wave w
+// issues blocks w, w + NW, ...
+template <int NW>
+__device__ __forceinline__ void copy_region(u32x4 *dst, const void *src, int nb, int wave, int lane) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(src), 0, nb * 1024, BUF_DWORD3);
+#pragma unroll
+  for (int i = 0; i < (NB_KH + NW - 1) / NW; ++i) {
+    const int t = i * NW + wave;
+    if (t < nb) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst + t * 64, 16, lane * 16, t * 1024, 0, 0);
+  }
+}
+
+template <int NW, bool U_LDS>
+__device__ __forceinline__ void stage_load(u32x4 *st, const ChunkArgs &a, size_t ch, size_t chk, int col0,
+                                           int wave, int lane) {
+  copy_region<NW>(st, a.vh + ch * (NB_VH * 64), NB_VH, wave, lane);
+  copy_region<NW>(st + NB_VH * 64, a.kh + chk * (NB_KH * 64), NB_KH, wave, lane);
+  if constexpr (U_LDS) copy_region<NW>(st + ST_U, a.Ut + ch * (DV * CK) + col0 * CK, 4 * NW, wave, lane);
+}
+
+// One chunk of the scan for this wave's 16 state columns.  Operand blocks are
+// read from LDS in batches of 8 (32 VGPRs), each issued while the MFMAs of the
+// previous batch run; the sched_barriers pin that order (left alone, the
+// compiler sinks every read next to its MFMA and exposes the LDS latency
+// once per MFMA, or hoists all reads and spills).
+#define GDN_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
+
+__device__ __forceinline__ void ld_batch(u32x4 (&r)[8], const u32x4 *st, int base, int lane) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = st[base + i * 64 + lane];
+}
+
+template <bool BF16_OUT>
+__device__ __forceinline__ void scan_chunk(const u32x4 *st, const f32x4 (&u)[4], f32x4 (&S)[8], const ChunkArgs &a,
+                                           int64_t t0, int len, int h, int col, int lane) {
+  const int g4 = lane >> 4;
+  const float *sc = reinterpret_cast<const float *>(st + ST_SC);
+  // Operand groups of 4 blocks, double-buffered in registers: group k+1 is
+  // read from LDS while the MFMAs of group k run.
+  //   groups 0-3: -W rows p=0..3    4-7: Q rows p=0..3    8: A blocks 0,2,4,5
+  //   9: A blocks 6,7               10-13: K^T tiles i=2m, 2m+1
+  u32x4 bufA[4], bufB[4];
+  auto ld4 = [&](u32x4 (&r)[4], int g) {
+    if (g < 4) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[i] = st[ST_W + (4 * g + i) * 64 + lane];
+    } else if (g < 8) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[i] = st[ST_Q + (4 * (g - 4) + i) * 64 + lane];
+    } else if (g == 8) {
+      r[0] = st[ST_A + 0 * 64 + lane];
+      r[1] = st[ST_A + 2 * 64 + lane];
+      r[2] = st[ST_A + 4 * 64 + lane];
+      r[3] = st[ST_A + 5 * 64 + lane];
+    } else if (g == 9) {
+      r[0] = st[ST_A + 6 * 64 + lane];
+      r[1] = st[ST_A + 7 * 64 + lane];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[i] = st[ST_KT + (4 * (g - 10) + i) * 64 + lane];
+    }
+  };
+
+  bf16x8 sb[4];  // state as bf16 B operands (k-steps over the 128 state rows)
+  f32x4 vp[4];   // V' = U - W S   (rows: chunk positions 16p + 4g + e)
+  f32x4 o[4];    // O = diag(e^gamma nq) (Q S) + A V'
+  bf16x8 vb[2], vh[2], vl[2];
+  float eL = 0.f;
+  auto compute = [&](const u32x4 (&r)[4], int g) {
+    if (g < 4) {
+      vp[g] = u[g];
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) vp[g] = mfma(as_bf16x8(r[s2]), sb[s2], vp[g]);
+    } else if (g < 8) {
+      const int p = g - 4;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) acc = mfma(as_bf16x8(r[s2]), sb[s2], acc);
+      o[p] = acc * *reinterpret_cast<const f32x4 *>(sc + 16 * p + 4 * g4);
+    } else if (g == 8) {
+      vb[0] = pack_hi(vp[0], vp[1]);
+      vb[1] = pack_hi(vp[2], vp[3]);
+      o[0] = mfma(as_bf16x8(r[0]), vb[0], o[0]);
+      o[1] = mfma(as_bf16x8(r[1]), vb[0], o[1]);
+      o[2] = mfma(as_bf16x8(r[2]), vb[0], o[2]);
+      o[2] = mfma(as_bf16x8(r[3]), vb[1], o[2]);
+    } else if (g == 9) {
+      o[3] = mfma(as_bf16x8(r[0]), vb[0], o[3]);
+      o[3] = mfma(as_bf16x8(r[1]), vb[1], o[3]);
+#pragma unroll
+      for (int p2 = 0; p2 < 2; ++p2) {  // V'' = diag(e^{gamma_63 - gamma} nk) V', hi + lo
+        const f32x4 ska = *reinterpret_cast<const f32x4 *>(sc + CK + 32 * p2 + 4 * g4);
+        const f32x4 skb = *reinterpret_cast<const f32x4 *>(sc + CK + 32 * p2 + 16 + 4 * g4);
+        pack_hilo(vp[2 * p2] * ska, vp[2 * p2 + 1] * skb, vh[p2], vl[p2]);
+      }
+      eL = sc[2 * CK];
+    } else {  // S <- e^{gamma_63} S + K^T V''   for tiles 2m, 2m+1
+      const int m = g - 10;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int i = 2 * m + t;
+        S[i] = S[i] * eL;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          S[i] = mfma(as_bf16x8(r[2 * t + s2]), vh[s2], S[i]);
+          S[i] = mfma(as_bf16x8(r[2 * t + s2]), vl[s2], S[i]);
+        }
+      }
+    }
+  };
+
+  ld4(bufA, 0);
+  ld4(bufB, 1);
+  GDN_SCHED_FENCE();
+#pragma unroll
+  for (int s2 = 0; s2 < 4; ++s2) sb[s2] = pack_hi(S[2 * s2], S[2 * s2 + 1]);
+#pragma unroll
+  for (int g = 0; g < 14; g += 2) {
+    compute(bufA, g);
+    GDN_SCHED_FENCE();
+    if (g + 2 < 14) ld4(bufA, g + 2);
+    GDN_SCHED_FENCE();
+    compute(bufB, g + 1);
+    GDN_SCHED_FENCE();
+    if (g + 3 < 14) ld4(bufB, g + 3);
+    GDN_SCHED_FENCE();
+  }
+
+  // output rows 16p + 4g + e of column col (rows past the sequence are skipped)
+  const int64_t ostep = static_cast<int64_t>(a.Hv) * DV;
+  typedef typename std::conditional<BF16_OUT, uint16_t, float>::type OT;
+  OT *obase = static_cast<OT *>(a.o) + (t0 + 4 * g4) * ostep + (int64_t)h * DV + col;
+  if (len == CK) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        OT *dst = obase + (16 * p + e) * ostep;
+        if constexpr (BF16_OUT) *dst = bf16_rne(o[p][e]); else *dst = o[p][e];
+      }
+  } else {
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (16 * p + 4 * g4 + e < len) {
+          OT *dst = obase + (16 * p + e) * ostep;
+          if constexpr (BF16_OUT) *dst = bf16_rne(o[p][e]); else *dst = o[p][e];
+        }
+      }
+  }
+}
+
+// Workgroup = NW waves = 16*NW state columns of one (sequence, v-head).
+template <int NW, bool BF16_OUT, bool U_LDS>
+__global__ __launch_bounds__(64 * NW) void chunk_scan_kernel(ChunkArgs a) {
+  __shared__ u32x4 stage0[Stage<NW, U_LDS>::u4];
+  __shared__ u32x4 stage1[Stage<NW, U_LDS>::u4];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g4 = lane >> 4;
   const int r16 = lane & 15;
   const int nh = a.n_seqs * a.Hv;
-  const int half = blockIdx.x / nh;  // heads of a sequence are adjacent: all
-  const int rest = blockIdx.x % nh;  // tiles of a head land on one XCD
+  const int ct = blockIdx.x / nh;    // the column tiles of one head share bid % 8,
+  const int rest = blockIdx.x % nh;  // i.e. one XCD and its L2
   const int n = rest / a.Hv;
   const int h = rest % a.Hv;
   const int hk = h / (a.Hv / a.Hk);
-  const int vt = 4 * half + wave;
-  const int col = 16 * vt + r16;     // this lane's state column
+  const int col0 = 16 * NW * ct;     // first column of the workgroup
+  const int ucol = 16 * wave + r16;  // this lane's column within the workgroup
+  const int col = col0 + ucol;
 
+  // Values read from memory are workgroup-uniform; readfirstlane tells the
+  // compiler so (buffer resources built from them must live in SGPRs).
   int64_t s0;
   int slen;
   seq_bounds(a, n, &s0, &slen);
-  const int c0 = a.chunk_start[n];
-  // chunk_start is built from the clamped lengths, so it never exceeds the
+  s0 = uniform64(s0);
+  slen = __builtin_amdgcn_readfirstlane(slen);
+  const int c0 = __builtin_amdgcn_readfirstlane(a.chunk_start[n]);
+  // chunk_start is built from clamped lengths, so it never exceeds the
   // workspace bound; the min() keeps that true by construction here too.
-  const int nch = max(0, min(a.chunk_start[n + 1], a.max_chunks) - c0);
+  const int nch = __builtin_amdgcn_readfirstlane(max(0, min(a.chunk_start[n + 1], a.max_chunks) - c0));
 
   f32x4 S[8];
-  const int64_t in_row = a.h0 ? (a.h0_idx ? a.h0_idx[n] : n) : -1;
+  const int64_t in_row = a.h0 ? uniform64(a.h0_idx ? a.h0_idx[n] : n) : -1;
   if (in_row >= 0) {
     const float *src = a.h0 + (in_row * a.Hv + h) * (int64_t)(DK * DV) + col;
 #pragma unroll
@@ -425,88 +685,42 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkArgs a) {
     for (int i = 0; i < 8; ++i) S[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  for (int c = 0; c < nch; ++c) {
-    const int j = c0 + c;
-    const size_t ch = static_cast<size_t>(j) * a.Hv + h;
-    const int64_t t0 = s0 + static_cast<int64_t>(c) * CK;
-    const int len = min(CK, slen - c * CK);
-    const uint16_t *Wc = a.W + ch * (CK * DK);
-    const float *Uc = a.Ut + ch * (DV * CK) + col * CK;
-    const uint16_t *Ac = a.A + ch * (CK * CK);
-    const uint16_t *Ktc = a.Kt + (static_cast<size_t>(j) * a.Hk + hk) * (DK * CK);
-    const float *sc = a.scal + ch * SCAL;
-
-    // state as bf16 B operands (k-steps over the 128 state rows)
-    bf16x8 sb[4];
+  f32x4 u0[4], u1[4];
+  auto load_stage = [&](u32x4 *st, f32x4 (&u)[4], int cidx) {
+    const size_t j = static_cast<size_t>(c0 + cidx);
+    const size_t ch = j * a.Hv + h;
+    stage_load<NW, U_LDS>(st, a, ch, j * a.Hk + hk, col0, wave, lane);
+    if constexpr (!U_LDS) {
+      const float *uc = a.Ut + ch * (DV * CK) + col * CK + 4 * g4;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) sb[s] = pack_hi(S[2 * s], S[2 * s + 1]);
-
-    // V' = U - W S     (rows: chunk positions 16p + 4g4 + e)
-    f32x4 vp[4];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      vp[p] = *reinterpret_cast<const f32x4 *>(Uc + 16 * p + 4 * g4);
-      const uint16_t *wrow = Wc + (16 * p + r16) * DK + 4 * g4;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) vp[p] = mfma(ld_pi(wrow + 32 * s), sb[s], vp[p]);
+      for (int p = 0; p < 4; ++p) u[p] = *reinterpret_cast<const f32x4 *>(uc + 16 * p);
     }
-
-    // O = diag(e^gamma nq) (Q S) + A V'
-    bf16x8 vb[2];
-    vb[0] = pack_hi(vp[0], vp[1]);
-    vb[1] = pack_hi(vp[2], vp[3]);
+  };
+  auto run_chunk = [&](const u32x4 *st, f32x4 (&u)[4], int c) {
+    if constexpr (U_LDS) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int row = 16 * p + r16;
-      const bool live = row < len;
-      const uint16_t *qrow = a.q + (t0 + row) * a.qs + (int64_t)hk * DK + 4 * g4;
-      f32x4 oq = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) oq = mfma(live ? ld_pi(qrow + 32 * s) : zero8(), sb[s], oq);
-      const f32x4 sq = *reinterpret_cast<const f32x4 *>(sc + 16 * p + 4 * g4);
-      f32x4 o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = oq[e] * sq[e];
-      const uint16_t *arow = Ac + row * CK + 4 * g4;
-      o = mfma(ld_pi(arow), vb[0], o);
-      if (p >= 2) o = mfma(ld_pi(arow + 32), vb[1], o);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int orow = 16 * p + 4 * g4 + e;
-        if (orow < len) store_elem(a.o, ((t0 + orow) * a.Hv + h) * (int64_t)DV + col, a.o_dt, o[e]);
-      }
+      for (int p = 0; p < 4; ++p) u[p] = __builtin_bit_cast(f32x4, st[ST_U + ucol * 16 + 4 * p + g4]);
     }
-
-    // S <- e^{gamma_63} S + K^T diag(e^{gamma_63 - gamma} nk) V'   (V'' hi + lo)
-    bf16x8 vh[2], vl[2];
-#pragma unroll
-    for (int p2 = 0; p2 < 2; ++p2) {
-      const f32x4 ska = *reinterpret_cast<const f32x4 *>(sc + CK + 32 * p2 + 4 * g4);
-      const f32x4 skb = *reinterpret_cast<const f32x4 *>(sc + CK + 32 * p2 + 16 + 4 * g4);
-      f32x4 xa, xb;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        xa[e] = vp[2 * p2][e] * ska[e];
-        xb[e] = vp[2 * p2 + 1][e] * skb[e];
-      }
-      pack_hilo(xa, xb, vh[p2], vl[p2]);
-    }
-    const float eL = sc[2 * CK];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) S[i][e] *= eL;
-      const uint16_t *krow = Ktc + (16 * i + r16) * CK + 4 * g4;
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const bf16x8 ak = ld_pi(krow + 32 * s);
-        S[i] = mfma(ak, vh[s], S[i]);
-        S[i] = mfma(ak, vl[s], S[i]);
-      }
-    }
+    scan_chunk<BF16_OUT>(st, u, S, a, s0 + static_cast<int64_t>(c) * CK, min(CK, slen - c * CK), h, col, lane);
+  };
+  if (nch > 0) {
+    load_stage(stage0, u0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  for (int c = 0; c < nch; c += 2) {
+    if (c + 1 < nch) load_stage(stage1, u1, c + 1);
+    run_chunk(stage0, u0, c);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (c + 1 >= nch) break;
+    if (c + 2 < nch) load_stage(stage0, u0, c + 2);
+    run_chunk(stage1, u1, c + 1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
   }
 
-  const int64_t out_row = a.hT ? (a.hT_idx ? a.hT_idx[n] : n) : -1;
+  const int64_t out_row = a.hT ? uniform64(a.hT_idx ? a.hT_idx[n] : n) : -1;
   if (out_row >= 0) {
     float *dst = a.hT + (out_row * a.Hv + h) * (int64_t)(DK * DV) + col;
 #pragma unroll
@@ -516,27 +730,30 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(ChunkArgs a) {
   }
 }
 
+// Scan workgroup shape (measured on MI355X at T=4096, 32 v-heads): 4 waves =
+// 64 state columns per workgroup, U^T staged through LDS.  With 8 waves per
+// workgroup every wave re-reads the whole operand stage from LDS and the LDS
+// bandwidth becomes the limit; with 2 the stage is streamed four times.
+constexpr int SCAN_WAVES = 4;
+constexpr bool SCAN_U_LDS = true;
+
 struct WsLayout {
-  size_t chunk_start, W, Ut, A, Kt, scal, total;
+  size_t chunk_start, vh, kh, Ut, total;
 };
 
-__host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-WsLayout ws_layout(int n_seqs, int64_t max_chunks, int Hv, int Hk) {
+WsLayout ws_layout(int n_seqs, int64_t nc, int Hv, int Hk) {
   WsLayout l;
   size_t off = 0;
   l.chunk_start = off;
   off = align256(off + sizeof(int32_t) * (n_seqs + 1));
-  l.W = off;
-  off = align256(off + sizeof(uint16_t) * max_chunks * Hv * CK * DK);
+  l.vh = off;
+  off = align256(off + 16ull * nc * Hv * NB_VH * 64);
+  l.kh = off;
+  off = align256(off + 16ull * nc * Hk * NB_KH * 64);
   l.Ut = off;
-  off = align256(off + sizeof(float) * max_chunks * Hv * DV * CK);
-  l.A = off;
-  off = align256(off + sizeof(uint16_t) * max_chunks * Hv * CK * CK);
-  l.Kt = off;
-  off = align256(off + sizeof(uint16_t) * max_chunks * Hk * DK * CK);
-  l.scal = off;
-  off = align256(off + sizeof(float) * max_chunks * Hv * SCAL);
+  off = align256(off + sizeof(float) * nc * Hv * DV * CK);
   l.total = off;
   return l;
 }
@@ -553,7 +770,7 @@ extern "C" size_t gdn_chunk_workspace_bytes(int32_t n_seqs, int64_t total_tokens
                                             int32_t V) {
   using namespace gdn;
   if (n_seqs <= 0 || total_tokens < 0 || Hv <= 0 || K != DK || V != DV) return 0;
-  // Upper bound valid with or without cu_seqlens; K tiles counted at Hk = Hv.
+  // Upper bound valid with or without cu_seqlens; k-head blocks counted at Hk = Hv.
   const int64_t nc = (total_tokens + CK - 1) / CK + n_seqs;
   return ws_layout(n_seqs, nc, Hv, Hv).total;
 }
@@ -574,7 +791,9 @@ extern "C" int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qk
     return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd: q/k/v must be bf16 (MFMA operands)");
   if (n_seqs < 0 || T < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk)
     return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_chunk_fwd: bad sizes n_seqs=%d T=%d Hk=%d Hv=%d", n_seqs, T, Hk, Hv);
-  if (!valid_dtype(beta_dtype) || !valid_dtype(o_dtype)) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_chunk_fwd: bad dtype");
+  if (!valid_dtype(beta_dtype)) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_chunk_fwd: bad beta dtype");
+  if (o_dtype != GDN_DTYPE_BF16 && o_dtype != GDN_DTYPE_F32)
+    return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd: output must be bf16 or fp32");
   if (n_seqs == 0) return ok();
   if (!q || !k || !v || !g || !beta || !o) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_chunk_fwd: null q/k/v/g/beta/o");
   if (q_stride_t < Hk * K || k_stride_t < Hk * K || v_stride_t < Hv * V || (q_stride_t | k_stride_t | v_stride_t) % 8)
@@ -586,18 +805,25 @@ extern "C" int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qk
   const WsLayout l = ws_layout(n_seqs, nc, Hv, Hk);
   if (!workspace || workspace_bytes < l.total)
     return fail(GDN_ERR_WORKSPACE, "gdn_chunk_fwd: workspace %zu bytes < %zu needed", workspace_bytes, l.total);
+  if (reinterpret_cast<uintptr_t>(workspace) % 256)
+    return fail(GDN_ERR_WORKSPACE, "gdn_chunk_fwd: workspace must be 256-byte aligned");
   if (nc > 65535) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_chunk_fwd: %lld chunks exceed one launch", (long long)nc);
-  if (static_cast<int64_t>(n_seqs) * Hv * 2 > 0x7fffffff) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_chunk_fwd: grid");
+  const int64_t scan_blocks = static_cast<int64_t>(n_seqs) * Hv * (DV / (16 * SCAN_WAVES));
+  if (scan_blocks > 0x7fffffff) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_chunk_fwd: grid too large");
   char *ws = static_cast<char *>(workspace);
   ChunkArgs a{static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
               q_stride_t, k_stride_t, v_stride_t, g, beta, beta_dtype, h0, h0_idx, hT, hT_idx, o, o_dtype,
               cu_seqlens, n_seqs, T, Hk, Hv, total, scale, l2norm_qk, static_cast<int>(nc),
-              reinterpret_cast<int32_t *>(ws + l.chunk_start), reinterpret_cast<uint16_t *>(ws + l.W),
-              reinterpret_cast<float *>(ws + l.Ut), reinterpret_cast<uint16_t *>(ws + l.A),
-              reinterpret_cast<uint16_t *>(ws + l.Kt), reinterpret_cast<float *>(ws + l.scal)};
+              reinterpret_cast<int32_t *>(ws + l.chunk_start), reinterpret_cast<u32x4 *>(ws + l.vh),
+              reinterpret_cast<u32x4 *>(ws + l.kh), reinterpret_cast<float *>(ws + l.Ut)};
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, s, a);
   if (nc > 0) hipLaunchKernelGGL(chunk_prep_kernel, dim3(Hv, static_cast<unsigned>(nc)), dim3(256), 0, s, a);
-  hipLaunchKernelGGL(chunk_scan_kernel, dim3(static_cast<unsigned>(n_seqs * Hv * 2)), dim3(256), 0, s, a);
+  if (o_dtype == GDN_DTYPE_BF16)
+    hipLaunchKernelGGL((chunk_scan_kernel<SCAN_WAVES, true, SCAN_U_LDS>), dim3(static_cast<unsigned>(scan_blocks)),
+                       dim3(64 * SCAN_WAVES), 0, s, a);
+  else
+    hipLaunchKernelGGL((chunk_scan_kernel<SCAN_WAVES, false, SCAN_U_LDS>), dim3(static_cast<unsigned>(scan_blocks)),
+                       dim3(64 * SCAN_WAVES), 0, s, a);
   return check_launch("gdn_chunk_fwd");
 }
