@@ -3,23 +3,27 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill]
 
 Headline (``value``): decode throughput of one GDN layer at batch 64
-tokens/s, with the fp32 state pool updated in place.
-A "step" is one decode launch over the 64-sequence batch.  Inputs are
-resident in HBM before timing; the state pools rotate over 4 disjoint
-256 MiB pools (1 GiB) so the 256 MB Infinity Cache cannot serve a step's
-state from the previous one.
+(configuration 1), tokens/s: one step = one ``fused_recurrent_gated_delta_rule``
+launch over 64 sequences that updates the fp32 slot pool in place.  Inputs
+are resident in HBM before timing.  Steps rotate over 4 disjoint 256 MiB
+state pools (1 GiB), so no step's state can be served by the 256 MB
+Infinity Cache from an earlier step.  ``value`` is the rate of plain
+(eager) launches on the stream, host launch path included; the rate of the
+same steps replayed from HIP graphs (one per pool) is reported beside it.
 
 The JSON line also carries
-  roofline      decode kernel: algorithmic bytes per launch / mean launch time
-                (HIP events on the launch stream) vs the 8 TB/s HBM peak;
-  prefill       chunk-64 prefill at T=4096 (config 2): tok/s and dense-equivalent
-                MFMA fraction of the 2.5 PFLOP/s bf16 peak;
-  cpu_baseline  the CPU oracle (numpy fp32) on a bounded sample of the same
-                decode workload, on the host cores.
+  roofline      decode kernel: algorithmic bytes per launch / mean kernel time
+                (K back-to-back launches between two HIP events on the launch
+                stream) against the 8 TB/s HBM peak;
+  prefill       chunk-64 prefill at T=4096 (configuration 2): tok/s and the
+                dense-equivalent flop rate against the 2.5 PFLOP/s bf16 peak;
+  cpu_baseline  the CPU oracle (numpy fp32, sequences split over the host's
+                cores) on a bounded sample of the same decode workload.
 """
 from __future__ import annotations
 
 import argparse
+import concurrent.futures as cf
 import json
 import os
 import sys
@@ -28,19 +32,22 @@ import time
 REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "paris-hackathon-2026-inference_amd"))
 
-HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
-MFMA_BF16_PEAK = 2.5e15    # dense flop/s
-DECODE_BYTES = 270_024_960  # per launch at B=64 (state r+w 268,435,456 + q/k@16 heads, v, o, g, beta, slots)
-PREFILL_FLOP_PER_CHUNK_HEAD = 11_709_099  # 2C^2(3K+2V) + 6CKV + (2/3)C^3, C=64, K=V=128
+HBM_PEAK = 8.0e12           # B/s, MI355X HBM3E (vendor figure)
+MFMA_BF16_PEAK = 2.5e15     # dense flop/s
+# bytes per decode launch at B=64: state read + write 268,435,456; q, k (16 heads) 524,288;
+# v 524,288; o 524,288; g, beta 16,384; slot ids 256
+DECODE_BYTES = 270_024_960
+# dense-equivalent flops per (chunk, head): 2C^2(3K+2V) + 6CKV + (2/3)C^3, C=64, K=V=128
+PREFILL_FLOP_PER_CHUNK_HEAD = 11_709_099
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill line")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill measurement")
     ap.add_argument("--pools", type=int, default=4, help="rotating decode state pools")
     return ap.parse_args()
 
@@ -54,7 +61,7 @@ def bench_decode(torch, steps, warmup, n_pools):
     q, k, v, g, beta = (c[x].to(dev) for x in ("q", "k", "v", "g", "beta"))
     slots = c["slots"].to(dev)
     pools = [c["pool"].to(dev)]
-    for i in range(1, n_pools):
+    for _ in range(1, n_pools):
         pools.append(torch.randn_like(pools[0]).mul_(0.1))
     b = q.shape[0]
 
@@ -67,19 +74,51 @@ def bench_decode(torch, steps, warmup, n_pools):
         step(i)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+
+    # kernel time: K back-to-back eager launches between two events on the launch stream
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    kernel_s = e0.elapsed_time(e1) * 1e-3 / steps
+
+    # eager whole-job rate (host launch path included)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        ev[i][0].record(stream)
         step(i)
-        ev[i][1].record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per = sorted(e0.elapsed_time(e1) * 1e-3 for e0, e1 in ev)
-    mean_launch = sum(per) / len(per)
-    return dict(tokens=b, wall=wall, steps=steps, mean_launch_s=mean_launch, median_launch_s=per[len(per) // 2],
-                min_launch_s=per[0])
+    eager_wall = time.perf_counter() - t0
+
+    # graph replay: one graph per pool
+    graphs = []
+    try:
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            for i in range(n_pools):
+                step(i)
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        for i in range(n_pools):
+            gph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gph):
+                step(i)
+            graphs.append(gph)
+        for i in range(warmup):
+            graphs[i % n_pools].replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            graphs[i % n_pools].replay()
+        torch.cuda.synchronize()
+        graph_wall = time.perf_counter() - t0
+    except RuntimeError as e:  # capture unavailable: fall back to the eager figure
+        print(f"bench.py: graph capture failed ({e}); reporting eager launches", file=sys.stderr)
+        graph_wall = None
+    return dict(tokens=b, steps=steps, kernel_s=kernel_s, eager_wall=eager_wall, graph_wall=graph_wall)
 
 
 def bench_prefill(torch, reps=20, warmup=3):
@@ -98,65 +137,65 @@ def bench_prefill(torch, reps=20, warmup=3):
         run()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    times = []
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
     for _ in range(reps):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
         run()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        times.append(e0.elapsed_time(e1) * 1e-3)
-    times.sort()
-    med = times[len(times) // 2]
-    n_chunks = (t + 63) // 64
-    flop = PREFILL_FLOP_PER_CHUNK_HEAD * n_chunks * 32
-    return {"config": "prefill B=1 T=4096 Hk=16 Hv=32 d=128 bf16, chunk 64, zero h0",
-            "tok_per_s": t / med, "ms": med * 1e3,
-            "mfma": {"achieved": flop / med / 1e12, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
-                     "frac": flop / med / MFMA_BF16_PEAK, "flop_per_call": flop}}
+    e1.record(stream)
+    torch.cuda.synchronize()
+    per = e0.elapsed_time(e1) * 1e-3 / reps
+    flop = PREFILL_FLOP_PER_CHUNK_HEAD * ((t + 63) // 64) * 32
+    return {"config": "prefill B=1 T=4096 Hk=16 Hv=32 d=128 bf16, chunk 64, zero h0, final state out",
+            "tok_per_s": t / per, "ms": per * 1e3,
+            "mfma": {"achieved": flop / per / 1e12, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+                     "frac": flop / per / MFMA_BF16_PEAK, "flop_per_call": flop}}
 
 
 def cpu_baseline(budget_s=15.0):
-    """CPU oracle (numpy fp32) on a bounded sample of the decode workload."""
+    """CPU oracle (numpy fp32) on a bounded sample of the decode workload, sequences
+    split across the host cores this process may use."""
     import numpy as np
-    import torch
     from engine import configs
     from oracle import gdn
 
     c = configs.config1()
     args = [c[x].float().numpy() for x in ("q", "k", "v", "g", "beta")]
-    pool = c["pool"].numpy()
-    slots = c["slots"].numpy()
-    h0 = pool[slots]
-    # warmup
-    gdn.recurrent_gated_delta_rule(*args, initial_state=h0, dtype=np.float32)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        gdn.recurrent_gated_delta_rule(*args, initial_state=h0, dtype=np.float32)
-        n += 1
-        el = time.perf_counter() - t0
-        if el > budget_s or n >= 200:
-            break
-    per = el / n
-    return {"value": 64 / per, "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": f"{n} decode steps of config 1 (B=64, one layer, 64 slots gathered) with the numpy fp32 "
-                      f"oracle on one host thread, {per * 1e3:.1f} ms/step",
-            "threads_note": f"torch threads {torch.get_num_threads()}, numpy einsum single-threaded"}
+    h0 = c["pool"].numpy()[c["slots"].numpy()]
+    n = min(16, len(os.sched_getaffinity(0)))
+    parts = [slice(i * 64 // n, (i + 1) * 64 // n) for i in range(n)]
+
+    def run_part(sl):
+        return gdn.recurrent_gated_delta_rule(*(a[sl] for a in args), initial_state=h0[sl], dtype=np.float32)
+
+    with cf.ThreadPoolExecutor(n) as ex:
+        list(ex.map(run_part, parts))  # warmup
+        steps, t0 = 0, time.perf_counter()
+        while True:
+            list(ex.map(run_part, parts))
+            steps += 1
+            el = time.perf_counter() - t0
+            if el > budget_s or steps >= 500:
+                break
+    per = el / steps
+    return {"value": 64 / per, "unit": "tok/s", "cores": n, "kind": "port",
+            "sample": f"{steps} decode steps of configuration 1 (B=64, one layer, 64 gathered slot states) with "
+                      f"the numpy fp32 oracle, sequences split over {n} threads; {per * 1e3:.1f} ms/step"}
 
 
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
-              "the GDN path needs no collective, see DESIGN.md for how it shards", file=sys.stderr)
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the GDN path "
+              "shards over sequences and heads with no exchange (DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     d = bench_decode(torch, args.steps, args.warmup, args.pools)
-    value = d["tokens"] * d["steps"] / d["wall"]
-    achieved = DECODE_BYTES / d["mean_launch_s"]
+    wall = d["eager_wall"]
+    value = d["tokens"] * d["steps"] / wall
+    achieved = DECODE_BYTES / d["kernel_s"]
     out = {
         "metric": "GDN decode tok/s @B=64 (HBM GB/s); prefill tok/s @T=4096 (MFMA %)",
         "value": value,
@@ -164,26 +203,23 @@ def main():
         "n_gpus": 1,
         "steps": d["steps"],
         "warmup": args.warmup,
-        "ms_per_step": d["wall"] / d["steps"] * 1e3,
+        "ms_per_step": wall / d["steps"] * 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": "synthetic (seeded BASELINE config 1: bf16 q/k/v, fp32 gates and state pool)",
-        "config": {"workload": "GDN decode, one layer, B=64, Hk=16 Hv=32 d=128, fp32 slot pool "
-                               "[128,32,128,128] updated in place, 4 rotating pools",
-                   "global_batch": 64, "seq_len": 1, "parallelism": "none (1 GPU)"},
+        "data": "synthetic, seeded (configuration 1: bf16 q/k/v, fp32 gates and state pool ~N(0,0.1))",
+        "config": {"workload": "GDN decode, one layer, B=64, Hk=16 Hv=32 d=128, fp32 slot pool [128,32,128,128] "
+                               "updated in place, 4 rotating pools",
+                   "global_batch": 64, "seq_len": 1, "parallelism": "none (1 GPU)", "launch": "eager"},
+        "graph_tok_per_s": (d["tokens"] * d["steps"] / d["graph_wall"]) if d["graph_wall"] else None,
         "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK, "traffic": None,
-                     "kernel": "recurrent_kernel<32>", "mean_launch_us": d["mean_launch_s"] * 1e6,
-                     "median_launch_us": d["median_launch_s"] * 1e6,
+                     "kernel": "gdn::recurrent_kernel<32>", "kernel_us": d["kernel_s"] * 1e6,
                      "bytes_per_launch": DECODE_BYTES},
     }
     if not args.no_prefill:
-        try:
-            out["prefill"] = bench_prefill(torch)
-        except RuntimeError as e:  # chunk kernel not built in this library
-            out["prefill"] = {"error": str(e).splitlines()[0]}
+        out["prefill"] = bench_prefill(torch)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)
