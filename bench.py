@@ -37,6 +37,9 @@ MFMA_BF16_PEAK = 2.5e15     # dense flop/s
 # bytes per decode launch at B=64: state read + write 268,435,456; q, k (16 heads) 524,288;
 # v 524,288; o 524,288; g, beta 16,384; slot ids 256
 DECODE_BYTES = 270_024_960
+# HBM bytes per decode launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE, each scaled by
+# the same counter on a plain 128 MiB copy (profiles/gdn_decode_b64_hbm_traffic_pmc.md)
+DECODE_TRAFFIC_MEASURED = 274_608_128
 # dense-equivalent flops per (chunk, head): 2C^2(3K+2V) + 6CKV + (2/3)C^3, C=64, K=V=128
 PREFILL_FLOP_PER_CHUNK_HEAD = 11_709_099
 
@@ -49,7 +52,21 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill measurement")
     ap.add_argument("--pools", type=int, default=4, help="rotating decode state pools")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 128 MiB device copy (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
+
+
+def copy_probe(torch, reps=20):
+    """A plain device-to-device copy of 128 MiB, repeated: the HBM traffic counters of
+    this kernel calibrate the decode kernel's (known bytes: 128 MiB read + 128 MiB written)."""
+    n = (128 << 20) // 4
+    src = [torch.randn(n, device="cuda") for _ in range(4)]
+    dst = [torch.empty(n, device="cuda") for _ in range(4)]
+    for i in range(reps):
+        dst[i % 4].copy_(src[(i + 1) % 4])
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_each_way": 128 << 20, "reps": reps}), flush=True)
 
 
 def bench_decode(torch, steps, warmup, n_pools):
@@ -192,6 +209,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.copy_probe:
+        copy_probe(torch)
+        return
     d = bench_decode(torch, args.steps, args.warmup, args.pools)
     wall = d["eager_wall"]
     value = d["tokens"] * d["steps"] / wall
@@ -214,7 +234,7 @@ def main():
                    "global_batch": 64, "seq_len": 1, "parallelism": "none (1 GPU)", "launch": "eager"},
         "graph_tok_per_s": (d["tokens"] * d["steps"] / d["graph_wall"]) if d["graph_wall"] else None,
         "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK, "traffic": None,
+                     "frac": achieved / HBM_PEAK, "traffic": DECODE_TRAFFIC_MEASURED,
                      "kernel": "gdn::recurrent_kernel<32>", "kernel_us": d["kernel_s"] * 1e6,
                      "bytes_per_launch": DECODE_BYTES},
     }
