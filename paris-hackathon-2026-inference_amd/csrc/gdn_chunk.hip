@@ -31,6 +31,7 @@
 // as the B operand of the next product, lane group g = l/16 holds reduction
 // indices {4g..4g+3, 16+4g..16+4g+3} ("pi" order); the scan's A-operand
 // blocks are stored in the same order, so no accumulator goes through LDS.
+#include <algorithm>
 #include <type_traits>
 
 #include "gdn_common.h"
@@ -118,11 +119,13 @@ struct ChunkArgs {
   float scale;
   int l2norm;
   int max_chunks;
+  int seg_begin, seg_end;  // global chunk range of this launch (workspace holds SEG chunks)
   // workspace
   int32_t *chunk_start;  // [n_seqs + 1]
-  u32x4 *vh;             // [NC][Hv][NB_VH][64]   -W, A, scalars
-  u32x4 *kh;             // [NC][Hk][NB_KH][64]   Q, K^T
-  float *Ut;             // [NC][Hv][128][64]     U transposed, fp32
+  u32x4 *vh;             // [SEG][Hv][NB_VH][64]   -W, A, scalars
+  u32x4 *kh;             // [SEG][Hk][NB_KH][64]   Q, K^T
+  float *Ut;             // [SEG][Hv][128][64]     U transposed, fp32
+  float *carry;          // [n_seqs][Hv][128][128] state between segments
 };
 
 __device__ __forceinline__ void seq_bounds(const ChunkArgs &a, int n, int64_t *s0, int *len) {
@@ -159,21 +162,32 @@ constexpr int WS_LD = DK + 8;    // bf16 row stride of the -W staging tile (same
 static_assert(CK * LT_LD * 4 == CK * WS_LD * 2, "W staging reuses the L/T buffer");
 
 // Transposed [128][64] bf16 tiles (K^T, V^T): 16-byte segment seg of row r is
-// stored at segment seg ^ (r & 7) to spread LDS banks.
+// stored at segment seg ^ f(r), f(r) = ((r >> 1) ^ (r >> 3)) & 7.  With this
+// swizzle the MFMA operand reads (16 consecutive rows, one segment) touch
+// distinct banks, and the transposing 2-byte writes (rows 8 apart, one
+// column) collide at most 2-way.
 __device__ __forceinline__ int tsw(int row, int col) {
-  return row * CK + ((((col >> 3) ^ row) & 7) << 3) + (col & 7);
+  return row * CK + ((((col >> 3) ^ (row >> 1) ^ (row >> 3)) & 7) << 3) + (col & 7);
 }
 
+// Row-major [64][128] bf16 K tile: 16-byte segment seg of row r at seg ^ (r & 15).
+__device__ __forceinline__ int nsw(int row, int col) {
+  return row * DK + ((((col >> 3) ^ row) & 15) << 3) + (col & 7);
+}
+constexpr int AS_LD = CK + 8;  // bf16 row stride of the A staging tile
+
 __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
-  __shared__ __align__(16) uint16_t kt_s[DK * CK];
-  __shared__ __align__(16) uint16_t vt_s[DV * CK];
-  __shared__ __align__(16) float lt[CK * LT_LD];   // L, then T in place, then -W staging
+  __shared__ __align__(16) uint16_t kn_s[CK * DK];   // K rows (MFMA operands of K K^T, Q K^T)
+  __shared__ __align__(16) uint16_t kt_s[DK * CK];   // K^T (B operand of W, scan operand blocks)
+  __shared__ __align__(16) uint16_t vt_s[DV * CK];   // V^T (B operand of U)
+  __shared__ __align__(16) float lt[CK * LT_LD];      // L, then T in place, then -W staging
+  __shared__ __align__(16) uint16_t as_s[CK * AS_LD]; // A staging
   __shared__ __align__(16) float xs[3][16][17];
-  __shared__ float gam_s[CK], beta_s[CK], nk_s[CK], nq_s[CK];
+  __shared__ float gam_s[CK], beta_s[CK], nk_s[CK], nq_s[CK], colw_s[CK];
 
   const int h = blockIdx.x;
-  const int j = blockIdx.y;
-  if (j >= a.chunk_start[a.n_seqs]) return;
+  const int j = a.seg_begin + static_cast<int>(blockIdx.y);  // global chunk index
+  if (j >= a.seg_end || j >= a.chunk_start[a.n_seqs]) return;
   int lo = 0, hi = a.n_seqs;  // sequence owning chunk j: last n with chunk_start[n] <= j
   while (hi - lo > 1) {
     const int mid = (lo + hi) >> 1;
@@ -196,8 +210,10 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
   const int wave = tid >> 6;
   const int g4 = lane >> 4;
   const int r16 = lane & 15;
-  const size_t ch = static_cast<size_t>(j) * a.Hv + h;
-  const size_t chk = static_cast<size_t>(j) * a.Hk + hk;
+  const int jl = static_cast<int>(blockIdx.y);  // chunk index within the segment's workspace
+  const size_t ch = static_cast<size_t>(jl) * a.Hv + h;
+  const size_t chk = static_cast<size_t>(jl) * a.Hk + hk;
+  const int p = wave;  // row block of K K^T / Q K^T / W / U owned by this wave
 
   // ---- issue every global load up front
   const int seg = tid & 15;
@@ -211,25 +227,12 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
     qu[it] = row < len ? *reinterpret_cast<const u32x4 *>(a.q + tok * a.qs + (int64_t)hk * DK + seg * 8) : z;
     vu[it] = row < len ? *reinterpret_cast<const u32x4 *>(a.v + tok * a.vs + (int64_t)h * DV + seg * 8) : z;
   }
-  // MFMA operands of K K^T / Q K^T for row block p = wave
-  const int p = wave;
-  bf16x8 ak[4], aq[4], bk[4][4];
+  bf16x8 aq[4];  // Q rows of block p (A operands of Q K^T)
   {
     const int row = 16 * p + r16;
-    const uint16_t *krow = a.k + (t0 + row) * a.ks + (int64_t)hk * DK + 8 * g4;
     const uint16_t *qrow = a.q + (t0 + row) * a.qs + (int64_t)hk * DK + 8 * g4;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      ak[s] = row < len ? ld8(krow + 32 * s) : zero8();
-      aq[s] = row < len ? ld8(qrow + 32 * s) : zero8();
-    }
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-      const int col = 16 * cb + r16;
-      const uint16_t *kcol = a.k + (t0 + col) * a.ks + (int64_t)hk * DK + 8 * g4;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) bk[cb][s] = (cb <= p && col < len) ? ld8(kcol + 32 * s) : zero8();
-    }
+    for (int s = 0; s < 4; ++s) aq[s] = row < len ? ld8(qrow + 32 * s) : zero8();
   }
   float gv = 0.f, bv = 0.f;
   if (wave == 0 && lane < len) {
@@ -237,10 +240,11 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
     bv = load_elem(a.beta, (t0 + lane) * a.Hv + h, a.beta_dt);
   }
 
-  // ---- A.1: K^T, V^T into LDS; row norms; chunk-local cumsum of g
+  // ---- A.1: K (rows and transposed), V^T into LDS; row norms; chunk-local cumsum of g
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int row = (tid >> 4) + 16 * it;
+    *reinterpret_cast<u32x4 *>(kn_s + nsw(row, seg * 8)) = ku[it];
     float sk = 0.f, sq = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -291,42 +295,61 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
   }
   __syncthreads();
 
-  // ---- A.2: K K^T -> L (fp32, LDS), Q K^T -> A (pi-order blocks, global)
+  // ---- A.2: K K^T -> L (fp32, LDS), Q K^T -> A (bf16, LDS staging)
+  if (wave == 0) colw_s[lane] = beta_s[lane] * expf(gam_s[lane]) * nk_s[lane];  // W's column scale
   {
-    u32x4 *aop = a.vh + ch * (NB_VH * 64) + VH_A * 64;
+    bf16x8 ak[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) ak[s] = ld8(kn_s + nsw(16 * p + r16, 32 * s + 8 * g4));
+    float gi[4], ni[4], qi[4], bi[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int ii = 16 * p + 4 * g4 + e;
+      gi[e] = gam_s[ii];
+      ni[e] = nk_s[ii];
+      qi[e] = nq_s[ii];
+      bi[e] = beta_s[ii];
+    }
+#pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
       f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = kk;
       if (cb <= p) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          kk = mfma(ak[s], bk[cb][s], kk);
-          qk = mfma(aq[s], bk[cb][s], qk);
+          const bf16x8 bk = ld8(kn_s + nsw(16 * cb + r16, 32 * s + 8 * g4));
+          kk = mfma(ak[s], bk, kk);
+          qk = mfma(aq[s], bk, qk);
         }
       }
       const int jj = 16 * cb + r16;
-      const int sblk = cb >> 1;
-      const bool a_used = sblk <= (p >= 2 ? 1 : 0);
-      uint16_t *ablk = reinterpret_cast<uint16_t *>(aop + (p * 2 + sblk) * 64);
+      const float gj = gam_s[jj], nj = nk_s[jj];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int ii = 16 * p + 4 * g4 + e;
         float lval = 0.f, aval = 0.f;
         if (cb <= p && ii >= jj) {
-          const float dec = expf(gam_s[ii] - gam_s[jj]);
-          aval = nq_s[ii] * nk_s[jj] * qk[e] * dec;
-          if (ii > jj) lval = beta_s[ii] * nk_s[ii] * nk_s[jj] * kk[e] * dec;
+          const float dec = expf(gi[e] - gj);
+          aval = qi[e] * nj * qk[e] * dec;
+          if (ii > jj) lval = bi[e] * ni[e] * nj * kk[e] * dec;
         }
         lt[ii * LT_LD + jj] = lval;
-        if (a_used) {
-          // element (row ii, col jj) of block (p, sblk): lane (ii&15) + 16 g, slot
-          const int cc = jj - 32 * sblk;
-          const int lane_op = (ii & 15) + 16 * ((cc & 15) >> 2);
-          ablk[lane_op * 8 + (cc >> 4) * 4 + (cc & 3)] = f32_to_bf16_bits(aval);
-        }
+        as_s[ii * AS_LD + jj] = bf16_rne(aval);
       }
     }
   }
   __syncthreads();
+  {  // A operand blocks (pi order) -> global: blocks 0, 2, 4, 5, 6, 7 of [p][s]
+    u32x4 *aop = a.vh + ch * (NB_VH * 64) + VH_A * 64;
+    for (int e = tid; e < 6 * 64; e += 256) {
+      const int id = e >> 6, l = e & 63;
+      const int blk = id == 0 ? 0 : (id == 1 ? 2 : id + 2);  // ids 0..5 -> blocks 0, 2, 4, 5, 6, 7
+      const int bp = blk >> 1, bs = blk & 1;
+      const uint16_t *src = as_s + (16 * bp + (l & 15)) * AS_LD + 32 * bs + 4 * (l >> 4);
+      const u32x2 x0 = *reinterpret_cast<const u32x2 *>(src);
+      const u32x2 x1 = *reinterpret_cast<const u32x2 *>(src + 16);
+      aop[blk * 64 + l] = u32x4{x0.x, x0.y, x1.x, x1.y};
+    }
+  }
 
   // ---- A.3: T = (I + L)^-1 in place (16x16 diagonal blocks by substitution)
   {
@@ -391,7 +414,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
         const int col = 32 * s + 8 * g4 + e;
         const float t = s < nsteps ? trow[e] : 0.f;
         const float tb = t * beta_s[col];
-        const float tw = tb * expf(gam_s[col]) * nk_s[col];
+        const float tw = t * colw_s[col];
         const __bf16 hw = static_cast<__bf16>(tw), hu = static_cast<__bf16>(tb);
         wa_hi[s][e] = hw;
         wa_lo[s][e] = static_cast<__bf16>(tw - static_cast<float>(hw));
@@ -667,15 +690,37 @@ __global__ __launch_bounds__(64 * NW) void chunk_scan_kernel(ChunkArgs a) {
   seq_bounds(a, n, &s0, &slen);
   s0 = uniform64(s0);
   slen = __builtin_amdgcn_readfirstlane(slen);
-  const int c0 = __builtin_amdgcn_readfirstlane(a.chunk_start[n]);
-  // chunk_start is built from clamped lengths, so it never exceeds the
-  // workspace bound; the min() keeps that true by construction here too.
-  const int nch = __builtin_amdgcn_readfirstlane(max(0, min(a.chunk_start[n + 1], a.max_chunks) - c0));
+  // Chunks [cs, ce) of sequence n; this launch covers global chunks
+  // [seg_begin, seg_end).  chunk_start is built from clamped lengths, so it
+  // never exceeds the workspace bound; the min() keeps that true here too.
+  const int cs = __builtin_amdgcn_readfirstlane(a.chunk_start[n]);
+  const int ce = __builtin_amdgcn_readfirstlane(max(cs, min(a.chunk_start[n + 1], a.max_chunks)));
+  const int lo = max(cs, a.seg_begin), hi = min(ce, a.seg_end);
+  const int64_t in_row = a.h0 ? uniform64(a.h0_idx ? a.h0_idx[n] : n) : -1;
+  const int64_t out_row = a.hT ? uniform64(a.hT_idx ? a.hT_idx[n] : n) : -1;
+  const int64_t kv = static_cast<int64_t>(DK) * DV;
+  if (cs == ce) {  // empty sequence: the final state is the initial one (handled once)
+    if (a.seg_begin == 0 && out_row >= 0) {
+      float *dst = a.hT + (out_row * a.Hv + h) * kv + col;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 16 * i + 4 * g4 + e;
+          dst[r * DV] = in_row >= 0 ? a.h0[(in_row * a.Hv + h) * kv + r * DV + col] : 0.f;
+        }
+    }
+    return;
+  }
+  if (lo >= hi) return;  // no chunk of this sequence in this segment
+  const int nch = hi - lo;
+  const int c0 = lo - a.seg_begin;             // first chunk, workspace-local
+  const int64_t seq_off = static_cast<int64_t>(lo - cs) * CK;  // its first token within the sequence
+  float *carry = a.carry + (static_cast<int64_t>(n) * a.Hv + h) * kv + col;
 
   f32x4 S[8];
-  const int64_t in_row = a.h0 ? uniform64(a.h0_idx ? a.h0_idx[n] : n) : -1;
-  if (in_row >= 0) {
-    const float *src = a.h0 + (in_row * a.Hv + h) * (int64_t)(DK * DV) + col;
+  const float *src = lo == cs ? (in_row >= 0 ? a.h0 + (in_row * a.Hv + h) * kv + col : nullptr) : carry;
+  if (src) {
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
@@ -701,7 +746,8 @@ __global__ __launch_bounds__(64 * NW) void chunk_scan_kernel(ChunkArgs a) {
 #pragma unroll
       for (int p = 0; p < 4; ++p) u[p] = __builtin_bit_cast(f32x4, st[ST_U + ucol * 16 + 4 * p + g4]);
     }
-    scan_chunk<BF16_OUT>(st, u, S, a, s0 + static_cast<int64_t>(c) * CK, min(CK, slen - c * CK), h, col, lane);
+    const int64_t toff = seq_off + static_cast<int64_t>(c) * CK;  // token offset within the sequence
+    scan_chunk<BF16_OUT>(st, u, S, a, s0 + toff, min<int64_t>(CK, slen - toff), h, col, lane);
   };
   if (nch > 0) {
     load_stage(stage0, u0, 0);
@@ -720,9 +766,8 @@ __global__ __launch_bounds__(64 * NW) void chunk_scan_kernel(ChunkArgs a) {
     __syncthreads();
   }
 
-  const int64_t out_row = a.hT ? uniform64(a.hT_idx ? a.hT_idx[n] : n) : -1;
-  if (out_row >= 0) {
-    float *dst = a.hT + (out_row * a.Hv + h) * (int64_t)(DK * DV) + col;
+  float *dst = hi == ce ? (out_row >= 0 ? a.hT + (out_row * a.Hv + h) * kv + col : nullptr) : carry;
+  if (dst) {
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
@@ -737,23 +782,30 @@ __global__ __launch_bounds__(64 * NW) void chunk_scan_kernel(ChunkArgs a) {
 constexpr int SCAN_WAVES = 4;
 constexpr bool SCAN_U_LDS = true;
 
+// Chunks per prep + scan segment: the operand workspace of one segment
+// (about 2.3 MiB per chunk at 32 v-heads) stays resident in the 256 MB
+// Infinity Cache between the producer and the consumer launch.
+constexpr int SEG_CHUNKS = 16;
+
 struct WsLayout {
-  size_t chunk_start, vh, kh, Ut, total;
+  size_t chunk_start, vh, kh, Ut, carry, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-WsLayout ws_layout(int n_seqs, int64_t nc, int Hv, int Hk) {
+WsLayout ws_layout(int n_seqs, int64_t seg_chunks, int Hv, int Hk, bool need_carry) {
   WsLayout l;
   size_t off = 0;
   l.chunk_start = off;
   off = align256(off + sizeof(int32_t) * (n_seqs + 1));
   l.vh = off;
-  off = align256(off + 16ull * nc * Hv * NB_VH * 64);
+  off = align256(off + 16ull * seg_chunks * Hv * NB_VH * 64);
   l.kh = off;
-  off = align256(off + 16ull * nc * Hk * NB_KH * 64);
+  off = align256(off + 16ull * seg_chunks * Hk * NB_KH * 64);
   l.Ut = off;
-  off = align256(off + sizeof(float) * nc * Hv * DV * CK);
+  off = align256(off + sizeof(float) * seg_chunks * Hv * DV * CK);
+  l.carry = off;
+  if (need_carry) off = align256(off + sizeof(float) * static_cast<size_t>(n_seqs) * Hv * DK * DV);
   l.total = off;
   return l;
 }
@@ -772,7 +824,7 @@ extern "C" size_t gdn_chunk_workspace_bytes(int32_t n_seqs, int64_t total_tokens
   if (n_seqs <= 0 || total_tokens < 0 || Hv <= 0 || K != DK || V != DV) return 0;
   // Upper bound valid with or without cu_seqlens; k-head blocks counted at Hk = Hv.
   const int64_t nc = (total_tokens + CK - 1) / CK + n_seqs;
-  return ws_layout(n_seqs, nc, Hv, Hv).total;
+  return ws_layout(n_seqs, std::min<int64_t>(nc, SEG_CHUNKS), Hv, Hv, nc > SEG_CHUNKS).total;
 }
 
 extern "C" int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
@@ -802,7 +854,8 @@ extern "C" int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qk
     return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_chunk_fwd: q/k/v must be 16-byte aligned");
   const int64_t total = cu_seqlens ? static_cast<int64_t>(T) : static_cast<int64_t>(n_seqs) * T;
   const int64_t nc = max_chunks_of(n_seqs, total, cu_seqlens != nullptr, T);
-  const WsLayout l = ws_layout(n_seqs, nc, Hv, Hk);
+  const int64_t seg = std::min<int64_t>(nc, SEG_CHUNKS);
+  const WsLayout l = ws_layout(n_seqs, seg, Hv, Hk, nc > SEG_CHUNKS);
   if (!workspace || workspace_bytes < l.total)
     return fail(GDN_ERR_WORKSPACE, "gdn_chunk_fwd: workspace %zu bytes < %zu needed", workspace_bytes, l.total);
   if (reinterpret_cast<uintptr_t>(workspace) % 256)
@@ -813,17 +866,24 @@ extern "C" int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qk
   char *ws = static_cast<char *>(workspace);
   ChunkArgs a{static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
               q_stride_t, k_stride_t, v_stride_t, g, beta, beta_dtype, h0, h0_idx, hT, hT_idx, o, o_dtype,
-              cu_seqlens, n_seqs, T, Hk, Hv, total, scale, l2norm_qk, static_cast<int>(nc),
+              cu_seqlens, n_seqs, T, Hk, Hv, total, scale, l2norm_qk, static_cast<int>(nc), 0, 0,
               reinterpret_cast<int32_t *>(ws + l.chunk_start), reinterpret_cast<u32x4 *>(ws + l.vh),
-              reinterpret_cast<u32x4 *>(ws + l.kh), reinterpret_cast<float *>(ws + l.Ut)};
+              reinterpret_cast<u32x4 *>(ws + l.kh), reinterpret_cast<float *>(ws + l.Ut),
+              reinterpret_cast<float *>(ws + l.carry)};
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, s, a);
-  if (nc > 0) hipLaunchKernelGGL(chunk_prep_kernel, dim3(Hv, static_cast<unsigned>(nc)), dim3(256), 0, s, a);
-  if (o_dtype == GDN_DTYPE_BF16)
-    hipLaunchKernelGGL((chunk_scan_kernel<SCAN_WAVES, true, SCAN_U_LDS>), dim3(static_cast<unsigned>(scan_blocks)),
-                       dim3(64 * SCAN_WAVES), 0, s, a);
-  else
-    hipLaunchKernelGGL((chunk_scan_kernel<SCAN_WAVES, false, SCAN_U_LDS>), dim3(static_cast<unsigned>(scan_blocks)),
-                       dim3(64 * SCAN_WAVES), 0, s, a);
+  // One prep + scan pair per segment of SEG_CHUNKS global chunks (at least one
+  // pair, so that empty sequences still pass their initial state through).
+  for (int64_t sb = 0; sb == 0 || sb < nc; sb += seg) {
+    a.seg_begin = static_cast<int>(sb);
+    a.seg_end = static_cast<int>(std::min<int64_t>(sb + seg, nc));
+    if (seg > 0) hipLaunchKernelGGL(chunk_prep_kernel, dim3(Hv, static_cast<unsigned>(seg)), dim3(256), 0, s, a);
+    if (o_dtype == GDN_DTYPE_BF16)
+      hipLaunchKernelGGL((chunk_scan_kernel<SCAN_WAVES, true, SCAN_U_LDS>), dim3(static_cast<unsigned>(scan_blocks)),
+                         dim3(64 * SCAN_WAVES), 0, s, a);
+    else
+      hipLaunchKernelGGL((chunk_scan_kernel<SCAN_WAVES, false, SCAN_U_LDS>), dim3(static_cast<unsigned>(scan_blocks)),
+                         dim3(64 * SCAN_WAVES), 0, s, a);
+  }
   return check_launch("gdn_chunk_fwd");
 }
