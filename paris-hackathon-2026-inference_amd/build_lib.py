@@ -40,6 +40,9 @@ COMMON_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the chunk kernels keep their fp32 state and
+    # results in the operand registers instead of copying them to and from AGPRs
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", INCLUDE,
     "-I", CSRC,
 ]

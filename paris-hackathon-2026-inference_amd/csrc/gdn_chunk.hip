@@ -124,7 +124,7 @@ struct ChunkArgs {
   int32_t *chunk_start;  // [n_seqs + 1]
   u32x4 *vh;             // [SEG][Hv][NB_VH][64]   -W, A, scalars
   u32x4 *kh;             // [SEG][Hk][NB_KH][64]   Q, K^T
-  float *Ut;             // [SEG][Hv][128][64]     U transposed, fp32
+  float *Ut;             // [SEG][Hv][8 x 4 blocks][64][4]  U, fp32
   float *carry;          // [n_seqs][Hv][128][128] state between segments
 };
 
@@ -422,6 +422,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
         ua_lo[s][e] = static_cast<__bf16>(tb - static_cast<float>(hu));
       }
     }
+    // U in scan operand order: 1 KiB block (column tile nb, row tile p),
+    // lane (g, c) holding rows 16p + 4g + 0..3 of column 16 nb + c
     float *Uout = a.Ut + ch * (DV * CK);
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) {
@@ -439,7 +441,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
         }
       }
       wacc[nb] = w;
-      *reinterpret_cast<f32x4 *>(Uout + row * CK + 16 * p + 4 * g4) = u;  // U^T[v][pos]
+      *reinterpret_cast<f32x4 *>(Uout + ((4 * nb + p) * 64 + lane) * 4) = u;
     }
   }
   __syncthreads();  // T no longer read: reuse lt as the -W staging tile [64][WS_LD] bf16
@@ -492,18 +494,16 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
 
 // ------------------------------------------------------------------ phase B
 // LDS stage: one chunk's scan operands for a workgroup of NW waves: the
-// v-head region, the k-head region, then (when U_LDS) U^T for the
-// workgroup's 16*NW columns, 4 blocks per wave.  Without U_LDS each wave
-// prefetches its own U^T rows into registers instead (keeps two stages of an
-// 8-wave workgroup within the 160 KiB of LDS).
+// v-head region, the k-head region, then U for the workgroup's 16*NW
+// columns, 4 blocks per wave.
 constexpr int ST_W = VH_W * 64;
 constexpr int ST_A = VH_A * 64;
 constexpr int ST_SC = VH_SC * 64;
 constexpr int ST_Q = (NB_VH + KH_Q) * 64;
 constexpr int ST_KT = (NB_VH + KH_KT) * 64;
 constexpr int ST_U = (NB_VH + NB_KH) * 64;
-template <int NW, bool U_LDS> struct Stage {
-  static constexpr int blocks = NB_VH + NB_KH + (U_LDS ? 4 * NW : 0);
+template <int NW> struct Stage {
+  static constexpr int blocks = NB_VH + NB_KH + 4 * NW;
   static constexpr int u4 = blocks * 64;  // size in 16-byte units
 };
 
@@ -511,164 +511,166 @@ constexpr int BUF_DWORD3 = 0x00020000;  // raw (untyped) buffer resource word 3 
 
 // Copies nb 1 KiB blocks of a region into LDS with buffer_load ... lds: a
 // uniform base (no per-lane 64-bit address math), 64 lanes x 16 bytes per
-// instruction, hardware bounds check against the region size.  Wave w
-// issues blocks w, w + NW, ...
+// instruction.  Wave w issues blocks w, w + NW, ...; a wave with no block
+// left in the last round copies the region's last block again (same bytes to
+// the same LDS address), which keeps the copy free of branches.
 template <int NW>
 __device__ __forceinline__ void copy_region(u32x4 *dst, const void *src, int nb, int wave, int lane) {
   const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(src), 0, nb * 1024, BUF_DWORD3);
 #pragma unroll
-  for (int i = 0; i < (NB_KH + NW - 1) / NW; ++i) {
-    const int t = i * NW + wave;
-    if (t < nb) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst + t * 64, 16, lane * 16, t * 1024, 0, 0);
+  for (int i = 0; i < (nb + NW - 1) / NW; ++i) {
+    const int t = min(i * NW + wave, nb - 1);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst + t * 64, 16, lane * 16, t * 1024, 0, 0);
   }
 }
 
-template <int NW, bool U_LDS>
-__device__ __forceinline__ void stage_load(u32x4 *st, const ChunkArgs &a, size_t ch, size_t chk, int col0,
-                                           int wave, int lane) {
+template <int NW>
+__device__ __forceinline__ void stage_load(u32x4 *st, const ChunkArgs &a, size_t ch, size_t chk, int ct, int wave,
+                                           int lane) {
   copy_region<NW>(st, a.vh + ch * (NB_VH * 64), NB_VH, wave, lane);
   copy_region<NW>(st + NB_VH * 64, a.kh + chk * (NB_KH * 64), NB_KH, wave, lane);
-  if constexpr (U_LDS) copy_region<NW>(st + ST_U, a.Ut + ch * (DV * CK) + col0 * CK, 4 * NW, wave, lane);
+  copy_region<NW>(st + ST_U, a.Ut + ch * (DV * CK) + ct * (NW * 4 * 256), 4 * NW, wave, lane);
 }
 
-// One chunk of the scan for this wave's 16 state columns.  Operand blocks are
-// read from LDS in batches of 8 (32 VGPRs), each issued while the MFMAs of the
-// previous batch run; the sched_barriers pin that order (left alone, the
-// compiler sinks every read next to its MFMA and exposes the LDS latency
-// once per MFMA, or hoists all reads and spills).
-#define GDN_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
-
-__device__ __forceinline__ void ld_batch(u32x4 (&r)[8], const u32x4 *st, int base, int lane) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) r[i] = st[base + i * 64 + lane];
-}
-
+// Output of one chunk: lane (g, c) holds rows 16p + 4g + e of its column.  The
+// buffer resource starts at the chunk's first token and ends after its last
+// valid row, so stores past the sequence end are dropped by the hardware
+// range check; voff[4p + e] is the byte offset of row 16p + 4g + e.
 template <bool BF16_OUT>
-__device__ __forceinline__ void scan_chunk(const u32x4 *st, const f32x4 (&u)[4], f32x4 (&S)[8], const ChunkArgs &a,
-                                           int64_t t0, int len, int h, int col, int lane) {
+__device__ __forceinline__ void store_chunk(const f32x4 (&o)[4], __amdgpu_buffer_rsrc_t r, const int (&voff)[16]) {
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (BF16_OUT)
+        __builtin_amdgcn_raw_buffer_store_b16(bf16_rne(o[p][e]), r, voff[4 * p + e], 0, 0);
+      else
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, o[p][e]), r, voff[4 * p + e], 0, 0);
+    }
+}
+
+// sched_group_barrier masks
+constexpr int SG_VALU = 0x2, SG_MFMA = 0x8, SG_VMEM_WR = 0x40, SG_DS_RD = 0x100;
+#define GDN_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
+#define GDN_GROUP(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
+
+// One chunk of the scan for this wave's 16 state columns, in three
+// scheduling regions.  The scan runs one wave per SIMD, so the vector ALU
+// work is interleaved with the MFMAs by hand (sched_group_barrier patterns):
+//   R1  V' = U - W S            16 MFMAs | S *= e^{gamma_63}, previous chunk's
+//                                          output stores; reads Q, scales
+//   R2  acc = Q S               16 MFMAs | V' to bf16, V'' = sk V' split hi + lo;
+//                                          reads A, K^T
+//   R3  S += K^T V'' (hi, lo)   32 MFMAs | O = sq acc, then O += A V' (6 MFMAs),
+//                                          next chunk's bf16 state operands
+// sb holds the state as bf16 B operands (k-steps over the 128 state rows);
+// on return it holds the updated state, o holds this chunk's output.
+template <bool BF16_OUT>
+__device__ __forceinline__ void scan_chunk(const u32x4 *st, int ubase, f32x4 (&S)[8], bf16x8 (&sb)[4], f32x4 (&o)[4],
+                                           __amdgpu_buffer_rsrc_t prev_out, const int (&voff)[16], int lane) {
   const int g4 = lane >> 4;
   const float *sc = reinterpret_cast<const float *>(st + ST_SC);
-  // Operand groups of 4 blocks, double-buffered in registers: group k+1 is
-  // read from LDS while the MFMAs of group k run.
-  //   groups 0-3: -W rows p=0..3    4-7: Q rows p=0..3    8: A blocks 0,2,4,5
-  //   9: A blocks 6,7               10-13: K^T tiles i=2m, 2m+1
-  u32x4 bufA[4], bufB[4];
-  auto ld4 = [&](u32x4 (&r)[4], int g) {
-    if (g < 4) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) r[i] = st[ST_W + (4 * g + i) * 64 + lane];
-    } else if (g < 8) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) r[i] = st[ST_Q + (4 * (g - 4) + i) * 64 + lane];
-    } else if (g == 8) {
-      r[0] = st[ST_A + 0 * 64 + lane];
-      r[1] = st[ST_A + 2 * 64 + lane];
-      r[2] = st[ST_A + 4 * 64 + lane];
-      r[3] = st[ST_A + 5 * 64 + lane];
-    } else if (g == 9) {
-      r[0] = st[ST_A + 6 * 64 + lane];
-      r[1] = st[ST_A + 7 * 64 + lane];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) r[i] = st[ST_KT + (4 * (g - 10) + i) * 64 + lane];
-    }
-  };
 
-  bf16x8 sb[4];  // state as bf16 B operands (k-steps over the 128 state rows)
-  f32x4 vp[4];   // V' = U - W S   (rows: chunk positions 16p + 4g + e)
-  f32x4 o[4];    // O = diag(e^gamma nq) (Q S) + A V'
-  bf16x8 vb[2], vh[2], vl[2];
-  float eL = 0.f;
-  auto compute = [&](const u32x4 (&r)[4], int g) {
-    if (g < 4) {
-      vp[g] = u[g];
+  // ---- R1
+  u32x4 wb[16];
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) vp[g] = mfma(as_bf16x8(r[s2]), sb[s2], vp[g]);
-    } else if (g < 8) {
-      const int p = g - 4;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < 16; ++i) wb[i] = st[ST_W + i * 64 + lane];
+  f32x4 vp[4];  // V' rows 16p + 4g + e
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) acc = mfma(as_bf16x8(r[s2]), sb[s2], acc);
-      o[p] = acc * *reinterpret_cast<const f32x4 *>(sc + 16 * p + 4 * g4);
-    } else if (g == 8) {
-      vb[0] = pack_hi(vp[0], vp[1]);
-      vb[1] = pack_hi(vp[2], vp[3]);
-      o[0] = mfma(as_bf16x8(r[0]), vb[0], o[0]);
-      o[1] = mfma(as_bf16x8(r[1]), vb[0], o[1]);
-      o[2] = mfma(as_bf16x8(r[2]), vb[0], o[2]);
-      o[2] = mfma(as_bf16x8(r[3]), vb[1], o[2]);
-    } else if (g == 9) {
-      o[3] = mfma(as_bf16x8(r[0]), vb[0], o[3]);
-      o[3] = mfma(as_bf16x8(r[1]), vb[1], o[3]);
+  for (int p = 0; p < 4; ++p) vp[p] = __builtin_bit_cast(f32x4, st[ubase + p * 64 + lane]);
+  const float eL = sc[2 * CK];
+  u32x4 qb[16];
 #pragma unroll
-      for (int p2 = 0; p2 < 2; ++p2) {  // V'' = diag(e^{gamma_63 - gamma} nk) V', hi + lo
-        const f32x4 ska = *reinterpret_cast<const f32x4 *>(sc + CK + 32 * p2 + 4 * g4);
-        const f32x4 skb = *reinterpret_cast<const f32x4 *>(sc + CK + 32 * p2 + 16 + 4 * g4);
-        pack_hilo(vp[2 * p2] * ska, vp[2 * p2 + 1] * skb, vh[p2], vl[p2]);
-      }
-      eL = sc[2 * CK];
-    } else {  // S <- e^{gamma_63} S + K^T V''   for tiles 2m, 2m+1
-      const int m = g - 10;
+  for (int i = 0; i < 16; ++i) qb[i] = st[ST_Q + i * 64 + lane];
+  f32x4 sk[4];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int i = 2 * m + t;
-        S[i] = S[i] * eL;
+  for (int p = 0; p < 4; ++p) sk[p] = *reinterpret_cast<const f32x4 *>(sc + CK + 16 * p + 4 * g4);
+  store_chunk<BF16_OUT>(o, prev_out, voff);
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          S[i] = mfma(as_bf16x8(r[2 * t + s2]), vh[s2], S[i]);
-          S[i] = mfma(as_bf16x8(r[2 * t + s2]), vl[s2], S[i]);
-        }
-      }
-    }
-  };
-
-  ld4(bufA, 0);
-  ld4(bufB, 1);
+  for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+    for (int p = 0; p < 4; ++p) vp[p] = mfma(as_bf16x8(wb[4 * p + s2]), sb[s2], vp[p]);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) S[i] = S[i] * eL;
+  GDN_GROUP(SG_DS_RD, 21);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    GDN_GROUP(SG_MFMA, 1);
+    GDN_GROUP(SG_DS_RD, 1);
+    GDN_GROUP(SG_VALU, 3);
+    GDN_GROUP(SG_VMEM_WR, 1);
+  }
   GDN_SCHED_FENCE();
+
+  // ---- R2
+  u32x4 ab[6], kb[16];  // A blocks 0, 2, 4, 5, 6, 7 (the others are zero); K^T tiles
+  ab[0] = st[ST_A + 0 * 64 + lane];
+  ab[1] = st[ST_A + 2 * 64 + lane];
+  ab[2] = st[ST_A + 4 * 64 + lane];
+  ab[3] = st[ST_A + 5 * 64 + lane];
+  ab[4] = st[ST_A + 6 * 64 + lane];
+  ab[5] = st[ST_A + 7 * 64 + lane];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) kb[i] = st[ST_KT + i * 64 + lane];
+  f32x4 sq[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) sq[p] = *reinterpret_cast<const f32x4 *>(sc + 16 * p + 4 * g4);
+  f32x4 acc[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) acc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+    for (int p = 0; p < 4; ++p) acc[p] = mfma(as_bf16x8(qb[4 * p + s2]), sb[s2], acc[p]);
+  bf16x8 vb[2], vh[2], vl[2];
+  vb[0] = pack_hi(vp[0], vp[1]);
+  vb[1] = pack_hi(vp[2], vp[3]);
+#pragma unroll
+  for (int p2 = 0; p2 < 2; ++p2)  // V'' = diag(e^{gamma_63 - gamma} nk) V', hi + lo
+    pack_hilo(vp[2 * p2] * sk[2 * p2], vp[2 * p2 + 1] * sk[2 * p2 + 1], vh[p2], vl[p2]);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    GDN_GROUP(SG_MFMA, 1);
+    GDN_GROUP(SG_DS_RD, 2);
+    GDN_GROUP(SG_VALU, 4);
+  }
+  GDN_SCHED_FENCE();
+
+  // ---- R3
+#pragma unroll
+  for (int half = 0; half < 2; ++half)
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) S[4 * half + t] = mfma(as_bf16x8(kb[2 * (4 * half + t) + s2]), vh[s2], S[4 * half + t]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) S[4 * half + t] = mfma(as_bf16x8(kb[2 * (4 * half + t) + s2]), vl[s2], S[4 * half + t]);
+    }
+#pragma unroll
+  for (int p = 0; p < 4; ++p) o[p] = acc[p] * sq[p];
+  o[0] = mfma(as_bf16x8(ab[0]), vb[0], o[0]);
+  o[1] = mfma(as_bf16x8(ab[1]), vb[0], o[1]);
+  o[2] = mfma(as_bf16x8(ab[2]), vb[0], o[2]);
+  o[3] = mfma(as_bf16x8(ab[4]), vb[0], o[3]);
+  o[2] = mfma(as_bf16x8(ab[3]), vb[1], o[2]);
+  o[3] = mfma(as_bf16x8(ab[5]), vb[1], o[3]);
 #pragma unroll
   for (int s2 = 0; s2 < 4; ++s2) sb[s2] = pack_hi(S[2 * s2], S[2 * s2 + 1]);
 #pragma unroll
-  for (int g = 0; g < 14; g += 2) {
-    compute(bufA, g);
-    GDN_SCHED_FENCE();
-    if (g + 2 < 14) ld4(bufA, g + 2);
-    GDN_SCHED_FENCE();
-    compute(bufB, g + 1);
-    GDN_SCHED_FENCE();
-    if (g + 3 < 14) ld4(bufB, g + 3);
-    GDN_SCHED_FENCE();
+  for (int i = 0; i < 38; ++i) {
+    GDN_GROUP(SG_MFMA, 1);
+    GDN_GROUP(SG_VALU, 1);
   }
-
-  // output rows 16p + 4g + e of column col (rows past the sequence are skipped)
-  const int64_t ostep = static_cast<int64_t>(a.Hv) * DV;
-  typedef typename std::conditional<BF16_OUT, uint16_t, float>::type OT;
-  OT *obase = static_cast<OT *>(a.o) + (t0 + 4 * g4) * ostep + (int64_t)h * DV + col;
-  if (len == CK) {
-#pragma unroll
-    for (int p = 0; p < 4; ++p)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        OT *dst = obase + (16 * p + e) * ostep;
-        if constexpr (BF16_OUT) *dst = bf16_rne(o[p][e]); else *dst = o[p][e];
-      }
-  } else {
-#pragma unroll
-    for (int p = 0; p < 4; ++p)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if (16 * p + 4 * g4 + e < len) {
-          OT *dst = obase + (16 * p + e) * ostep;
-          if constexpr (BF16_OUT) *dst = bf16_rne(o[p][e]); else *dst = o[p][e];
-        }
-      }
-  }
+  GDN_SCHED_FENCE();
 }
 
-// Workgroup = NW waves = 16*NW state columns of one (sequence, v-head).
-template <int NW, bool BF16_OUT, bool U_LDS>
-__global__ __launch_bounds__(64 * NW) void chunk_scan_kernel(ChunkArgs a) {
-  __shared__ u32x4 stage0[Stage<NW, U_LDS>::u4];
-  __shared__ u32x4 stage1[Stage<NW, U_LDS>::u4];
+// Workgroup = NW waves = 16*NW state columns of one (sequence, v-head).  The
+// two LDS stages leave room for one workgroup per CU, so each SIMD runs one
+// wave and may use the whole register file.
+template <int NW, bool BF16_OUT>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1))) void chunk_scan_kernel(ChunkArgs a) {
+  __shared__ u32x4 stage0[Stage<NW>::u4];
+  __shared__ u32x4 stage1[Stage<NW>::u4];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g4 = lane >> 4;
@@ -679,9 +681,8 @@ __global__ __launch_bounds__(64 * NW) void chunk_scan_kernel(ChunkArgs a) {
   const int n = rest / a.Hv;
   const int h = rest % a.Hv;
   const int hk = h / (a.Hv / a.Hk);
-  const int col0 = 16 * NW * ct;     // first column of the workgroup
-  const int ucol = 16 * wave + r16;  // this lane's column within the workgroup
-  const int col = col0 + ucol;
+  const int col = 16 * NW * ct + 16 * wave + r16;
+  const int ubase = ST_U + wave * 4 * 64;  // this wave's U blocks in a stage
 
   // Values read from memory are workgroup-uniform; readfirstlane tells the
   // compiler so (buffer resources built from them must live in SGPRs).
@@ -714,7 +715,7 @@ __global__ __launch_bounds__(64 * NW) void chunk_scan_kernel(ChunkArgs a) {
   }
   if (lo >= hi) return;  // no chunk of this sequence in this segment
   const int nch = hi - lo;
-  const int c0 = lo - a.seg_begin;             // first chunk, workspace-local
+  const int c0 = lo - a.seg_begin;                             // first chunk, workspace-local
   const int64_t seq_off = static_cast<int64_t>(lo - cs) * CK;  // its first token within the sequence
   float *carry = a.carry + (static_cast<int64_t>(n) * a.Hv + h) * kv + col;
 
@@ -729,42 +730,54 @@ __global__ __launch_bounds__(64 * NW) void chunk_scan_kernel(ChunkArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) S[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  bf16x8 sb[4];
+#pragma unroll
+  for (int s2 = 0; s2 < 4; ++s2) sb[s2] = pack_hi(S[2 * s2], S[2 * s2 + 1]);
 
-  f32x4 u0[4], u1[4];
-  auto load_stage = [&](u32x4 *st, f32x4 (&u)[4], int cidx) {
+  // Output addressing: byte offsets of rows 16p + 4g + e within a chunk.
+  typedef typename std::conditional<BF16_OUT, uint16_t, float>::type OT;
+  const int64_t ostep = static_cast<int64_t>(a.Hv) * DV;  // elements per token
+  int voff[16];
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      voff[4 * p + e] = static_cast<int>(((16 * p + 4 * g4 + e) * ostep + h * DV + col) * sizeof(OT));
+  auto out_rsrc = [&](int c) {  // chunk c of this launch: rows [0, min(64, rest of sequence))
+    const int64_t toff = seq_off + static_cast<int64_t>(c) * CK;
+    const int rows = static_cast<int>(min<int64_t>(CK, slen - toff));
+    OT *base = static_cast<OT *>(a.o) + (s0 + toff) * ostep;
+    return __builtin_amdgcn_make_buffer_rsrc(base, 0, static_cast<int>(rows * ostep * sizeof(OT)), BUF_DWORD3);
+  };
+  // Before the first chunk there is no output to store: a zero-sized range.
+  __amdgpu_buffer_rsrc_t prev = __builtin_amdgcn_make_buffer_rsrc(a.o, 0, 0, BUF_DWORD3);
+  f32x4 o[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) o[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto load_stage = [&](u32x4 *st, int cidx) {
     const size_t j = static_cast<size_t>(c0 + cidx);
-    const size_t ch = j * a.Hv + h;
-    stage_load<NW, U_LDS>(st, a, ch, j * a.Hk + hk, col0, wave, lane);
-    if constexpr (!U_LDS) {
-      const float *uc = a.Ut + ch * (DV * CK) + col * CK + 4 * g4;
-#pragma unroll
-      for (int p = 0; p < 4; ++p) u[p] = *reinterpret_cast<const f32x4 *>(uc + 16 * p);
-    }
+    stage_load<NW>(st, a, j * a.Hv + h, j * a.Hk + hk, ct, wave, lane);
   };
-  auto run_chunk = [&](const u32x4 *st, f32x4 (&u)[4], int c) {
-    if constexpr (U_LDS) {
-#pragma unroll
-      for (int p = 0; p < 4; ++p) u[p] = __builtin_bit_cast(f32x4, st[ST_U + ucol * 16 + 4 * p + g4]);
-    }
-    const int64_t toff = seq_off + static_cast<int64_t>(c) * CK;  // token offset within the sequence
-    scan_chunk<BF16_OUT>(st, u, S, a, s0 + toff, min<int64_t>(CK, slen - toff), h, col, lane);
-  };
-  if (nch > 0) {
-    load_stage(stage0, u0, 0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-  }
+  // A chunk's output is stored during the next chunk (vmcnt counts stores
+  // too, so the wait at the end of each chunk then finds them long done).
+  load_stage(stage0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
   for (int c = 0; c < nch; c += 2) {
-    if (c + 1 < nch) load_stage(stage1, u1, c + 1);
-    run_chunk(stage0, u0, c);
+    if (c + 1 < nch) load_stage(stage1, c + 1);
+    scan_chunk<BF16_OUT>(stage0, ubase, S, sb, o, prev, voff, lane);
+    prev = out_rsrc(c);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (c + 1 >= nch) break;
-    if (c + 2 < nch) load_stage(stage0, u0, c + 2);
-    run_chunk(stage1, u1, c + 1);
+    if (c + 2 < nch) load_stage(stage0, c + 2);
+    scan_chunk<BF16_OUT>(stage1, ubase, S, sb, o, prev, voff, lane);
+    prev = out_rsrc(c + 1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
+  store_chunk<BF16_OUT>(o, prev, voff);
 
   float *dst = hi == ce ? (out_row >= 0 ? a.hT + (out_row * a.Hv + h) * kv + col : nullptr) : carry;
   if (dst) {
@@ -776,11 +789,10 @@ __global__ __launch_bounds__(64 * NW) void chunk_scan_kernel(ChunkArgs a) {
 }
 
 // Scan workgroup shape (measured on MI355X at T=4096, 32 v-heads): 4 waves =
-// 64 state columns per workgroup, U^T staged through LDS.  With 8 waves per
-// workgroup every wave re-reads the whole operand stage from LDS and the LDS
-// bandwidth becomes the limit; with 2 the stage is streamed four times.
+// 64 state columns per workgroup.  With 8 waves per workgroup every wave
+// re-reads the whole operand stage from LDS and the LDS bandwidth becomes the
+// limit; with 2 the stage is streamed four times.
 constexpr int SCAN_WAVES = 4;
-constexpr bool SCAN_U_LDS = true;
 
 // Chunks per prep + scan segment: the operand workspace of one segment
 // (about 2.3 MiB per chunk at 32 v-heads) stays resident in the 256 MB
@@ -879,10 +891,10 @@ extern "C" int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qk
     a.seg_end = static_cast<int>(std::min<int64_t>(sb + seg, nc));
     if (seg > 0) hipLaunchKernelGGL(chunk_prep_kernel, dim3(Hv, static_cast<unsigned>(seg)), dim3(256), 0, s, a);
     if (o_dtype == GDN_DTYPE_BF16)
-      hipLaunchKernelGGL((chunk_scan_kernel<SCAN_WAVES, true, SCAN_U_LDS>), dim3(static_cast<unsigned>(scan_blocks)),
+      hipLaunchKernelGGL((chunk_scan_kernel<SCAN_WAVES, true>), dim3(static_cast<unsigned>(scan_blocks)),
                          dim3(64 * SCAN_WAVES), 0, s, a);
     else
-      hipLaunchKernelGGL((chunk_scan_kernel<SCAN_WAVES, false, SCAN_U_LDS>), dim3(static_cast<unsigned>(scan_blocks)),
+      hipLaunchKernelGGL((chunk_scan_kernel<SCAN_WAVES, false>), dim3(static_cast<unsigned>(scan_blocks)),
                          dim3(64 * SCAN_WAVES), 0, s, a);
   }
   return check_launch("gdn_chunk_fwd");
