@@ -157,33 +157,80 @@ __global__ __launch_bounds__(256) void chunk_table_kernel(ChunkArgs a) {
 }
 
 // ------------------------------------------------------------------ phase A
-constexpr int LT_LD = CK + 4;    // fp32 row stride of L / T (16-byte aligned rows)
-constexpr int WS_LD = DK + 8;    // bf16 row stride of the -W staging tile (same bytes as L / T)
-static_assert(CK * LT_LD * 4 == CK * WS_LD * 2, "W staging reuses the L/T buffer");
+// One workgroup of 4 waves per (chunk, v-head); wave p owns chunk rows
+// 16p..16p+15.  Fragment layouts used below (lane = 16 g + r, r < 16):
+//   pi fragment of X (bf16 MFMA operand, k-step s):  lane holds row r of the
+//     tile, columns 32s + 4g + 0..3 and 32s + 16 + 4g + 0..3;
+//   row layout (16x16 fp32 block):  lane holds X[r][4g + e], e < 4;
+//   D layout (16x16 fp32 block):    lane holds X[4g + e][r] (an MFMA result).
 
-// Transposed [128][64] bf16 tiles (K^T, V^T): 16-byte segment seg of row r is
-// stored at segment seg ^ f(r), f(r) = ((r >> 1) ^ (r >> 3)) & 7.  With this
-// swizzle the MFMA operand reads (16 consecutive rows, one segment) touch
-// distinct banks, and the transposing 2-byte writes (rows 8 apart, one
-// column) collide at most 2-way.
-__device__ __forceinline__ int tsw(int row, int col) {
-  return row * CK + ((((col >> 3) ^ (row >> 1) ^ (row >> 3)) & 7) << 3) + (col & 7);
-}
-
-// Row-major [64][128] bf16 K tile: 16-byte segment seg of row r at seg ^ (r & 15).
+// Row-major [64][128] bf16 tile (K or V): 16-byte segment seg of row r is
+// stored at segment seg ^ (r & 15).  Row writes, pi-fragment reads and the
+// transposing reads below are all free of bank conflicts with it.
 __device__ __forceinline__ int nsw(int row, int col) {
   return row * DK + ((((col >> 3) ^ row) & 15) << 3) + (col & 7);
 }
-constexpr int AS_LD = CK + 8;  // bf16 row stride of the A staging tile
+
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives 16-bit
+// element (i % 4) of the 8 bytes addressed by source lanes 4k + i / 4 of the
+// group, k = 0..3.  With source lane L pointing at X[j0 + L/4][n0 + 4 (L%4)],
+// lane i therefore holds X[j0 + k][n0 + i]: four consecutive rows of column
+// n0 + i, which is the MFMA operand layout of X^T.
+__device__ __forceinline__ s16x4 ld_tr(const uint16_t *tile, int j0, int n0, int lane) {
+  const int L = lane & 15;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_s16x4 *)(const_cast<uint16_t *>(tile) + nsw(j0 + (L >> 2), n0 + 4 * (L & 3))));
+}
+// Pi fragment of X^T for k-step s over the rows of X and columns n0..n0+15.
+__device__ __forceinline__ bf16x8 frag_tr(const uint16_t *tile, int s, int n0, int lane) {
+  const int g4 = lane >> 4;
+  const s16x4 lo = ld_tr(tile, 32 * s + 4 * g4, n0, lane);
+  const s16x4 hi = ld_tr(tile, 32 * s + 16 + 4 * g4, n0, lane);
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+// Pi fragment of rows row0..row0+15 of X, k-step s.
+__device__ __forceinline__ bf16x8 frag_pi(const uint16_t *tile, int row0, int s, int lane) {
+  const int r = row0 + (lane & 15), g4 = lane >> 4;
+  const u32x2 a = *reinterpret_cast<const u32x2 *>(tile + nsw(r, 32 * s + 4 * g4));
+  const u32x2 b = *reinterpret_cast<const u32x2 *>(tile + nsw(r, 32 * s + 16 + 4 * g4));
+  return as_bf16x8(u32x4{a.x, a.y, b.x, b.y});
+}
+
+// 16x16x16 fp32 product on MFMA (v_mfma_f32_16x16x4_f32: lane (r, g) gives
+// A[r][g] and B[g][r]).  With X in row layout and Y in D layout, call kc
+// reduces over the indices 4g + kc, so mm16(X, Y) is X Y in D layout, and
+// mm16(Y, X) (arguments swapped) is the same product in row layout.
+__device__ __forceinline__ f32x4 mm16(f32x4 a, f32x4 b, f32x4 acc) {
+#pragma unroll
+  for (int kc = 0; kc < 4; ++kc) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[kc], b[kc], acc, 0, 0, 0);
+  return acc;
+}
+
+// Sum over the 16 lanes of a DPP row (every lane receives the sum).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_mov<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_mov<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp_mov<0x141>(x);  // row_half_mirror
+  x += dpp_mov<0x140>(x);  // row_mirror
+  return x;
+}
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
 __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
-  __shared__ __align__(16) uint16_t kn_s[CK * DK];   // K rows (MFMA operands of K K^T, Q K^T)
-  __shared__ __align__(16) uint16_t kt_s[DK * CK];   // K^T (B operand of W, scan operand blocks)
-  __shared__ __align__(16) uint16_t vt_s[DV * CK];   // V^T (B operand of U)
-  __shared__ __align__(16) float lt[CK * LT_LD];      // L, then T in place, then -W staging
-  __shared__ __align__(16) uint16_t as_s[CK * AS_LD]; // A staging
-  __shared__ __align__(16) float xs[3][16][17];
-  __shared__ float gam_s[CK], beta_s[CK], nk_s[CK], nq_s[CK], colw_s[CK];
+  __shared__ __align__(16) uint16_t kn[CK * DK];  // K rows (swizzled)
+  __shared__ __align__(16) uint16_t vn[CK * DV];  // V rows (swizzled)
+  __shared__ __align__(16) f32x4 lbuf[4 * 64];    // diagonal blocks of L, row layout by lane
+  __shared__ __align__(16) f32x4 dxch[4 * 64];    // diagonal blocks of T, D layout by lane
+  __shared__ __align__(16) f32x4 txch[3 * 64];    // T[1][0], T[2][1], T[2][0], D layout by lane
+  __shared__ __align__(16) float dtr[4][16 * 20];  // D layout -> row layout transposes
+  __shared__ __align__(16) float gam_s[CK], beta_s[CK], nk_s[CK], nq_s[CK], colw_s[CK];
 
   const int h = blockIdx.x;
   const int j = a.seg_begin + static_cast<int>(blockIdx.y);  // global chunk index
@@ -207,69 +254,75 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int p = tid >> 6;  // this wave's row block
   const int g4 = lane >> 4;
   const int r16 = lane & 15;
   const int jl = static_cast<int>(blockIdx.y);  // chunk index within the segment's workspace
   const size_t ch = static_cast<size_t>(jl) * a.Hv + h;
   const size_t chk = static_cast<size_t>(jl) * a.Hk + hk;
-  const int p = wave;  // row block of K K^T / Q K^T / W / U owned by this wave
+  const int irow = 16 * p + r16;  // this lane's chunk row in row-layout / pi fragments
 
-  // ---- issue every global load up front
+  // ---- global loads: K, V rows (16 bytes per thread), this wave's Q rows as
+  // pi fragments, and the gates
   const int seg = tid & 15;
-  u32x4 ku[4], qu[4], vu[4];
+  u32x4 ku[4], vu[4];
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int row = (tid >> 4) + 16 * it;
     const int64_t tok = t0 + row;
     const u32x4 z = {0u, 0u, 0u, 0u};
     ku[it] = row < len ? *reinterpret_cast<const u32x4 *>(a.k + tok * a.ks + (int64_t)hk * DK + seg * 8) : z;
-    qu[it] = row < len ? *reinterpret_cast<const u32x4 *>(a.q + tok * a.qs + (int64_t)hk * DK + seg * 8) : z;
     vu[it] = row < len ? *reinterpret_cast<const u32x4 *>(a.v + tok * a.vs + (int64_t)h * DV + seg * 8) : z;
   }
-  bf16x8 aq[4];  // Q rows of block p (A operands of Q K^T)
+  bf16x8 qf[4];
   {
-    const int row = 16 * p + r16;
-    const uint16_t *qrow = a.q + (t0 + row) * a.qs + (int64_t)hk * DK + 8 * g4;
+    const uint16_t *qrow = a.q + (t0 + irow) * a.qs + (int64_t)hk * DK + 4 * g4;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) aq[s] = row < len ? ld8(qrow + 32 * s) : zero8();
+    for (int s = 0; s < 4; ++s) {
+      u32x2 x0 = {0u, 0u}, x1 = {0u, 0u};
+      if (irow < len) {
+        x0 = *reinterpret_cast<const u32x2 *>(qrow + 32 * s);
+        x1 = *reinterpret_cast<const u32x2 *>(qrow + 32 * s + 16);
+      }
+      qf[s] = as_bf16x8(u32x4{x0.x, x0.y, x1.x, x1.y});
+    }
   }
   float gv = 0.f, bv = 0.f;
-  if (wave == 0 && lane < len) {
+  if (p == 0 && lane < len) {
     gv = a.g[(t0 + lane) * a.Hv + h];
     bv = load_elem(a.beta, (t0 + lane) * a.Hv + h, a.beta_dt);
   }
 
-  // ---- A.1: K (rows and transposed), V^T into LDS; row norms; chunk-local cumsum of g
+  // ---- A.1: K, V rows into LDS; K row norms; chunk-local cumsum of g; Q row norms
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int row = (tid >> 4) + 16 * it;
-    *reinterpret_cast<u32x4 *>(kn_s + nsw(row, seg * 8)) = ku[it];
-    float sk = 0.f, sq = 0.f;
+    *reinterpret_cast<u32x4 *>(kn + nsw(row, seg * 8)) = ku[it];
+    *reinterpret_cast<u32x4 *>(vn + nsw(row, seg * 8)) = vu[it];
+    float sk = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const uint32_t kw = ku[it][e], qw = qu[it][e], vw = vu[it][e];
+      const uint32_t kw = ku[it][e];
       const float k0 = bf16_bits_to_f32(kw & 0xffffu), k1 = bf16_bits_to_f32(kw >> 16);
-      const float q0 = bf16_bits_to_f32(qw & 0xffffu), q1 = bf16_bits_to_f32(qw >> 16);
       sk += k0 * k0 + k1 * k1;
-      sq += q0 * q0 + q1 * q1;
-      const int d0 = seg * 8 + 2 * e;
-      kt_s[tsw(d0, row)] = static_cast<uint16_t>(kw & 0xffffu);
-      kt_s[tsw(d0 + 1, row)] = static_cast<uint16_t>(kw >> 16);
-      vt_s[tsw(d0, row)] = static_cast<uint16_t>(vw & 0xffffu);
-      vt_s[tsw(d0 + 1, row)] = static_cast<uint16_t>(vw >> 16);
     }
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) {
-      sk += __shfl_xor(sk, m, 64);
-      sq += __shfl_xor(sq, m, 64);
-    }
-    if (seg == 0) {
-      nk_s[row] = a.l2norm ? rsqrtf(sk + 1e-6f) : 1.f;
-      nq_s[row] = (a.l2norm ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
-    }
+    sk = row16_sum(sk);
+    if (seg == 0) nk_s[row] = a.l2norm ? rsqrtf(sk + 1e-6f) : 1.f;
   }
-  if (wave == 0) {
+  {
+    float sq = 0.f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = static_cast<float>(qf[s][e]);
+        sq += x * x;
+      }
+    sq += __shfl_xor(sq, 16, 64);
+    sq += __shfl_xor(sq, 32, 64);
+    if (g4 == 0) nq_s[irow] = (a.l2norm ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
+  }
+  if (p == 0) {
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const float x = __shfl_up(gv, off, 64);
@@ -278,218 +331,173 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
     gam_s[lane] = gv;
     beta_s[lane] = bv;
   }
-  // Q operand blocks for the scan (pi order), straight from the loaded rows
+  // the scan's Q operand blocks are this wave's pi fragments
   if (khead_writer) {
     u32x4 *qop = a.kh + chk * (NB_KH * 64) + KH_Q * 64;
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int row = (tid >> 4) + 16 * it;
-      const int s = seg >> 2, m = seg & 3;       // columns 32 s + 8 m .. +8
-      const int blk = (row >> 4) * 4 + s;
-      const int half = m >> 1;                   // slots 0-3 or 4-7
-      const int gA = 2 * (m & 1);                // lane group of columns +0..3; +4..7 -> gA + 1
-      u32x2 *base = reinterpret_cast<u32x2 *>(qop + blk * 64);
-      base[2 * ((row & 15) + 16 * gA) + half] = u32x2{qu[it][0], qu[it][1]};
-      base[2 * ((row & 15) + 16 * (gA + 1)) + half] = u32x2{qu[it][2], qu[it][3]};
-    }
+    for (int s = 0; s < 4; ++s) qop[(4 * p + s) * 64 + lane] = __builtin_bit_cast(u32x4, qf[s]);
   }
   __syncthreads();
 
-  // ---- A.2: K K^T -> L (fp32, LDS), Q K^T -> A (bf16, LDS staging)
-  if (wave == 0) colw_s[lane] = beta_s[lane] * expf(gam_s[lane]) * nk_s[lane];  // W's column scale
-  {
-    bf16x8 ak[4];
+  // Per-position scalars: the scan's output / state-increment scales, and W's column scale.
+  if (p == 0) {
+    float *sc = reinterpret_cast<float *>(a.vh + ch * (NB_VH * 64) + VH_SC * 64);
+    const float gl = gam_s[CK - 1], gm = gam_s[lane];
+    sc[lane] = fast_exp(gm) * nq_s[lane];
+    sc[CK + lane] = fast_exp(gl - gm) * nk_s[lane];
+    if (lane == 0) sc[2 * CK] = fast_exp(gl);
+    colw_s[lane] = beta_s[lane] * fast_exp(gm) * nk_s[lane];
+  }
+
+  // ---- A.2: tiles (cb, p), cb <= p, of K K^T and K Q^T.  The MFMA result
+  // lane holds (K_cb K_p^T)[4g + e][r] = k_j . k_i with i = 16p + r (this
+  // lane's row) and j = 16cb + 4g + e: L and A come out in row layout.
+  const float gi = gam_s[irow], bi = beta_s[irow], nki = nk_s[irow], nqi = nq_s[irow];
+  // (register arrays are only indexed by unrolled loop counters; the wave's
+  // own block is selected with uniform branches)
+  bf16x8 kown[4];  // pi fragments of this wave's K rows
 #pragma unroll
-    for (int s = 0; s < 4; ++s) ak[s] = ld8(kn_s + nsw(16 * p + r16, 32 * s + 8 * g4));
-    float gi[4], ni[4], qi[4], bi[4];
+  for (int s = 0; s < 4; ++s) kown[s] = frag_pi(kn, 16 * p, s, lane);
+  f32x4 lf[4], af[4];  // L and A blocks (p, cb), row layout
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int ii = 16 * p + 4 * g4 + e;
-      gi[e] = gam_s[ii];
-      ni[e] = nk_s[ii];
-      qi[e] = nq_s[ii];
-      bi[e] = beta_s[ii];
-    }
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
+  for (int cb = 0; cb < 4; ++cb) {
+    lf[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    af[cb] = lf[cb];
+    if (cb <= p) {
       f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = kk;
-      if (cb <= p) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const bf16x8 bk = ld8(kn_s + nsw(16 * cb + r16, 32 * s + 8 * g4));
-          kk = mfma(ak[s], bk, kk);
-          qk = mfma(aq[s], bk, qk);
-        }
+      for (int s = 0; s < 4; ++s) {
+        const bf16x8 kcb = frag_pi(kn, 16 * cb, s, lane);
+        kk = mfma(kcb, kown[s], kk);
+        qk = mfma(kcb, qf[s], qk);
       }
-      const int jj = 16 * cb + r16;
-      const float gj = gam_s[jj], nj = nk_s[jj];
+      const f32x4 gj = *reinterpret_cast<const f32x4 *>(gam_s + 16 * cb + 4 * g4);
+      const f32x4 nj = *reinterpret_cast<const f32x4 *>(nk_s + 16 * cb + 4 * g4);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int ii = 16 * p + 4 * g4 + e;
-        float lval = 0.f, aval = 0.f;
-        if (cb <= p && ii >= jj) {
-          const float dec = expf(gi[e] - gj);
-          aval = qi[e] * nj * qk[e] * dec;
-          if (ii > jj) lval = bi[e] * ni[e] * nj * kk[e] * dec;
-        }
-        lt[ii * LT_LD + jj] = lval;
-        as_s[ii * AS_LD + jj] = bf16_rne(aval);
+        const int jj = 16 * cb + 4 * g4 + e;
+        const float dec = jj <= irow ? fast_exp(gi - gj[e]) : 0.f;
+        af[cb][e] = nqi * nj[e] * qk[e] * dec;
+        lf[cb][e] = jj < irow ? bi * nki * nj[e] * kk[e] * dec : 0.f;
       }
     }
   }
-  __syncthreads();
-  {  // A operand blocks (pi order) -> global: blocks 0, 2, 4, 5, 6, 7 of [p][s]
+  {  // the scan's A operand blocks (p, s) = A tiles 2s, 2s + 1 (zero past the diagonal)
     u32x4 *aop = a.vh + ch * (NB_VH * 64) + VH_A * 64;
-    for (int e = tid; e < 6 * 64; e += 256) {
-      const int id = e >> 6, l = e & 63;
-      const int blk = id == 0 ? 0 : (id == 1 ? 2 : id + 2);  // ids 0..5 -> blocks 0, 2, 4, 5, 6, 7
-      const int bp = blk >> 1, bs = blk & 1;
-      const uint16_t *src = as_s + (16 * bp + (l & 15)) * AS_LD + 32 * bs + 4 * (l >> 4);
-      const u32x2 x0 = *reinterpret_cast<const u32x2 *>(src);
-      const u32x2 x1 = *reinterpret_cast<const u32x2 *>(src + 16);
-      aop[blk * 64 + l] = u32x4{x0.x, x0.y, x1.x, x1.y};
-    }
+    aop[(2 * p) * 64 + lane] = __builtin_bit_cast(u32x4, pack_hi(af[0], af[1]));
+    if (p >= 2) aop[(2 * p + 1) * 64 + lane] = __builtin_bit_cast(u32x4, pack_hi(af[2], af[3]));
   }
 
-  // ---- A.3: T = (I + L)^-1 in place (16x16 diagonal blocks by substitution)
+  // ---- A.3: T = (I + L)^-1.  Diagonal blocks by substitution (each lane one
+  // column, rows of L broadcast from LDS), then the blocks below the diagonal
+  // on fp32 MFMA: T[p][b] = -T[p][p] sum_{b <= kb < p} L[p][kb] T[kb][b].
+  f32x4 dl, drow;  // T[p][p] in D layout and row layout
   {
+    f32x4 *lb = lbuf + p * 64;
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+      if (cb == p) lb[lane] = lf[cb];
+    __builtin_amdgcn_wave_barrier();
     float x[16];
-    const int b = tid >> 4, cc = tid & 15;
-    if (tid < 64) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) x[i] = (i == cc) ? 1.f : 0.f;
-      const float *lb = lt + (16 * b) * LT_LD + 16 * b;
+    for (int i = 0; i < 16; ++i) {
+      float acc = i == r16 ? 1.f : 0.f;
 #pragma unroll
-      for (int i = 1; i < 16; ++i) {
-        if (i > cc) {
-          float sacc = 0.f;
+      for (int q4 = 0; q4 < 4; ++q4)
+        if (4 * q4 < i) {
+          const f32x4 lrow = lb[i + 16 * q4];  // L[i][4 q4 .. 4 q4 + 3]
 #pragma unroll
-          for (int jx = 0; jx < i; ++jx) sacc += lb[i * LT_LD + jx] * x[jx];
-          x[i] = -sacc;
+          for (int e = 0; e < 4; ++e)
+            if (4 * q4 + e < i) acc -= lrow[e] * x[4 * q4 + e];
         }
-      }
+      x[i] = acc;
     }
-    __syncthreads();
-    if (tid < 64) {
-      float *tb = lt + (16 * b) * LT_LD + 16 * b;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) tb[i * LT_LD + cc] = x[i];
-    }
-    __syncthreads();
-  }
-  for (int ab = 1; ab < 4; ++ab) {
-    for (int e = tid; e < ab * 256; e += 256) {  // X_b = sum_{kb=b}^{ab-1} L[ab][kb] T[kb][b]
-      const int b = e >> 8, r = (e >> 4) & 15, cc = e & 15;
-      float sacc = 0.f;
-      for (int kb = b; kb < ab; ++kb) {
-        const float *lrow = lt + (16 * ab + r) * LT_LD + 16 * kb;
-        const float *tcol = lt + (16 * kb) * LT_LD + 16 * b + cc;
+    for (int e = 0; e < 4; ++e)
+      dl[e] = g4 == 0 ? x[e] : g4 == 1 ? x[4 + e] : g4 == 2 ? x[8 + e] : x[12 + e];
+    dxch[p * 64 + lane] = dl;
+    float *tr = dtr[p];
 #pragma unroll
-        for (int qx = 0; qx < 16; ++qx) sacc += lrow[qx] * tcol[qx * LT_LD];
-      }
-      xs[b][r][cc] = sacc;
-    }
-    __syncthreads();
-    for (int e = tid; e < ab * 256; e += 256) {  // T[ab][b] = -T[ab][ab] X_b
-      const int b = e >> 8, r = (e >> 4) & 15, cc = e & 15;
-      const float *trow = lt + (16 * ab + r) * LT_LD + 16 * ab;
-      float sacc = 0.f;
-#pragma unroll
-      for (int qx = 0; qx < 16; ++qx) sacc += trow[qx] * xs[b][qx][cc];
-      lt[(16 * ab + r) * LT_LD + 16 * b + cc] = -sacc;
-    }
-    __syncthreads();
-  }
-
-  // ---- A.4: W = T diag(beta e^gamma nk) K,  U = T diag(beta) V  (T split hi + lo)
-  f32x4 wacc[8];
-  {
-    const int nsteps = p >= 2 ? 2 : 1;  // T is lower triangular
-    bf16x8 wa_hi[2], wa_lo[2], ua_hi[2], ua_lo[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const float *trow = lt + (16 * p + r16) * LT_LD + 32 * s + 8 * g4;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int col = 32 * s + 8 * g4 + e;
-        const float t = s < nsteps ? trow[e] : 0.f;
-        const float tb = t * beta_s[col];
-        const float tw = t * colw_s[col];
-        const __bf16 hw = static_cast<__bf16>(tw), hu = static_cast<__bf16>(tb);
-        wa_hi[s][e] = hw;
-        wa_lo[s][e] = static_cast<__bf16>(tw - static_cast<float>(hw));
-        ua_hi[s][e] = hu;
-        ua_lo[s][e] = static_cast<__bf16>(tb - static_cast<float>(hu));
-      }
-    }
-    // U in scan operand order: 1 KiB block (column tile nb, row tile p),
-    // lane (g, c) holding rows 16p + 4g + 0..3 of column 16 nb + c
-    float *Uout = a.Ut + ch * (DV * CK);
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      f32x4 w = {0.f, 0.f, 0.f, 0.f}, u = w;
-      const int row = 16 * nb + r16;
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        if (s < nsteps) {
-          const bf16x8 bk2 = ld8(kt_s + tsw(row, 32 * s + 8 * g4));
-          const bf16x8 bv2 = ld8(vt_s + tsw(row, 32 * s + 8 * g4));
-          w = mfma(wa_hi[s], bk2, w);
-          w = mfma(wa_lo[s], bk2, w);
-          u = mfma(ua_hi[s], bv2, u);
-          u = mfma(ua_lo[s], bv2, u);
-        }
-      }
-      wacc[nb] = w;
-      *reinterpret_cast<f32x4 *>(Uout + ((4 * nb + p) * 64 + lane) * 4) = u;
-    }
-  }
-  __syncthreads();  // T no longer read: reuse lt as the -W staging tile [64][WS_LD] bf16
-  {
-    uint16_t *ws = reinterpret_cast<uint16_t *>(lt);
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ws[(16 * p + 4 * g4 + e) * WS_LD + 16 * nb + r16] = f32_to_bf16_bits(-wacc[nb][e]);
+    for (int e = 0; e < 4; ++e) tr[(4 * g4 + e) * 20 + r16] = dl[e];
+    __builtin_amdgcn_wave_barrier();
+    drow = *reinterpret_cast<const f32x4 *>(tr + r16 * 20 + 4 * g4);
   }
   __syncthreads();
-
-  // ---- A.5: operand blocks (-W, K^T) and per-position scalars
-  {
-    const uint16_t *ws = reinterpret_cast<const uint16_t *>(lt);
-    u32x4 *wop = a.vh + ch * (NB_VH * 64) + VH_W * 64;
+  f32x4 trow[4];  // T[p][b], row layout
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int e = tid + 256 * it;          // block e/64, lane e%64
-      const int blk = e >> 6, l = e & 63;
-      const int bp = blk >> 2, bs = blk & 3;
-      const uint16_t *src = ws + (16 * bp + (l & 15)) * WS_LD + 32 * bs + 4 * (l >> 4);
-      const u32x2 x0 = *reinterpret_cast<const u32x2 *>(src);
-      const u32x2 x1 = *reinterpret_cast<const u32x2 *>(src + 16);
-      wop[e] = u32x4{x0.x, x0.y, x1.x, x1.y};
+  for (int b = 0; b < 4; ++b) trow[b] = b == p ? drow : z4;
+  // round 1: T[p][p-1] = -T[p][p] L[p][p-1] T[p-1][p-1]
+#pragma unroll
+  for (int b = 0; b < 3; ++b)
+    if (b == p - 1) {
+      const f32x4 x = mm16(lf[b], dxch[b * 64 + lane], z4);
+      trow[b] = -mm16(x, drow, z4);
+      if (b <= 1) txch[b * 64 + lane] = -mm16(drow, x, z4);  // T[1][0], T[2][1]
     }
-    if (khead_writer) {
-      u32x4 *kop = a.kh + chk * (NB_KH * 64) + KH_KT * 64;
+  __syncthreads();
+  // round 2: T[p][p-2] = -T[p][p] (L[p][p-2] T[p-2][p-2] + L[p][p-1] T[p-1][p-2])
 #pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int e = tid + 256 * it;
-        const int blk = e >> 6, l = e & 63;
-        const int bi = blk >> 1, bs = blk & 1;
-        const int row = 16 * bi + (l & 15);
-        const int col = 32 * bs + 4 * (l >> 4);
-        const u32x2 x0 = *reinterpret_cast<const u32x2 *>(kt_s + tsw(row, col));
-        const u32x2 x1 = *reinterpret_cast<const u32x2 *>(kt_s + tsw(row, col + 16));
-        kop[e] = u32x4{x0.x, x0.y, x1.x, x1.y};
+  for (int b = 0; b < 2; ++b)
+    if (b == p - 2) {
+      f32x4 x = mm16(lf[b], dxch[b * 64 + lane], z4);
+      x = mm16(lf[b + 1], txch[b * 64 + lane], x);  // T[b+1][b]: T[1][0] or T[2][1]
+      trow[b] = -mm16(x, drow, z4);
+      if (b == 0) txch[2 * 64 + lane] = -mm16(drow, x, z4);  // T[2][0]
+    }
+  __syncthreads();
+  if (p == 3) {  // round 3: T[3][0]
+    f32x4 x = mm16(lf[0], dxch[lane], z4);
+    x = mm16(lf[1], txch[lane], x);           // T[1][0]
+    x = mm16(lf[2], txch[2 * 64 + lane], x);  // T[2][0]
+    trow[0] = -mm16(x, drow, z4);
+  }
+
+  // ---- A.4: W^T = K^T (T diag(colw))^T and U = T diag(beta) V on bf16 MFMA,
+  // with the T factors split into bf16 hi + lo.  Reduction over chunk
+  // positions in pi order: k-step s covers T blocks 2s and 2s + 1.
+  f32x4 wt[8], ut[8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) {
+    wt[nb] = z4;
+    ut[nb] = z4;
+  }
+  const int nsteps = p >= 2 ? 2 : 1;  // T is lower triangular
+  const bool kt_writer = khead_writer && p >= 2;
+  u32x4 *kop = a.kh + chk * (NB_KH * 64) + KH_KT * 64;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    if (s < nsteps) {
+      const f32x4 cw0 = *reinterpret_cast<const f32x4 *>(colw_s + 32 * s + 4 * g4);
+      const f32x4 cw1 = *reinterpret_cast<const f32x4 *>(colw_s + 32 * s + 16 + 4 * g4);
+      const f32x4 be0 = *reinterpret_cast<const f32x4 *>(beta_s + 32 * s + 4 * g4);
+      const f32x4 be1 = *reinterpret_cast<const f32x4 *>(beta_s + 32 * s + 16 + 4 * g4);
+      bf16x8 whi, wlo, uhi, ulo;
+      pack_hilo(trow[2 * s] * cw0, trow[2 * s + 1] * cw1, whi, wlo);
+      pack_hilo(trow[2 * s] * be0, trow[2 * s + 1] * be1, uhi, ulo);
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) {
+        const bf16x8 kt = frag_tr(kn, s, 16 * nb, lane);
+        const bf16x8 vf = frag_tr(vn, s, 16 * nb, lane);
+        wt[nb] = mfma(kt, whi, wt[nb]);
+        wt[nb] = mfma(kt, wlo, wt[nb]);
+        ut[nb] = mfma(uhi, vf, ut[nb]);
+        ut[nb] = mfma(ulo, vf, ut[nb]);
+        // the scan's K^T operand blocks (i, s) are these fragments: waves 2
+        // and 3 (which read both k-steps) write tiles 0-3 and 4-7
+        if (kt_writer && (nb >> 2) == p - 2) kop[(2 * nb + s) * 64 + lane] = __builtin_bit_cast(u32x4, kt);
       }
     }
-    if (tid < CK) {
-      float *sc = reinterpret_cast<float *>(a.vh + ch * (NB_VH * 64) + VH_SC * 64);
-      const float gl = gam_s[CK - 1];
-      sc[tid] = expf(gam_s[tid]) * nq_s[tid];
-      sc[CK + tid] = expf(gl - gam_s[tid]) * nk_s[tid];
-      if (tid == 0) sc[2 * CK] = expf(gl);
-    }
   }
+
+  // ---- A.5: outputs.  -W blocks (p, s) = W^T tiles 2s, 2s + 1; U blocks in
+  // the scan's lane order (column tile nb, row tile p).
+  u32x4 *wop = a.vh + ch * (NB_VH * 64) + VH_W * 64;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) wop[(4 * p + s) * 64 + lane] = __builtin_bit_cast(u32x4, pack_hi(-wt[2 * s], -wt[2 * s + 1]));
+  float *Uout = a.Ut + ch * (DV * CK);
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) *reinterpret_cast<f32x4 *>(Uout + ((4 * nb + p) * 64 + lane) * 4) = ut[nb];
 }
 
 // ------------------------------------------------------------------ phase B
