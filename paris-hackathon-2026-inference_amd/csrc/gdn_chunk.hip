@@ -32,6 +32,7 @@
 // indices {4g..4g+3, 16+4g..16+4g+3} ("pi" order); the scan's A-operand
 // blocks are stored in the same order, so no accumulator goes through LDS.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "gdn_common.h"
@@ -802,30 +803,46 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 // limit; with 2 the stage is streamed four times.
 constexpr int SCAN_WAVES = 4;
 
-// Chunks per prep + scan segment: the operand workspace of one segment
-// (about 2.3 MiB per chunk at 32 v-heads) stays resident in the 256 MB
-// Infinity Cache between the producer and the consumer launch.
-constexpr int SEG_CHUNKS = 16;
+// Chunks per prep + scan segment.  One segment's operand workspace (about
+// 2.3 MiB per chunk at 32 v-heads, so ~150 MB) stays resident in the 256 MB
+// Infinity Cache between the producer and the consumer.  Longer inputs run as
+// several segments with the next segment's prep on a side stream; a
+// cross-stream hand-off costs ~10 us on MI355X, so segments are kept long
+// enough (a 64-chunk scan takes ~120 us) for that to be small.
+constexpr int SEG_CHUNKS = 64;
 
+// Workspace: the chunk table, the state carried between segments, and the
+// scan operands of one segment of SEG_CHUNKS chunks -- twice when there are
+// several segments, so that the next segment's operands are produced while
+// the current one is scanned.
 struct WsLayout {
-  size_t chunk_start, vh, kh, Ut, carry, total;
+  size_t chunk_start, carry, total;
+  size_t vh[2], kh[2], Ut[2];  // segment k uses buffer k % 2
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-WsLayout ws_layout(int n_seqs, int64_t seg_chunks, int Hv, int Hk, bool need_carry) {
+WsLayout ws_layout(int n_seqs, int64_t seg_chunks, int Hv, int Hk, bool multi) {
   WsLayout l;
   size_t off = 0;
   l.chunk_start = off;
   off = align256(off + sizeof(int32_t) * (n_seqs + 1));
-  l.vh = off;
-  off = align256(off + 16ull * seg_chunks * Hv * NB_VH * 64);
-  l.kh = off;
-  off = align256(off + 16ull * seg_chunks * Hk * NB_KH * 64);
-  l.Ut = off;
-  off = align256(off + sizeof(float) * seg_chunks * Hv * DV * CK);
   l.carry = off;
-  if (need_carry) off = align256(off + sizeof(float) * static_cast<size_t>(n_seqs) * Hv * DK * DV);
+  if (multi) off = align256(off + sizeof(float) * static_cast<size_t>(n_seqs) * Hv * DK * DV);
+  for (int b = 0; b < 2; ++b) {
+    if (b == 1 && !multi) {
+      l.vh[1] = l.vh[0];
+      l.kh[1] = l.kh[0];
+      l.Ut[1] = l.Ut[0];
+      break;
+    }
+    l.vh[b] = off;
+    off = align256(off + 16ull * seg_chunks * Hv * NB_VH * 64);
+    l.kh[b] = off;
+    off = align256(off + 16ull * seg_chunks * Hk * NB_KH * 64);
+    l.Ut[b] = off;
+    off = align256(off + sizeof(float) * seg_chunks * Hv * DV * CK);
+  }
   l.total = off;
   return l;
 }
@@ -833,6 +850,36 @@ WsLayout ws_layout(int n_seqs, int64_t seg_chunks, int Hv, int Hk, bool need_car
 int64_t max_chunks_of(int n_seqs, int64_t total_tokens, bool varlen, int T) {
   if (!varlen) return static_cast<int64_t>(n_seqs) * ((T + CK - 1) / CK);
   return (total_tokens + CK - 1) / CK + n_seqs;
+}
+
+// Per-device side stream for the segment producer (chunk_prep_kernel), plus a
+// ring of events for the hand-offs.  Created on the first multi-segment call
+// on a device (that call must not be under graph capture) and kept until the
+// process ends.  The stream is non-blocking, so it does not synchronise
+// implicitly with the legacy default stream; default priority.
+constexpr int SIDE_EVENTS = 8;
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t ev[SIDE_EVENTS] = {};
+};
+constexpr int MAX_DEVICES = 64;
+SideStream g_side[MAX_DEVICES];
+std::mutex g_side_mu;
+
+int side_stream(SideStream **out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
+    return fail(GDN_ERR_LAUNCH, "gdn_chunk_fwd: no current device");
+  SideStream &ss = g_side[dev];
+  if (!ss.stream) {
+    if (hipStreamCreateWithFlags(&ss.stream, hipStreamNonBlocking) != hipSuccess)
+      return fail(GDN_ERR_LAUNCH, "gdn_chunk_fwd: hipStreamCreateWithFlags failed");
+    for (int i = 0; i < SIDE_EVENTS; ++i)
+      if (hipEventCreateWithFlags(&ss.ev[i], hipEventDisableTiming) != hipSuccess)
+        return fail(GDN_ERR_LAUNCH, "gdn_chunk_fwd: hipEventCreateWithFlags failed");
+  }
+  *out = &ss;
+  return GDN_OK;
 }
 
 }  // namespace
@@ -887,23 +934,67 @@ extern "C" int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qk
   ChunkArgs a{static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
               q_stride_t, k_stride_t, v_stride_t, g, beta, beta_dtype, h0, h0_idx, hT, hT_idx, o, o_dtype,
               cu_seqlens, n_seqs, T, Hk, Hv, total, scale, l2norm_qk, static_cast<int>(nc), 0, 0,
-              reinterpret_cast<int32_t *>(ws + l.chunk_start), reinterpret_cast<u32x4 *>(ws + l.vh),
-              reinterpret_cast<u32x4 *>(ws + l.kh), reinterpret_cast<float *>(ws + l.Ut),
+              reinterpret_cast<int32_t *>(ws + l.chunk_start), nullptr, nullptr, nullptr,
               reinterpret_cast<float *>(ws + l.carry)};
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, s, a);
-  // One prep + scan pair per segment of SEG_CHUNKS global chunks (at least one
-  // pair, so that empty sequences still pass their initial state through).
-  for (int64_t sb = 0; sb == 0 || sb < nc; sb += seg) {
-    a.seg_begin = static_cast<int>(sb);
-    a.seg_end = static_cast<int>(std::min<int64_t>(sb + seg, nc));
-    if (seg > 0) hipLaunchKernelGGL(chunk_prep_kernel, dim3(Hv, static_cast<unsigned>(seg)), dim3(256), 0, s, a);
+  auto use_buffer = [&](int64_t segment) {
+    const int b = static_cast<int>(segment & 1);
+    a.vh = reinterpret_cast<u32x4 *>(ws + l.vh[b]);
+    a.kh = reinterpret_cast<u32x4 *>(ws + l.kh[b]);
+    a.Ut = reinterpret_cast<float *>(ws + l.Ut[b]);
+  };
+  auto set_segment = [&](int64_t segment) {
+    a.seg_begin = static_cast<int>(segment * seg);
+    a.seg_end = static_cast<int>(std::min<int64_t>((segment + 1) * seg, nc));
+    use_buffer(segment);
+  };
+  auto launch_prep = [&](hipStream_t st) {
+    hipLaunchKernelGGL(chunk_prep_kernel, dim3(Hv, static_cast<unsigned>(seg)), dim3(256), 0, st, a);
+  };
+  auto launch_scan = [&](hipStream_t st) {
     if (o_dtype == GDN_DTYPE_BF16)
       hipLaunchKernelGGL((chunk_scan_kernel<SCAN_WAVES, true>), dim3(static_cast<unsigned>(scan_blocks)),
-                         dim3(64 * SCAN_WAVES), 0, s, a);
+                         dim3(64 * SCAN_WAVES), 0, st, a);
     else
       hipLaunchKernelGGL((chunk_scan_kernel<SCAN_WAVES, false>), dim3(static_cast<unsigned>(scan_blocks)),
-                         dim3(64 * SCAN_WAVES), 0, s, a);
+                         dim3(64 * SCAN_WAVES), 0, st, a);
+  };
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, s, a);
+  const int64_t nseg = seg > 0 ? (nc + seg - 1) / seg : 0;
+  if (nseg <= 1) {  // one segment (or none: empty sequences still pass their state through)
+    set_segment(0);
+    if (seg > 0) launch_prep(s);
+    launch_scan(s);
+    return check_launch("gdn_chunk_fwd");
   }
+  // Several segments: segment k + 1 is prepared on the side stream while
+  // segment k is scanned on the caller's stream.  prep(k + 1) writes buffer
+  // (k + 1) % 2, which scan(k - 1) read: it waits for that scan.  Every side
+  // stream operation is followed by an event the caller's stream waits on,
+  // so the caller's stream ends after all of this call's work (and a graph
+  // captured on it contains the side branch).
+  std::lock_guard<std::mutex> lock(g_side_mu);
+  SideStream *side = nullptr;
+  if (const int st = side_stream(&side)) return st;
+  hipEvent_t *ev = side->ev;
+  const int R = SIDE_EVENTS / 2;  // ring of prep-done events ev[0..R) and scan-done events ev[R..2R)
+  int rc = hipEventRecord(ev[0], s) != hipSuccess;  // inputs and chunk table ready
+  rc |= hipStreamWaitEvent(side->stream, ev[0], 0) != hipSuccess;
+  set_segment(0);
+  launch_prep(side->stream);
+  rc |= hipEventRecord(ev[0], side->stream) != hipSuccess;
+  for (int64_t kseg = 0; kseg < nseg; ++kseg) {
+    if (kseg + 1 < nseg) {
+      if (kseg >= 1) rc |= hipStreamWaitEvent(side->stream, ev[R + (kseg - 1) % R], 0) != hipSuccess;
+      set_segment(kseg + 1);
+      launch_prep(side->stream);
+      rc |= hipEventRecord(ev[(kseg + 1) % R], side->stream) != hipSuccess;
+    }
+    rc |= hipStreamWaitEvent(s, ev[kseg % R], 0) != hipSuccess;
+    set_segment(kseg);
+    launch_scan(s);
+    rc |= hipEventRecord(ev[R + kseg % R], s) != hipSuccess;
+  }
+  if (rc) return fail(GDN_ERR_LAUNCH, "gdn_chunk_fwd: stream event hand-off failed");
   return check_launch("gdn_chunk_fwd");
 }

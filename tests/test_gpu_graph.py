@@ -53,8 +53,9 @@ def test_decode_step_graph_replays_match_eager():
         assert torch.equal(pool, pool_eager)
 
 
-def test_chunk_prefill_graph_replays_match_eager():
-    c = configs.config2(seed=12, t=300)
+@pytest.mark.parametrize("t", [300, 4200])  # one segment; two (side-stream producer)
+def test_chunk_prefill_graph_replays_match_eager(t):
+    c = configs.config2(seed=12, t=t)
     q, k, v, g, beta = (c[x].to(DEV) for x in ("q", "k", "v", "g", "beta"))
     h0 = torch.randn(1, 32, 128, 128, generator=torch.Generator().manual_seed(4)).mul(0.1).to(DEV)
 
