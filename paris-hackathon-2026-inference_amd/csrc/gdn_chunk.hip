@@ -6,14 +6,17 @@
 //   U = T (beta V),  W = T (beta e^gamma K~)
 //   V' = U - W S ;  O = (e^gamma Q~) S + lower(Q~K~^T * Gamma) V'
 //   S <- e^{gamma_63} S + (e^{gamma_63 - gamma} K~)^T V'
-// runs as three launches:
-//   chunk_table_kernel  chunk -> sequence table (cu_seqlens aware)
+// runs as up to three launches:
+//   chunk_table_kernel  chunk -> sequence table (only with cu_seqlens)
 //   chunk_prep_kernel   one workgroup per (chunk, v-head), all in parallel:
-//                       K K^T and Q K^T on MFMA from the raw bf16 rows (exact
+//                       K K^T and K Q^T on MFMA from the raw bf16 rows (exact
 //                       products; l2norm and gate factors scale the fp32
-//                       results), T by blocked substitution in fp32 (LDS),
-//                       W = T' K and U = T'' V on MFMA with T', T'' split into
-//                       bf16 hi + lo parts.  Every operand the scan needs is
+//                       results), computed transposed so that L and A come out
+//                       in the layout their consumers read; T = (I + L)^-1 by
+//                       substitution on the 16x16 diagonal blocks and fp32 MFMA
+//                       below them; W = T' K and U = T'' V on MFMA with T', T''
+//                       split into bf16 hi + lo parts and K, V read transposed
+//                       (ds_read_b64_tr_b16).  Every operand the scan needs is
 //                       written pre-swizzled: one 1 KiB block per (MFMA, wave),
 //                       lane l's 16 bytes at offset 16 l.
 //   chunk_scan_kernel   one wave per (sequence, v-head, 16 state columns),
@@ -21,6 +24,8 @@
 //                       accumulators for the whole sequence.  The next chunk's
 //                       operand blocks stream into a second LDS buffer with
 //                       buffer_load ... lds while the current chunk computes.
+// Inputs longer than one segment (64 chunks) run prep / scan per segment,
+// the next segment's prep on a side stream.
 // Precision (checked against an fp64 restatement at T=4096): the state is fed
 // to MFMA as bf16, U stays fp32 (it initialises the V' accumulator), the state
 // increment K^T V'' uses V'' split into bf16 hi + lo.
@@ -132,6 +137,11 @@ struct ChunkArgs {
 __device__ __forceinline__ void seq_bounds(const ChunkArgs &a, int n, int64_t *s0, int *len) {
   seq_range(a.cu, n, a.T, a.total, s0, len);
 }
+// First global chunk of sequence n (n = n_seqs: the chunk count).  Without
+// cu_seqlens every sequence has ceil(T / 64) chunks and no table is built.
+__device__ __forceinline__ int chunk_start_at(const ChunkArgs &a, int n) {
+  return a.cu ? a.chunk_start[n] : n * ((a.T + CK - 1) / CK);
+}
 
 // ------------------------------------------------------------------ chunk table
 __global__ __launch_bounds__(256) void chunk_table_kernel(ChunkArgs a) {
@@ -235,17 +245,21 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
 
   const int h = blockIdx.x;
   const int j = a.seg_begin + static_cast<int>(blockIdx.y);  // global chunk index
-  if (j >= a.seg_end || j >= a.chunk_start[a.n_seqs]) return;
+  if (j >= a.seg_end || j >= chunk_start_at(a, a.n_seqs)) return;
   int lo = 0, hi = a.n_seqs;  // sequence owning chunk j: last n with chunk_start[n] <= j
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (a.chunk_start[mid] <= j) lo = mid; else hi = mid;
+  if (!a.cu) {
+    lo = j / ((a.T + CK - 1) / CK);
+  } else {
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (a.chunk_start[mid] <= j) lo = mid; else hi = mid;
+    }
   }
   const int n = lo;
   int64_t s0;
   int slen;
   seq_bounds(a, n, &s0, &slen);
-  const int c = j - a.chunk_start[n];
+  const int c = j - chunk_start_at(a, n);
   const int64_t t0 = s0 + static_cast<int64_t>(c) * CK;
   const int len = min(CK, slen - c * CK);
   if (len <= 0) return;
@@ -703,8 +717,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
   // Chunks [cs, ce) of sequence n; this launch covers global chunks
   // [seg_begin, seg_end).  chunk_start is built from clamped lengths, so it
   // never exceeds the workspace bound; the min() keeps that true here too.
-  const int cs = __builtin_amdgcn_readfirstlane(a.chunk_start[n]);
-  const int ce = __builtin_amdgcn_readfirstlane(max(cs, min(a.chunk_start[n + 1], a.max_chunks)));
+  const int cs = __builtin_amdgcn_readfirstlane(chunk_start_at(a, n));
+  const int ce = __builtin_amdgcn_readfirstlane(max(cs, min(chunk_start_at(a, n + 1), a.max_chunks)));
   const int lo = max(cs, a.seg_begin), hi = min(ce, a.seg_end);
   const int64_t in_row = a.h0 ? uniform64(a.h0_idx ? a.h0_idx[n] : n) : -1;
   const int64_t out_row = a.hT ? uniform64(a.hT_idx ? a.hT_idx[n] : n) : -1;
@@ -959,7 +973,7 @@ extern "C" int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qk
                          dim3(64 * SCAN_WAVES), 0, st, a);
   };
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, s, a);
+  if (cu_seqlens) hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, s, a);
   const int64_t nseg = seg > 0 ? (nc + seg - 1) / seg : 0;
   if (nseg <= 1) {  // one segment (or none: empty sequences still pass their state through)
     set_segment(0);
