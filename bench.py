@@ -16,7 +16,9 @@ The JSON line also carries
                 (K back-to-back launches between two HIP events on the launch
                 stream) against the 8 TB/s HBM peak;
   prefill       chunk-64 prefill at T=4096 (configuration 2): tok/s and the
-                dense-equivalent flop rate against the 2.5 PFLOP/s bf16 peak;
+                dense-equivalent flop rate against the 2.5 PFLOP/s bf16 peak
+                (q/k at 16 heads; prefill_qk_repeated: q/k repeated to 32 heads
+                as HF passes them);
   cpu_baseline  the CPU oracle (numpy fp32, sequences split over the host's
                 cores) on a bounded sample of the same decode workload.
 """
@@ -50,7 +52,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill measurement")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill measurements")
+    ap.add_argument("--no-prefill-repeated", action="store_true",
+                    help="skip the prefill timing with q/k repeated to 32 heads")
     ap.add_argument("--pools", type=int, default=4, help="rotating decode state pools")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 128 MiB device copy (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -138,13 +142,19 @@ def bench_decode(torch, steps, warmup, n_pools):
     return dict(tokens=b, steps=steps, kernel_s=kernel_s, eager_wall=eager_wall, graph_wall=graph_wall)
 
 
-def bench_prefill(torch, reps=20, warmup=3):
+def bench_prefill(torch, reps=20, warmup=3, repeat_qk=False):
+    """Configuration 2.  With repeat_qk, q and k arrive repeated to the 32 v-heads
+    (HF's repeat_interleave before the call), the layout the reference's boundary
+    actually receives; otherwise they keep their 16 heads (native GQA)."""
     from engine import configs
     from engine.kernels import chunk_gated_delta_rule
 
     c = configs.config2()
     dev = torch.device("cuda", 0)
     q, k, v, g, beta = (c[x].to(dev) for x in ("q", "k", "v", "g", "beta"))
+    if repeat_qk:
+        rep = v.shape[2] // q.shape[2]
+        q, k = q.repeat_interleave(rep, dim=2), k.repeat_interleave(rep, dim=2)
     t = q.shape[1]
 
     def run():
@@ -162,7 +172,7 @@ def bench_prefill(torch, reps=20, warmup=3):
     torch.cuda.synchronize()
     per = e0.elapsed_time(e1) * 1e-3 / reps
     flop = PREFILL_FLOP_PER_CHUNK_HEAD * ((t + 63) // 64) * 32
-    return {"config": "prefill B=1 T=4096 Hk=16 Hv=32 d=128 bf16, chunk 64, zero h0, final state out",
+    return {"config": f"prefill B=1 T=4096 Hk={q.shape[2]} Hv=32 d=128 bf16, chunk 64, zero h0, final state out",
             "tok_per_s": t / per, "ms": per * 1e3,
             "mfma": {"achieved": flop / per / 1e12, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
                      "frac": flop / per / MFMA_BF16_PEAK, "flop_per_call": flop}}
@@ -240,6 +250,8 @@ def main():
     }
     if not args.no_prefill:
         out["prefill"] = bench_prefill(torch)
+        if not args.no_prefill_repeated:
+            out["prefill_qk_repeated"] = bench_prefill(torch, repeat_qk=True)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)
