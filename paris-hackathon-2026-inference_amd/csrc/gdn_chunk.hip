@@ -516,64 +516,76 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
 }
 
 // ------------------------------------------------------------------ phase B
-// LDS stage: one chunk's scan operands for a workgroup of NW waves: the
-// v-head region, the k-head region, then U for the workgroup's 16*NW
-// columns, 4 blocks per wave.
+// LDS stage: one chunk's shared scan operands, the v-head region then the
+// k-head region (57 blocks of 1 KiB).  U is per wave and goes straight from
+// global memory to registers.
 constexpr int ST_W = VH_W * 64;
 constexpr int ST_A = VH_A * 64;
 constexpr int ST_SC = VH_SC * 64;
 constexpr int ST_Q = (NB_VH + KH_Q) * 64;
 constexpr int ST_KT = (NB_VH + KH_KT) * 64;
-constexpr int ST_U = (NB_VH + NB_KH) * 64;
-template <int NW> struct Stage {
-  static constexpr int blocks = NB_VH + NB_KH + 4 * NW;
-  static constexpr int u4 = blocks * 64;  // size in 16-byte units
-};
+constexpr int ST_U4 = (NB_VH + NB_KH) * 64;  // stage size in 16-byte units
 
 constexpr int BUF_DWORD3 = 0x00020000;  // raw (untyped) buffer resource word 3 on CDNA
 
-// Copies nb 1 KiB blocks of a region into LDS with buffer_load ... lds: a
-// uniform base (no per-lane 64-bit address math), 64 lanes x 16 bytes per
-// instruction.  Wave w issues blocks w, w + NW, ...; a wave with no block
-// left in the last round copies the region's last block again (same bytes to
-// the same LDS address), which keeps the copy free of branches.
+// The next chunk's stage is copied with buffer_load ... lds (64 lanes x 16
+// bytes per instruction, uniform base, range-checked), spread over the
+// current chunk's MFMA work: a CU's vector-memory path moves 64 B/clk, so
+// issuing all of a chunk's copies at once would stall every wave for about
+// a thousand cycles.  Wave w copies blocks w, w + NW, ... of each region; a
+// wave with no block left in the last round copies the region's last block
+// again (same bytes to the same LDS address), which keeps it branch-free.
+struct StageSrc {
+  __amdgpu_buffer_rsrc_t vh, kh;
+};
+template <int NW> struct Dma {
+  static constexpr int vh = (NB_VH + NW - 1) / NW;
+  static constexpr int kh = (NB_KH + NW - 1) / NW;
+  static constexpr int n = vh + kh;  // copies per wave per chunk
+};
 template <int NW>
-__device__ __forceinline__ void copy_region(u32x4 *dst, const void *src, int nb, int wave, int lane) {
-  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(src), 0, nb * 1024, BUF_DWORD3);
-#pragma unroll
-  for (int i = 0; i < (nb + NW - 1) / NW; ++i) {
-    const int t = min(i * NW + wave, nb - 1);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst + t * 64, 16, lane * 16, t * 1024, 0, 0);
+__device__ __forceinline__ void dma_copy(int i, u32x4 *dst, const StageSrc &src, int wave, int lane) {
+  if (i < Dma<NW>::vh) {
+    const int t = min(i * NW + wave, NB_VH - 1);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src.vh, dst + t * 64, 16, lane * 16, t * 1024, 0, 0);
+  } else {
+    const int t = min((i - Dma<NW>::vh) * NW + wave, NB_KH - 1);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src.kh, dst + (NB_VH + t) * 64, 16, lane * 16, t * 1024, 0, 0);
   }
 }
-
 template <int NW>
-__device__ __forceinline__ void stage_load(u32x4 *st, const ChunkArgs &a, size_t ch, size_t chk, int ct, int wave,
-                                           int lane) {
-  copy_region<NW>(st, a.vh + ch * (NB_VH * 64), NB_VH, wave, lane);
-  copy_region<NW>(st + NB_VH * 64, a.kh + chk * (NB_KH * 64), NB_KH, wave, lane);
-  copy_region<NW>(st + ST_U, a.Ut + ch * (DV * CK) + ct * (NW * 4 * 256), 4 * NW, wave, lane);
+__device__ __forceinline__ StageSrc stage_src(const ChunkArgs &a, size_t ch, size_t chk) {
+  return StageSrc{__builtin_amdgcn_make_buffer_rsrc(a.vh + ch * (NB_VH * 64), 0, NB_VH * 1024, BUF_DWORD3),
+                  __builtin_amdgcn_make_buffer_rsrc(a.kh + chk * (NB_KH * 64), 0, NB_KH * 1024, BUF_DWORD3)};
+}
+// This wave's U rows of one chunk (4 blocks of 1 KiB, lane l's 16 bytes at 16 l).
+__device__ __forceinline__ void load_u(f32x4 (&u)[4], __amdgpu_buffer_rsrc_t r, int voff) {
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+    u[p] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + p * 1024, 0, 0));
 }
 
 // Output of one chunk: lane (g, c) holds rows 16p + 4g + e of its column.  The
 // buffer resource starts at the chunk's first token and ends after its last
 // valid row, so stores past the sequence end are dropped by the hardware
-// range check; voff[4p + e] is the byte offset of row 16p + 4g + e.
+// range check (which covers the VGPR offset: voff0 + row * row_bytes, with
+// voff0 the byte offset of row 4g of this lane's column).
 template <bool BF16_OUT>
-__device__ __forceinline__ void store_chunk(const f32x4 (&o)[4], __amdgpu_buffer_rsrc_t r, const int (&voff)[16]) {
+__device__ __forceinline__ void store_chunk(const f32x4 (&o)[4], __amdgpu_buffer_rsrc_t r, int voff0, int row_bytes) {
 #pragma unroll
   for (int p = 0; p < 4; ++p)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
+      const int off = voff0 + (16 * p + e) * row_bytes;
       if constexpr (BF16_OUT)
-        __builtin_amdgcn_raw_buffer_store_b16(bf16_rne(o[p][e]), r, voff[4 * p + e], 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b16(bf16_rne(o[p][e]), r, off, 0, 0);
       else
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, o[p][e]), r, voff[4 * p + e], 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, o[p][e]), r, off, 0, 0);
     }
 }
 
 // sched_group_barrier masks
-constexpr int SG_VALU = 0x2, SG_MFMA = 0x8, SG_VMEM_WR = 0x40, SG_DS_RD = 0x100;
+constexpr int SG_VALU = 0x2, SG_MFMA = 0x8, SG_VMEM_RD = 0x20, SG_VMEM_WR = 0x40, SG_DS_RD = 0x100;
 #define GDN_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 #define GDN_GROUP(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
 
@@ -588,11 +600,14 @@ constexpr int SG_VALU = 0x2, SG_MFMA = 0x8, SG_VMEM_WR = 0x40, SG_DS_RD = 0x100;
 //                                          next chunk's bf16 state operands
 // sb holds the state as bf16 B operands (k-steps over the 128 state rows);
 // on return it holds the updated state, o holds this chunk's output.
-template <bool BF16_OUT>
-__device__ __forceinline__ void scan_chunk(const u32x4 *st, int ubase, f32x4 (&S)[8], bf16x8 (&sb)[4], f32x4 (&o)[4],
-                                           __amdgpu_buffer_rsrc_t prev_out, const int (&voff)[16], int lane) {
+template <int NW, bool BF16_OUT>
+__device__ __forceinline__ void scan_chunk(const u32x4 *st, const f32x4 (&u)[4], f32x4 (&S)[8], bf16x8 (&sb)[4],
+                                           f32x4 (&o)[4], __amdgpu_buffer_rsrc_t prev_out, int voff0, int row_bytes,
+                                           u32x4 *st_next, const StageSrc &src_next, f32x4 (&u_next)[4],
+                                           __amdgpu_buffer_rsrc_t u_rsrc_next, int u_voff, int wave, int lane) {
   const int g4 = lane >> 4;
   const float *sc = reinterpret_cast<const float *>(st + ST_SC);
+  constexpr int D1 = Dma<NW>::n / 2, D2 = Dma<NW>::n;  // copies issued in R1 | R2 (R3 none: its copies would land late)
 
   // ---- R1
   u32x4 wb[16];
@@ -600,7 +615,7 @@ __device__ __forceinline__ void scan_chunk(const u32x4 *st, int ubase, f32x4 (&S
   for (int i = 0; i < 16; ++i) wb[i] = st[ST_W + i * 64 + lane];
   f32x4 vp[4];  // V' rows 16p + 4g + e
 #pragma unroll
-  for (int p = 0; p < 4; ++p) vp[p] = __builtin_bit_cast(f32x4, st[ubase + p * 64 + lane]);
+  for (int p = 0; p < 4; ++p) vp[p] = u[p];
   const float eL = sc[2 * CK];
   u32x4 qb[16];
 #pragma unroll
@@ -608,20 +623,24 @@ __device__ __forceinline__ void scan_chunk(const u32x4 *st, int ubase, f32x4 (&S
   f32x4 sk[4];
 #pragma unroll
   for (int p = 0; p < 4; ++p) sk[p] = *reinterpret_cast<const f32x4 *>(sc + CK + 16 * p + 4 * g4);
-  store_chunk<BF16_OUT>(o, prev_out, voff);
+  store_chunk<BF16_OUT>(o, prev_out, voff0, row_bytes);
+  load_u(u_next, u_rsrc_next, u_voff);
+#pragma unroll
+  for (int i = 0; i < D1; ++i) dma_copy<NW>(i, st_next, src_next, wave, lane);
 #pragma unroll
   for (int s2 = 0; s2 < 4; ++s2)
 #pragma unroll
     for (int p = 0; p < 4; ++p) vp[p] = mfma(as_bf16x8(wb[4 * p + s2]), sb[s2], vp[p]);
 #pragma unroll
   for (int i = 0; i < 8; ++i) S[i] = S[i] * eL;
-  GDN_GROUP(SG_DS_RD, 21);
+  GDN_GROUP(SG_DS_RD, 17);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     GDN_GROUP(SG_MFMA, 1);
     GDN_GROUP(SG_DS_RD, 1);
     GDN_GROUP(SG_VALU, 3);
     GDN_GROUP(SG_VMEM_WR, 1);
+    GDN_GROUP(SG_VMEM_RD, 1);
   }
   GDN_SCHED_FENCE();
 
@@ -638,6 +657,8 @@ __device__ __forceinline__ void scan_chunk(const u32x4 *st, int ubase, f32x4 (&S
   f32x4 sq[4];
 #pragma unroll
   for (int p = 0; p < 4; ++p) sq[p] = *reinterpret_cast<const f32x4 *>(sc + 16 * p + 4 * g4);
+#pragma unroll
+  for (int i = D1; i < D2; ++i) dma_copy<NW>(i, st_next, src_next, wave, lane);
   f32x4 acc[4];
 #pragma unroll
   for (int p = 0; p < 4; ++p) acc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -656,6 +677,7 @@ __device__ __forceinline__ void scan_chunk(const u32x4 *st, int ubase, f32x4 (&S
     GDN_GROUP(SG_MFMA, 1);
     GDN_GROUP(SG_DS_RD, 2);
     GDN_GROUP(SG_VALU, 4);
+    GDN_GROUP(SG_VMEM_RD, 1);
   }
   GDN_SCHED_FENCE();
 
@@ -680,9 +702,12 @@ __device__ __forceinline__ void scan_chunk(const u32x4 *st, int ubase, f32x4 (&S
 #pragma unroll
   for (int s2 = 0; s2 < 4; ++s2) sb[s2] = pack_hi(S[2 * s2], S[2 * s2 + 1]);
 #pragma unroll
+  for (int i = D2; i < Dma<NW>::n; ++i) dma_copy<NW>(i, st_next, src_next, wave, lane);
+#pragma unroll
   for (int i = 0; i < 38; ++i) {
     GDN_GROUP(SG_MFMA, 1);
     GDN_GROUP(SG_VALU, 1);
+    GDN_GROUP(SG_VMEM_RD, 1);
   }
   GDN_SCHED_FENCE();
 }
@@ -692,8 +717,8 @@ __device__ __forceinline__ void scan_chunk(const u32x4 *st, int ubase, f32x4 (&S
 // wave and may use the whole register file.
 template <int NW, bool BF16_OUT>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1))) void chunk_scan_kernel(ChunkArgs a) {
-  __shared__ u32x4 stage0[Stage<NW>::u4];
-  __shared__ u32x4 stage1[Stage<NW>::u4];
+  __shared__ u32x4 stage0[ST_U4];
+  __shared__ u32x4 stage1[ST_U4];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g4 = lane >> 4;
@@ -705,7 +730,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
   const int h = rest % a.Hv;
   const int hk = h / (a.Hv / a.Hk);
   const int col = 16 * NW * ct + 16 * wave + r16;
-  const int ubase = ST_U + wave * 4 * 64;  // this wave's U blocks in a stage
+  const int u_voff = ((4 * NW * ct + 4 * wave) * 64 + lane) * 16;  // this wave's U blocks in a chunk's U region
 
   // Values read from memory are workgroup-uniform; readfirstlane tells the
   // compiler so (buffer resources built from them must live in SGPRs).
@@ -760,12 +785,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
   // Output addressing: byte offsets of rows 16p + 4g + e within a chunk.
   typedef typename std::conditional<BF16_OUT, uint16_t, float>::type OT;
   const int64_t ostep = static_cast<int64_t>(a.Hv) * DV;  // elements per token
-  int voff[16];
-#pragma unroll
-  for (int p = 0; p < 4; ++p)
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      voff[4 * p + e] = static_cast<int>(((16 * p + 4 * g4 + e) * ostep + h * DV + col) * sizeof(OT));
+  const int row_bytes = static_cast<int>(ostep * sizeof(OT));
+  const int voff0 = static_cast<int>((4 * g4 * ostep + h * DV + col) * sizeof(OT));
   auto out_rsrc = [&](int c) {  // chunk c of this launch: rows [0, min(64, rest of sequence))
     const int64_t toff = seq_off + static_cast<int64_t>(c) * CK;
     const int rows = static_cast<int>(min<int64_t>(CK, slen - toff));
@@ -778,29 +799,38 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 #pragma unroll
   for (int p = 0; p < 4; ++p) o[p] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto load_stage = [&](u32x4 *st, int cidx) {
-    const size_t j = static_cast<size_t>(c0 + cidx);
-    stage_load<NW>(st, a, j * a.Hv + h, j * a.Hk + hk, ct, wave, lane);
+  // Chunk cidx of this launch (clamped: after the last chunk the "next"
+  // copies reload the last chunk into the idle stage).
+  auto chunk_of = [&](int cidx) { return static_cast<size_t>(c0 + min(cidx, nch - 1)); };
+  auto src_of = [&](int cidx) { const size_t j = chunk_of(cidx); return stage_src<NW>(a, j * a.Hv + h, j * a.Hk + hk); };
+  auto u_rsrc_of = [&](int cidx) {
+    return __builtin_amdgcn_make_buffer_rsrc(a.Ut + (chunk_of(cidx) * a.Hv + h) * (DV * CK), 0, DV * CK * 4, BUF_DWORD3);
   };
-  // A chunk's output is stored during the next chunk (vmcnt counts stores
-  // too, so the wait at the end of each chunk then finds them long done).
-  load_stage(stage0, 0);
+  f32x4 u0[4], u1[4];
+  {
+    const StageSrc src = src_of(0);
+#pragma unroll
+    for (int i = 0; i < Dma<NW>::n; ++i) dma_copy<NW>(i, stage0, src, wave, lane);
+    load_u(u0, u_rsrc_of(0), u_voff);
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  // A chunk's output is stored during the next chunk (vmcnt counts stores
+  // too, so the wait at the end of each chunk then finds them long done).
   for (int c = 0; c < nch; c += 2) {
-    if (c + 1 < nch) load_stage(stage1, c + 1);
-    scan_chunk<BF16_OUT>(stage0, ubase, S, sb, o, prev, voff, lane);
+    scan_chunk<NW, BF16_OUT>(stage0, u0, S, sb, o, prev, voff0, row_bytes, stage1, src_of(c + 1), u1, u_rsrc_of(c + 1), u_voff,
+                             wave, lane);
     prev = out_rsrc(c);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (c + 1 >= nch) break;
-    if (c + 2 < nch) load_stage(stage0, c + 2);
-    scan_chunk<BF16_OUT>(stage1, ubase, S, sb, o, prev, voff, lane);
+    scan_chunk<NW, BF16_OUT>(stage1, u1, S, sb, o, prev, voff0, row_bytes, stage0, src_of(c + 2), u0, u_rsrc_of(c + 2), u_voff,
+                             wave, lane);
     prev = out_rsrc(c + 1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
-  store_chunk<BF16_OUT>(o, prev, voff);
+  store_chunk<BF16_OUT>(o, prev, voff0, row_bytes);
 
   float *dst = hi == ce ? (out_row >= 0 ? a.hT + (out_row * a.Hv + h) * kv + col : nullptr) : carry;
   if (dst) {
