@@ -10,10 +10,13 @@
  *
  * Conventions shared by every entry point
  *   - Pointers are device pointers unless stated otherwise.  Nothing here
- *     allocates device memory, synchronises the device or the stream, or
- *     keeps state between calls: every kernel is enqueued on `stream`
- *     (a hipStream_t passed as void*; NULL is the null stream), so calls are
- *     safe to record into a HIP graph.
+ *     allocates device memory or synchronises the device or the stream:
+ *     every kernel is enqueued on `stream` (a hipStream_t passed as void*;
+ *     NULL is the null stream), so calls are safe to record into a HIP graph.
+ *     The only state kept between calls: a chunk prefill longer than one
+ *     segment (64 chunks) runs its producer on a per-device side stream,
+ *     created with a ring of events by the first such call on the device
+ *     (which must not itself be under graph capture) and kept until exit.
  *   - The return value is a gdn_status_t.  On failure nothing was launched
  *     and gdn_last_error_string() (thread-local) says why.
  *   - Token-major activations: element (token t, head h, dim d) of q/k/v lives
@@ -38,7 +41,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 1
+#define GDN_ABI_VERSION 2
 
 typedef enum {
   GDN_OK = 0,
@@ -95,6 +98,28 @@ int gdn_recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype
                       float scale, int l2norm_qk, void *stream);
 
 /*
+ * gdn_recurrent_fwd with the gates computed in the kernel prologue from the
+ * layer's raw projections instead of passed precomputed:
+ *   beta = sigmoid(b),  g = -exp(A_log[h]) * softplus(a + dt_bias[h])
+ * (softplus(x) = x for x > 20), replacing the torch glue of HF's GDN layer
+ * forward (transformers modeling_qwen3_5_moe.py:495-497) and its extra
+ * [tokens, Hv] round trips.
+ *   a, b     [tokens, Hv] (ab_dtype, token stride ab_stride_t >= Hv)
+ *   A_log, dt_bias  fp32 [Hv]
+ * Every other argument as for gdn_recurrent_fwd.
+ */
+int gdn_recurrent_fwd_gated(const void *q, const void *k, const void *v, int qkv_dtype,
+                            int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
+                            const void *a, const void *b, int ab_dtype, int64_t ab_stride_t,
+                            const float *A_log, const float *dt_bias,
+                            const float *state_in, const int64_t *state_in_idx,
+                            float *state_out, const int64_t *state_out_idx,
+                            void *o, int o_dtype, float *snapshots,
+                            const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
+                            int32_t Hk, int32_t Hv, int32_t K, int32_t V,
+                            float scale, int l2norm_qk, void *stream);
+
+/*
  * Chunk-64 prefill (WY/UT form).
  *
  * Replaces engine/kernels/delta_rule.py:352-438 (chunk_gated_delta_rule, the
@@ -121,10 +146,44 @@ int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
                   float scale, int l2norm_qk,
                   void *workspace, size_t workspace_bytes, void *stream);
 
-/* Workspace bytes gdn_chunk_fwd needs for `total_tokens` tokens in `n_seqs`
- * sequences (an upper bound that needs no knowledge of the lengths). */
+/*
+ * gdn_chunk_fwd with the gates computed in the kernel prologue from the
+ * layer's raw projections (a, b, A_log, dt_bias as for
+ * gdn_recurrent_fwd_gated; transformers modeling_qwen3_5_moe.py:495-497).
+ */
+int gdn_chunk_fwd_gated(const void *q, const void *k, const void *v, int qkv_dtype,
+                        int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
+                        const void *a, const void *b, int ab_dtype, int64_t ab_stride_t,
+                        const float *A_log, const float *dt_bias,
+                        const float *h0, const int64_t *h0_idx,
+                        float *hT, const int64_t *hT_idx,
+                        void *o, int o_dtype,
+                        const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
+                        int32_t Hk, int32_t Hv, int32_t K, int32_t V,
+                        float scale, int l2norm_qk,
+                        void *workspace, size_t workspace_bytes, void *stream);
+
+/* Workspace bytes gdn_chunk_fwd(_gated) needs for `total_tokens` tokens in
+ * `n_seqs` sequences (an upper bound that needs no knowledge of the lengths). */
 size_t gdn_chunk_workspace_bytes(int32_t n_seqs, int64_t total_tokens,
                                  int32_t Hv, int32_t K, int32_t V);
+
+/*
+ * Gated RMS norm of the GDN output, per (token, head) row of D values:
+ *   y = weight * x / sqrt(mean(x^2) + eps) * silu(z)
+ * in fp32, rounded once to y's dtype.  Replaces HF's RMSNormGated module
+ * applied to the core output (transformers modeling_qwen3_5_moe.py:169-185,
+ * called at :535-538), one pass instead of its chain of elementwise ops.
+ *   x, z, y  [tokens, H, D] with token strides x/z/y_stride_t (elements),
+ *            rows contiguous; dtypes bf16, fp16 or fp32 each
+ *   weight   [D] (w_dtype)
+ * Requires D == 128.
+ */
+int gdn_rmsnorm_gated_fwd(const void *x, int x_dtype, int64_t x_stride_t,
+                          const void *z, int z_dtype, int64_t z_stride_t,
+                          const void *weight, int w_dtype,
+                          void *y, int y_dtype, int64_t y_stride_t,
+                          int64_t n_tokens, int32_t H, int32_t D, float eps, void *stream);
 
 /*
  * Causal depthwise conv, prefill.

@@ -38,6 +38,41 @@ def l2norm(x: np.ndarray, eps: float = 1e-6) -> np.ndarray:
     return x / np.sqrt((x * x).sum(axis=-1, keepdims=True) + eps)
 
 
+def softplus(x: np.ndarray) -> np.ndarray:
+    """torch.nn.functional.softplus with its default threshold: x for x > 20,
+    log(1 + e^x) otherwise."""
+    x = np.asarray(x)
+    return np.where(x > 20, x, np.log1p(np.exp(np.minimum(x, 20))))
+
+
+def gdn_gates(a, b, A_log, dt_bias, dtype=np.float64):
+    """The GDN layer's gates from its raw projections.
+
+    Follows transformers 5.15.0 modeling_qwen3_5_moe.py:495-497 (the layer
+    forward the reference runs): ``beta = b.sigmoid()``,
+    ``g = -A_log.float().exp() * softplus(a.float() + dt_bias)``.
+    a, b [..., H]; A_log, dt_bias [H].  Returns (g, beta).
+    """
+    a, b, A_log, dt_bias = (np.asarray(x, dtype=dtype) for x in (a, b, A_log, dt_bias))
+    beta = 1.0 / (1.0 + np.exp(-b))
+    g = -np.exp(A_log) * softplus(a + dt_bias)
+    return g, beta
+
+
+def rms_norm_gated(x, z, weight, eps=1e-6, dtype=np.float64):
+    """Gated RMS norm over the last axis:
+    ``weight * x / sqrt(mean(x^2) + eps) * silu(z)``.
+
+    Follows transformers 5.15.0 ``Qwen3_5MoeRMSNormGated.forward``
+    (modeling_qwen3_5_moe.py:169-185), applied to the GDN core output at
+    :535-538, in one precision (the module rounds x * rsqrt(.) to the input
+    dtype before the weight; in fp32 that rounding is the identity).
+    """
+    x, z, weight = (np.asarray(t, dtype=dtype) for t in (x, z, weight))
+    r = 1.0 / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps)
+    return weight * (x * r) * (z / (1.0 + np.exp(-z)))
+
+
 def _prep(q, k, v, g, beta, use_qk_l2norm, dtype):
     q, k, v, g, beta = (np.asarray(a, dtype=dtype) for a in (q, k, v, g, beta))
     h = v.shape[2]

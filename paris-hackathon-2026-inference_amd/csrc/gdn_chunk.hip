@@ -79,13 +79,6 @@ __device__ __forceinline__ int64_t uniform64(int64_t x) {
 __device__ __forceinline__ uint16_t bf16_rne(float x) {  // hardware round-to-nearest-even
   return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
 }
-__device__ __forceinline__ bf16x8 ld8(const uint16_t *p) {
-  return as_bf16x8(*reinterpret_cast<const u32x4 *>(p));
-}
-__device__ __forceinline__ bf16x8 zero8() {
-  u32x4 u = {0u, 0u, 0u, 0u};
-  return as_bf16x8(u);
-}
 __device__ __forceinline__ bf16x8 pack_hi(f32x4 a, f32x4 b) {
   bf16x8 r;
 #pragma unroll
@@ -110,9 +103,7 @@ __device__ __forceinline__ void pack_hilo(f32x4 a, f32x4 b, bf16x8 &hi, bf16x8 &
 struct ChunkArgs {
   const uint16_t *q, *k, *v;  // bf16
   int64_t qs, ks, vs;         // token strides (elements)
-  const float *g;
-  const void *beta;
-  int beta_dt;
+  GateArgs gate;
   const float *h0;
   const int64_t *h0_idx;
   float *hT;
@@ -220,18 +211,6 @@ __device__ __forceinline__ f32x4 mm16(f32x4 a, f32x4 b, f32x4 acc) {
   return acc;
 }
 
-// Sum over the 16 lanes of a DPP row (every lane receives the sum).
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float row16_sum(float x) {
-  x += dpp_mov<0xB1>(x);   // quad_perm [1,0,3,2]
-  x += dpp_mov<0x4E>(x);   // quad_perm [2,3,0,1]
-  x += dpp_mov<0x141>(x);  // row_half_mirror
-  x += dpp_mov<0x140>(x);  // row_mirror
-  return x;
-}
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
 __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
@@ -304,8 +283,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
   }
   float gv = 0.f, bv = 0.f;
   if (p == 0 && lane < len) {
-    gv = a.g[(t0 + lane) * a.Hv + h];
-    bv = load_elem(a.beta, (t0 + lane) * a.Hv + h, a.beta_dt);
+    load_gates(a.gate, t0 + lane, h, &gv, &bv);
   }
 
   // ---- A.1: K, V rows into LDS; K row norms; chunk-local cumsum of g; Q row norms
@@ -938,45 +916,46 @@ extern "C" size_t gdn_chunk_workspace_bytes(int32_t n_seqs, int64_t total_tokens
   return ws_layout(n_seqs, std::min<int64_t>(nc, SEG_CHUNKS), Hv, Hv, nc > SEG_CHUNKS).total;
 }
 
-extern "C" int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
-                             int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
-                             const float *g, const void *beta, int beta_dtype,
-                             const float *h0, const int64_t *h0_idx,
-                             float *hT, const int64_t *hT_idx,
-                             void *o, int o_dtype,
-                             const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
-                             int32_t Hk, int32_t Hv, int32_t K, int32_t V,
-                             float scale, int l2norm_qk,
-                             void *workspace, size_t workspace_bytes, void *stream) {
-  using namespace gdn;
-  if (K != DK || V != DV) return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd: K=%d V=%d; only K=V=128 is built", K, V);
+namespace gdn {
+namespace {
+
+int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
+              int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t, const GateArgs &gate,
+              const float *h0, const int64_t *h0_idx, float *hT, const int64_t *hT_idx,
+              void *o, int o_dtype, const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
+              int32_t Hk, int32_t Hv, int32_t K, int32_t V, float scale, int l2norm_qk,
+              void *workspace, size_t workspace_bytes, void *stream, const char *name) {
+  if (K != DK || V != DV) return fail(GDN_ERR_UNSUPPORTED, "%s: K=%d V=%d; only K=V=128 is built", name, K, V);
   if (qkv_dtype != GDN_DTYPE_BF16)
-    return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd: q/k/v must be bf16 (MFMA operands)");
+    return fail(GDN_ERR_UNSUPPORTED, "%s: q/k/v must be bf16 (MFMA operands)", name);
   if (n_seqs < 0 || T < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk)
-    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_chunk_fwd: bad sizes n_seqs=%d T=%d Hk=%d Hv=%d", n_seqs, T, Hk, Hv);
-  if (!valid_dtype(beta_dtype)) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_chunk_fwd: bad beta dtype");
+    return fail(GDN_ERR_INVALID_ARGUMENT, "%s: bad sizes n_seqs=%d T=%d Hk=%d Hv=%d", name, n_seqs, T, Hk, Hv);
+  if (!valid_dtype(gate.dt)) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: bad gate dtype", name);
   if (o_dtype != GDN_DTYPE_BF16 && o_dtype != GDN_DTYPE_F32)
-    return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd: output must be bf16 or fp32");
+    return fail(GDN_ERR_UNSUPPORTED, "%s: output must be bf16 or fp32", name);
   if (n_seqs == 0) return ok();
-  if (!q || !k || !v || !g || !beta || !o) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_chunk_fwd: null q/k/v/g/beta/o");
+  if (!q || !k || !v || !gate.g_or_a || !gate.beta_or_b || !o)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "%s: null q/k/v/gate/o", name);
+  if (gate.A_log && !gate.dt_bias) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: null dt_bias", name);
+  if (gate.stride < Hv) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: gate token stride smaller than Hv", name);
   if (q_stride_t < Hk * K || k_stride_t < Hk * K || v_stride_t < Hv * V || (q_stride_t | k_stride_t | v_stride_t) % 8)
-    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_chunk_fwd: token strides must cover a row and be multiples of 8");
+    return fail(GDN_ERR_INVALID_ARGUMENT, "%s: token strides must cover a row and be multiples of 8", name);
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) % 16)
-    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_chunk_fwd: q/k/v must be 16-byte aligned");
+    return fail(GDN_ERR_INVALID_ARGUMENT, "%s: q/k/v must be 16-byte aligned", name);
   const int64_t total = cu_seqlens ? static_cast<int64_t>(T) : static_cast<int64_t>(n_seqs) * T;
   const int64_t nc = max_chunks_of(n_seqs, total, cu_seqlens != nullptr, T);
   const int64_t seg = std::min<int64_t>(nc, SEG_CHUNKS);
   const WsLayout l = ws_layout(n_seqs, seg, Hv, Hk, nc > SEG_CHUNKS);
   if (!workspace || workspace_bytes < l.total)
-    return fail(GDN_ERR_WORKSPACE, "gdn_chunk_fwd: workspace %zu bytes < %zu needed", workspace_bytes, l.total);
+    return fail(GDN_ERR_WORKSPACE, "%s: workspace %zu bytes < %zu needed", name, workspace_bytes, l.total);
   if (reinterpret_cast<uintptr_t>(workspace) % 256)
-    return fail(GDN_ERR_WORKSPACE, "gdn_chunk_fwd: workspace must be 256-byte aligned");
-  if (nc > 65535) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_chunk_fwd: %lld chunks exceed one launch", (long long)nc);
+    return fail(GDN_ERR_WORKSPACE, "%s: workspace must be 256-byte aligned", name);
+  if (nc > 65535) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: %lld chunks exceed one launch", name, (long long)nc);
   const int64_t scan_blocks = static_cast<int64_t>(n_seqs) * Hv * (DV / (16 * SCAN_WAVES));
-  if (scan_blocks > 0x7fffffff) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_chunk_fwd: grid too large");
+  if (scan_blocks > 0x7fffffff) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: grid too large", name);
   char *ws = static_cast<char *>(workspace);
   ChunkArgs a{static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
-              q_stride_t, k_stride_t, v_stride_t, g, beta, beta_dtype, h0, h0_idx, hT, hT_idx, o, o_dtype,
+              q_stride_t, k_stride_t, v_stride_t, gate, h0, h0_idx, hT, hT_idx, o, o_dtype,
               cu_seqlens, n_seqs, T, Hk, Hv, total, scale, l2norm_qk, static_cast<int>(nc), 0, 0,
               reinterpret_cast<int32_t *>(ws + l.chunk_start), nullptr, nullptr, nullptr,
               reinterpret_cast<float *>(ws + l.carry)};
@@ -1009,7 +988,7 @@ extern "C" int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qk
     set_segment(0);
     if (seg > 0) launch_prep(s);
     launch_scan(s);
-    return check_launch("gdn_chunk_fwd");
+    return check_launch(name);
   }
   // Several segments: segment k + 1 is prepared on the side stream while
   // segment k is scanned on the caller's stream.  prep(k + 1) writes buffer
@@ -1039,6 +1018,43 @@ extern "C" int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qk
     launch_scan(s);
     rc |= hipEventRecord(ev[R + kseg % R], s) != hipSuccess;
   }
-  if (rc) return fail(GDN_ERR_LAUNCH, "gdn_chunk_fwd: stream event hand-off failed");
-  return check_launch("gdn_chunk_fwd");
+  if (rc) return fail(GDN_ERR_LAUNCH, "%s: stream event hand-off failed", name);
+  return check_launch(name);
+}
+
+}  // namespace
+}  // namespace gdn
+
+extern "C" int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
+                             int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
+                             const float *g, const void *beta, int beta_dtype,
+                             const float *h0, const int64_t *h0_idx,
+                             float *hT, const int64_t *hT_idx,
+                             void *o, int o_dtype,
+                             const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
+                             int32_t Hk, int32_t Hv, int32_t K, int32_t V,
+                             float scale, int l2norm_qk,
+                             void *workspace, size_t workspace_bytes, void *stream) {
+  const gdn::GateArgs gate{g, beta, beta_dtype, Hv, nullptr, nullptr};
+  return gdn::chunk_fwd(q, k, v, qkv_dtype, q_stride_t, k_stride_t, v_stride_t, gate, h0, h0_idx, hT, hT_idx, o,
+                        o_dtype, cu_seqlens, n_seqs, T, Hk, Hv, K, V, scale, l2norm_qk, workspace, workspace_bytes,
+                        stream, "gdn_chunk_fwd");
+}
+
+extern "C" int gdn_chunk_fwd_gated(const void *q, const void *k, const void *v, int qkv_dtype,
+                                   int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
+                                   const void *a, const void *b, int ab_dtype, int64_t ab_stride_t,
+                                   const float *A_log, const float *dt_bias,
+                                   const float *h0, const int64_t *h0_idx,
+                                   float *hT, const int64_t *hT_idx,
+                                   void *o, int o_dtype,
+                                   const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
+                                   int32_t Hk, int32_t Hv, int32_t K, int32_t V,
+                                   float scale, int l2norm_qk,
+                                   void *workspace, size_t workspace_bytes, void *stream) {
+  if (!A_log) return gdn::fail(GDN_ERR_INVALID_ARGUMENT, "gdn_chunk_fwd_gated: null A_log");
+  const gdn::GateArgs gate{a, b, ab_dtype, ab_stride_t, A_log, dt_bias};
+  return gdn::chunk_fwd(q, k, v, qkv_dtype, q_stride_t, k_stride_t, v_stride_t, gate, h0, h0_idx, hT, hT_idx, o,
+                        o_dtype, cu_seqlens, n_seqs, T, Hk, Hv, K, V, scale, l2norm_qk, workspace, workspace_bytes,
+                        stream, "gdn_chunk_fwd_gated");
 }

@@ -51,6 +51,47 @@ __device__ __forceinline__ void store_elem(void *p, int64_t i, int dt, float x) 
   }
 }
 
+// Gate inputs of one (token, v-head).  Precomputed: g (fp32 log-decay) and
+// beta (dtype `dt`), both [tokens, Hv] with token stride `stride`.  Raw (the
+// HF Qwen3.5 GDN layer's projections, engine reference: the layer forward
+// computes them before the kernel, transformers modeling_qwen3_5_moe.py:495-497):
+//   beta = sigmoid(b),  g = -exp(A_log[h]) * softplus(a + dt_bias[h]),
+// softplus(x) = x for x > 20 (torch's threshold), log1p(e^x) otherwise; a and b
+// in dtype `dt`, A_log and dt_bias fp32 [Hv].  Raw mode when A_log is set.
+struct GateArgs {
+  const void *g_or_a;
+  const void *beta_or_b;
+  int dt;
+  int64_t stride;
+  const float *A_log;
+  const float *dt_bias;
+};
+__device__ __forceinline__ void load_gates(const GateArgs &ga, int64_t tok, int h, float *g, float *beta) {
+  const int64_t i = tok * ga.stride + h;
+  if (ga.A_log) {
+    const float x = load_elem(ga.g_or_a, i, ga.dt) + ga.dt_bias[h];
+    const float sp = x > 20.f ? x : log1pf(expf(x));
+    *g = -expf(ga.A_log[h]) * sp;
+    *beta = 1.f / (1.f + expf(-load_elem(ga.beta_or_b, i, ga.dt)));
+  } else {
+    *g = static_cast<const float *>(ga.g_or_a)[i];
+    *beta = load_elem(ga.beta_or_b, i, ga.dt);
+  }
+}
+
+// Sum over the 16 lanes of a DPP row (every lane receives the sum).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_mov<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_mov<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp_mov<0x141>(x);  // row_half_mirror
+  x += dpp_mov<0x140>(x);  // row_mirror
+  return x;
+}
+
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);

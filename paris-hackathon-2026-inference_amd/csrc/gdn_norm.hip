@@ -1,0 +1,145 @@
+// Gated RMS norm of the GDN core output (HF RMSNormGated,
+// transformers modeling_qwen3_5_moe.py:169-185, applied at :535-538):
+//   y = weight * x * rsqrt(mean(x^2) + eps) * silu(z)    per (token, head) row
+// One pass over HBM (x, z in, y out) instead of the module's chain of
+// elementwise torch ops.  Arithmetic in fp32, one rounding to y's dtype
+// (the module rounds x * rsqrt(.) to the input dtype before the weight; the
+// difference is within one output ulp).
+#include "gdn_common.h"
+
+namespace gdn {
+namespace {
+
+constexpr int ND = 128;          // row length (v head dim)
+constexpr int ROWS_PER_WG = 16;  // 16 lanes x 8 values per row, 4 rows per wave
+
+struct NormArgs {
+  const void *x, *z, *w;
+  void *y;
+  int x_dt, z_dt, w_dt, y_dt;
+  int64_t xs, zs, ys;  // token strides (elements)
+  int64_t rows;        // tokens * H
+  int H;
+  float eps;
+};
+
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
+
+// 8 consecutive values of dtype dt starting at element i (16-byte aligned for
+// 2-byte types, 32-byte for fp32).
+__device__ __forceinline__ void load8(const void *p, int64_t i, int dt, float (&v)[8]) {
+  if (dt == GDN_DTYPE_F32) {
+    const u32x4 a = *reinterpret_cast<const u32x4 *>(static_cast<const float *>(p) + i);
+    const u32x4 b = *reinterpret_cast<const u32x4 *>(static_cast<const float *>(p) + i + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = __uint_as_float(a[e]);
+      v[4 + e] = __uint_as_float(b[e]);
+    }
+  } else {
+    const u32x4 a = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(p) + i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (dt == GDN_DTYPE_BF16) {
+        v[2 * e] = bf16_bits_to_f32(a[e] & 0xffffu);
+        v[2 * e + 1] = bf16_bits_to_f32(a[e] >> 16);
+      } else {
+        v[2 * e] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(a[e] & 0xffffu)));
+        v[2 * e + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(a[e] >> 16)));
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ void store8(void *p, int64_t i, int dt, const float (&v)[8]) {
+  if (dt == GDN_DTYPE_F32) {
+    u32x4 a, b;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a[e] = __float_as_uint(v[e]);
+      b[e] = __float_as_uint(v[4 + e]);
+    }
+    *reinterpret_cast<u32x4 *>(static_cast<float *>(p) + i) = a;
+    *reinterpret_cast<u32x4 *>(static_cast<float *>(p) + i + 4) = b;
+  } else {
+    u32x4 a;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint32_t lo, hi;
+      if (dt == GDN_DTYPE_BF16) {
+        lo = f32_to_bf16_bits(v[2 * e]);
+        hi = f32_to_bf16_bits(v[2 * e + 1]);
+      } else {
+        lo = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v[2 * e]));
+        hi = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v[2 * e + 1]));
+      }
+      a[e] = lo | (hi << 16);
+    }
+    *reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(p) + i) = a;
+  }
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_gated_kernel(NormArgs a) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * ROWS_PER_WG + (threadIdx.x >> 4);
+  const int c0 = (threadIdx.x & 15) * 8;  // this lane's 8 columns
+  const bool valid = row < a.rows;        // (all lanes take part in the row reduction)
+  const int64_t t = valid ? row / a.H : 0;
+  const int hh = valid ? static_cast<int>(row % a.H) : 0;
+  float x[8], z[8], w[8];
+  if (valid) {
+    load8(a.x, t * a.xs + static_cast<int64_t>(hh) * ND + c0, a.x_dt, x);
+    load8(a.z, t * a.zs + static_cast<int64_t>(hh) * ND + c0, a.z_dt, z);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = z[e] = 0.f;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) w[e] = load_elem(a.w, c0 + e, a.w_dt);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+  ss = row16_sum(ss);
+  const float r = rsqrtf(ss * (1.f / ND) + a.eps);
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = w[e] * (x[e] * r) * (z[e] / (1.f + expf(-z[e])));
+  if (valid) store8(a.y, t * a.ys + static_cast<int64_t>(hh) * ND + c0, a.y_dt, y);
+}
+
+bool aligned_rows(const void *p, int dt, int64_t stride) {
+  const int64_t unit = 8;  // rows start on 8-element boundaries: 16 bytes (2-byte types) or 32 (fp32)
+  const size_t align = dt == GDN_DTYPE_F32 ? 32 : 16;
+  return reinterpret_cast<uintptr_t>(p) % align == 0 && stride % unit == 0;
+}
+
+}  // namespace
+}  // namespace gdn
+
+extern "C" int gdn_rmsnorm_gated_fwd(const void *x, int x_dtype, int64_t x_stride_t,
+                                     const void *z, int z_dtype, int64_t z_stride_t,
+                                     const void *weight, int w_dtype,
+                                     void *y, int y_dtype, int64_t y_stride_t,
+                                     int64_t n_tokens, int32_t H, int32_t D, float eps, void *stream) {
+  using namespace gdn;
+  if (D != ND) return fail(GDN_ERR_UNSUPPORTED, "gdn_rmsnorm_gated_fwd: D=%d; only D=128 is built", D);
+  if (n_tokens < 0 || H <= 0) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_rmsnorm_gated_fwd: bad sizes");
+  if (!valid_dtype(x_dtype) || !valid_dtype(z_dtype) || !valid_dtype(w_dtype) || !valid_dtype(y_dtype))
+    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_rmsnorm_gated_fwd: bad dtype");
+  if (!(eps >= 0.f)) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_rmsnorm_gated_fwd: eps must be >= 0");
+  if (n_tokens == 0) return ok();
+  if (!x || !z || !weight || !y) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_rmsnorm_gated_fwd: null pointer");
+  const int64_t row_len = static_cast<int64_t>(H) * D;
+  if (x_stride_t < row_len || z_stride_t < row_len || y_stride_t < row_len)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_rmsnorm_gated_fwd: token stride smaller than H*D");
+  if (!aligned_rows(x, x_dtype, x_stride_t) || !aligned_rows(z, z_dtype, z_stride_t) ||
+      !aligned_rows(y, y_dtype, y_stride_t))
+    return fail(GDN_ERR_INVALID_ARGUMENT,
+                "gdn_rmsnorm_gated_fwd: x/z/y must be 16-byte (32 for fp32) aligned with strides multiple of 8");
+  const int64_t rows = n_tokens * H;
+  const int64_t blocks = (rows + ROWS_PER_WG - 1) / ROWS_PER_WG;
+  if (blocks > 0x7fffffff) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_rmsnorm_gated_fwd: grid too large");
+  NormArgs a{x, z, weight, y, x_dtype, z_dtype, w_dtype, y_dtype, x_stride_t, z_stride_t, y_stride_t, rows, H, eps};
+  hipLaunchKernelGGL(rmsnorm_gated_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch("gdn_rmsnorm_gated_fwd");
+}

@@ -27,8 +27,7 @@ constexpr int VD = 128;  // head dim of v (columns of the state)
 struct RecArgs {
   const void *q, *k, *v;
   int64_t qs, ks, vs;  // token strides (elements)
-  const float *g;
-  const void *beta;
+  GateArgs gate;
   const float *state_in;
   const int64_t *in_idx;
   float *state_out;
@@ -40,7 +39,7 @@ struct RecArgs {
   int64_t total;
   float scale;
   int l2norm;
-  int qkv_dt, beta_dt, o_dt;
+  int qkv_dt, o_dt;
 };
 
 template <int VT>
@@ -109,8 +108,9 @@ __global__ __launch_bounds__(2 * VT) void recurrent_kernel(RecArgs a) {
       ks_l[2 * lane + 1] = k1 * rk;
     }
     const float qk = sqk * qsc * rk;
-    const float eg = expf(a.g[tok * a.Hv + h]);
-    const float bt = load_elem(a.beta, tok * a.Hv + h, a.beta_dt);
+    float gl, bt;
+    load_gates(a.gate, tok, h, &gl, &bt);
+    const float eg = expf(gl);
     float vv[4];
     const int64_t voff = tok * a.vs + (int64_t)h * VD + col0;
 #pragma unroll
@@ -195,6 +195,47 @@ __global__ __launch_bounds__(2 * VT) void recurrent_kernel(RecArgs a) {
 }  // namespace
 }  // namespace gdn
 
+namespace gdn {
+namespace {
+
+int recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
+                  int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t, const GateArgs &gate,
+                  const float *state_in, const int64_t *state_in_idx,
+                  float *state_out, const int64_t *state_out_idx,
+                  void *o, int o_dtype, float *snapshots,
+                  const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
+                  int32_t Hk, int32_t Hv, int32_t K, int32_t V,
+                  float scale, int l2norm_qk, void *stream, const char *name) {
+  if (K != KD || V != VD)
+    return fail(GDN_ERR_UNSUPPORTED, "%s: K=%d V=%d; only K=V=128 is built", name, K, V);
+  if (n_seqs < 0 || T < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "%s: bad sizes n_seqs=%d T=%d Hk=%d Hv=%d", name, n_seqs, T, Hk, Hv);
+  if (!valid_dtype(qkv_dtype) || !valid_dtype(gate.dt) || !valid_dtype(o_dtype))
+    return fail(GDN_ERR_INVALID_ARGUMENT, "%s: bad dtype", name);
+  if (n_seqs == 0) return ok();
+  if (!q || !k || !v || !gate.g_or_a || !gate.beta_or_b || !o)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "%s: null q/k/v/gate/o", name);
+  if (gate.A_log && !gate.dt_bias) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: null dt_bias", name);
+  if (gate.stride < Hv) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: gate token stride smaller than Hv", name);
+  if (snapshots && cu_seqlens)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "%s: snapshots need equal-length sequences", name);
+  if (q_stride_t < Hk * K || k_stride_t < Hk * K || v_stride_t < Hv * V)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "%s: token stride smaller than a row", name);
+  const int64_t n_blocks = static_cast<int64_t>(n_seqs) * Hv * (VD / 32);
+  if (n_blocks > 0x7fffffff) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: grid too large", name);
+
+  RecArgs a{q, k, v, q_stride_t, k_stride_t, v_stride_t, gate, state_in, state_in_idx,
+            state_out, state_out_idx, o, snapshots, cu_seqlens, n_seqs, T, Hk, Hv,
+            cu_seqlens ? static_cast<int64_t>(T) : static_cast<int64_t>(n_seqs) * T,
+            scale, l2norm_qk, qkv_dtype, o_dtype};
+  hipLaunchKernelGGL(recurrent_kernel<32>, dim3(static_cast<unsigned>(n_blocks)), dim3(64), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch(name);
+}
+
+}  // namespace
+}  // namespace gdn
+
 extern "C" int gdn_recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
                                  int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
                                  const float *g, const void *beta, int beta_dtype,
@@ -204,29 +245,25 @@ extern "C" int gdn_recurrent_fwd(const void *q, const void *k, const void *v, in
                                  const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
                                  int32_t Hk, int32_t Hv, int32_t K, int32_t V,
                                  float scale, int l2norm_qk, void *stream) {
-  using namespace gdn;
-  if (K != KD || V != VD)
-    return fail(GDN_ERR_UNSUPPORTED, "gdn_recurrent_fwd: K=%d V=%d; only K=V=128 is built", K, V);
-  if (n_seqs < 0 || T < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk)
-    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_recurrent_fwd: bad sizes n_seqs=%d T=%d Hk=%d Hv=%d",
-                n_seqs, T, Hk, Hv);
-  if (!valid_dtype(qkv_dtype) || !valid_dtype(beta_dtype) || !valid_dtype(o_dtype))
-    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_recurrent_fwd: bad dtype");
-  if (n_seqs == 0) return ok();
-  if (!q || !k || !v || !g || !beta || !o)
-    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_recurrent_fwd: null q/k/v/g/beta/o");
-  if (snapshots && cu_seqlens)
-    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_recurrent_fwd: snapshots need equal-length sequences");
-  if (q_stride_t < Hk * K || k_stride_t < Hk * K || v_stride_t < Hv * V)
-    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_recurrent_fwd: token stride smaller than a row");
-  const int64_t n_blocks = static_cast<int64_t>(n_seqs) * Hv * (VD / 32);
-  if (n_blocks > 0x7fffffff) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_recurrent_fwd: grid too large");
+  const gdn::GateArgs gate{g, beta, beta_dtype, Hv, nullptr, nullptr};
+  return gdn::recurrent_fwd(q, k, v, qkv_dtype, q_stride_t, k_stride_t, v_stride_t, gate, state_in, state_in_idx,
+                            state_out, state_out_idx, o, o_dtype, snapshots, cu_seqlens, n_seqs, T, Hk, Hv, K, V,
+                            scale, l2norm_qk, stream, "gdn_recurrent_fwd");
+}
 
-  RecArgs a{q, k, v, q_stride_t, k_stride_t, v_stride_t, g, beta, state_in, state_in_idx,
-            state_out, state_out_idx, o, snapshots, cu_seqlens, n_seqs, T, Hk, Hv,
-            cu_seqlens ? static_cast<int64_t>(T) : static_cast<int64_t>(n_seqs) * T,
-            scale, l2norm_qk, qkv_dtype, beta_dtype, o_dtype};
-  hipLaunchKernelGGL(recurrent_kernel<32>, dim3(static_cast<unsigned>(n_blocks)), dim3(64), 0,
-                     static_cast<hipStream_t>(stream), a);
-  return check_launch("gdn_recurrent_fwd");
+extern "C" int gdn_recurrent_fwd_gated(const void *q, const void *k, const void *v, int qkv_dtype,
+                                       int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
+                                       const void *a, const void *b, int ab_dtype, int64_t ab_stride_t,
+                                       const float *A_log, const float *dt_bias,
+                                       const float *state_in, const int64_t *state_in_idx,
+                                       float *state_out, const int64_t *state_out_idx,
+                                       void *o, int o_dtype, float *snapshots,
+                                       const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
+                                       int32_t Hk, int32_t Hv, int32_t K, int32_t V,
+                                       float scale, int l2norm_qk, void *stream) {
+  if (!A_log) return gdn::fail(GDN_ERR_INVALID_ARGUMENT, "gdn_recurrent_fwd_gated: null A_log");
+  const gdn::GateArgs gate{a, b, ab_dtype, ab_stride_t, A_log, dt_bias};
+  return gdn::recurrent_fwd(q, k, v, qkv_dtype, q_stride_t, k_stride_t, v_stride_t, gate, state_in, state_in_idx,
+                            state_out, state_out_idx, o, o_dtype, snapshots, cu_seqlens, n_seqs, T, Hk, Hv, K, V,
+                            scale, l2norm_qk, stream, "gdn_recurrent_fwd_gated");
 }

@@ -11,13 +11,22 @@ third-party packages (fla, causal-conv1d) via HF:
 - ``recurrent_gated_delta_rule``        HF-signature adapter of the above
 - ``causal_conv1d_fn``, ``causal_conv1d_update``
 - ``gdn_state_commit``, ``LinearAttentionSlotPool``
+- ``chunk_gated_delta_rule_from_projections``,
+  ``fused_recurrent_gated_delta_rule_from_projections``  gates computed in
+  the kernels from the layer's raw a / b projections
+- ``rms_norm_gated``                    the GDN output norm in one pass
+- ``gated_delta_net_forward``, ``install_gdn_layer_patch``  HF's GDN layer
+  forward on these kernels (native GQA, fused gates and norm)
 
 All of them run hand-written HIP kernels from ``libgdn_mi355x.so`` through
 a C ABI (include/gdn_capi.h); there is no CPU or Triton fallback.
 """
 from .causal_conv1d import causal_conv1d_fn, causal_conv1d_update
-from .delta_rule import chunk_gated_delta_rule, install_delta_rule_monkeypatch
-from .fused_recurrent import fused_recurrent_gated_delta_rule, recurrent_gated_delta_rule
+from .delta_rule import (chunk_gated_delta_rule, chunk_gated_delta_rule_from_projections,
+                         install_delta_rule_monkeypatch)
+from .fused_recurrent import (fused_recurrent_gated_delta_rule, fused_recurrent_gated_delta_rule_from_projections,
+                              recurrent_gated_delta_rule)
+from .gdn_layer import gated_delta_net_forward, install_gdn_layer_patch, rms_norm_gated
 from .state_pool import LinearAttentionSlotPool, gdn_state_commit
 
 __all__ = [
@@ -29,4 +38,9 @@ __all__ = [
     "causal_conv1d_update",
     "gdn_state_commit",
     "LinearAttentionSlotPool",
+    "chunk_gated_delta_rule_from_projections",
+    "fused_recurrent_gated_delta_rule_from_projections",
+    "rms_norm_gated",
+    "gated_delta_net_forward",
+    "install_gdn_layer_patch",
 ]

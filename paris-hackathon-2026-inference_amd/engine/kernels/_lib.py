@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libgdn_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 GDN_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
@@ -53,6 +53,35 @@ SIGNATURES = {
         _f32, _int,
         _c_void_p, _size, _c_void_p]),              # workspace, bytes, stream
     "gdn_chunk_workspace_bytes": (_size, [_i32, _i64, _i32, _i32, _i32]),
+    "gdn_recurrent_fwd_gated": (_int, [
+        _c_void_p, _c_void_p, _c_void_p, _int,      # q k v qkv_dtype
+        _i64, _i64, _i64,                           # token strides
+        _c_void_p, _c_void_p, _int, _i64,           # a b ab_dtype ab_stride
+        _c_void_p, _c_void_p,                       # A_log dt_bias
+        _c_void_p, _c_void_p,                       # state_in, state_in_idx
+        _c_void_p, _c_void_p,                       # state_out, state_out_idx
+        _c_void_p, _int, _c_void_p,                 # o, o_dtype, snapshots
+        _c_void_p, _i32, _i32,                      # cu_seqlens n_seqs T
+        _i32, _i32, _i32, _i32,                     # Hk Hv K V
+        _f32, _int, _c_void_p]),                    # scale l2norm stream
+    "gdn_chunk_fwd_gated": (_int, [
+        _c_void_p, _c_void_p, _c_void_p, _int,
+        _i64, _i64, _i64,
+        _c_void_p, _c_void_p, _int, _i64,           # a b ab_dtype ab_stride
+        _c_void_p, _c_void_p,                       # A_log dt_bias
+        _c_void_p, _c_void_p,                       # h0, h0_idx
+        _c_void_p, _c_void_p,                       # hT, hT_idx
+        _c_void_p, _int,                            # o, o_dtype
+        _c_void_p, _i32, _i32,
+        _i32, _i32, _i32, _i32,
+        _f32, _int,
+        _c_void_p, _size, _c_void_p]),              # workspace, bytes, stream
+    "gdn_rmsnorm_gated_fwd": (_int, [
+        _c_void_p, _int, _i64,                      # x x_dtype x_stride
+        _c_void_p, _int, _i64,                      # z z_dtype z_stride
+        _c_void_p, _int,                            # weight w_dtype
+        _c_void_p, _int, _i64,                      # y y_dtype y_stride
+        _i64, _i32, _i32, _f32, _c_void_p]),        # n_tokens H D eps stream
     "causal_conv1d_fwd": (_int, [
         _c_void_p, _i64, _c_void_p, _c_void_p,      # x x_stride w bias
         _c_void_p, _i64,                            # y y_stride
@@ -147,6 +176,19 @@ def token_major(x: torch.Tensor, what: str) -> tuple[torch.Tensor, int]:
     if not ok:
         x = x.contiguous()
         st = h * d
+    return x, st
+
+
+def per_token(x: torch.Tensor, b: int, t: int, h: int, what: str) -> tuple[torch.Tensor, int]:
+    """View a [B, T, H] per-token, per-head tensor (gates, gate projections)
+    as token-major rows; returns (tensor, token stride).  Heads must be
+    contiguous and batches evenly spaced, otherwise a contiguous copy is made."""
+    if tuple(x.shape) != (b, t, h):
+        raise ValueError(f"{what}: expected shape {(b, t, h)}, got {tuple(x.shape)}")
+    st = x.stride(1) if t > 1 else h
+    if not (x.stride(2) == 1 or h == 1) or st < h or (b > 1 and x.stride(0) != t * st):
+        x = x.contiguous()
+        st = h
     return x, st
 
 

@@ -61,16 +61,74 @@ def chunk_gated_delta_rule(
     last_recurrent_state [N, Hv, K, V] fp32 or None)`` as the reference does
     (delta_rule.py:366-374).
     """
+    b, t, hv = value.shape[0], value.shape[1], value.shape[2]
+    _lib.require_gpu(g, beta)
+    g32, _ = _lib.per_token(g.to(torch.float32), b, t, hv, "g")
+    if beta.dtype not in _lib.GDN_DTYPE:
+        beta = beta.float()
+    beta_c, _ = _lib.per_token(beta, b, t, hv, "beta")
+    g32, beta_c = g32.contiguous(), beta_c.contiguous()  # the precomputed-gate ABI takes token stride Hv
+    gates = ("gdn_chunk_fwd", [_lib.ptr(g32), _lib.ptr(beta_c), _lib.dtype_code(beta_c, "beta")])
+    return _chunk(query, key, value, gates, chunk_size, initial_state, output_final_state,
+                  use_qk_l2norm_in_kernel, cu_seqlens, scale, ssm_state_indices, inplace_final_state)
+
+
+def chunk_gated_delta_rule_from_projections(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    A_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    initial_state: Optional[torch.Tensor] = None,
+    output_final_state: bool = False,
+    use_qk_l2norm_in_kernel: bool = True,
+    cu_seqlens: Optional[torch.Tensor] = None,
+    scale: Optional[float] = None,
+    ssm_state_indices: Optional[torch.Tensor] = None,
+    inplace_final_state: bool = False,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """:func:`chunk_gated_delta_rule` with the gates computed inside the
+    kernel from the GDN layer's raw projections (``a``, ``b`` ``[B, T, Hv]``,
+    ``A_log``, ``dt_bias`` ``[Hv]``): beta = sigmoid(b),
+    g = -exp(A_log) * softplus(a + dt_bias), the glue of HF's layer forward
+    (transformers modeling_qwen3_5_moe.py:495-497)."""
+    bsz, t, hv = value.shape[0], value.shape[1], value.shape[2]
+    _lib.require_gpu(a, b, A_log, dt_bias)
+    if a.dtype not in _lib.GDN_DTYPE:
+        a = a.float()
+    if b.dtype != a.dtype:
+        b = b.to(a.dtype)
+    ax, ast = _lib.per_token(a, bsz, t, hv, "a")
+    bx, bst = _lib.per_token(b, bsz, t, hv, "b")
+    if ast != bst:
+        ax, bx, ast = ax.contiguous(), bx.contiguous(), hv
+    alog = A_log.detach().to(torch.float32).reshape(-1).contiguous()
+    dtb = dt_bias.detach().to(torch.float32).reshape(-1).contiguous()
+    if alog.numel() != hv or dtb.numel() != hv:
+        raise ValueError(f"A_log / dt_bias must have {hv} entries")
+    gates = ("gdn_chunk_fwd_gated", [_lib.ptr(ax), _lib.ptr(bx), _lib.dtype_code(ax, "a"), ast,
+                                     _lib.ptr(alog), _lib.ptr(dtb)])
+    keep = (ax, bx, alog, dtb)  # alive until the launch is enqueued
+    out = _chunk(query, key, value, gates, CHUNK_SIZE, initial_state, output_final_state,
+                 use_qk_l2norm_in_kernel, cu_seqlens, scale, ssm_state_indices, inplace_final_state)
+    del keep
+    return out
+
+
+def _chunk(query, key, value, gates, chunk_size, initial_state, output_final_state,
+           use_qk_l2norm_in_kernel, cu_seqlens, scale, ssm_state_indices, inplace_final_state):
+    """Shared body: shape checks, state / workspace plumbing and the launch.
+    ``gates`` = (entry point, its gate arguments)."""
     if chunk_size != CHUNK_SIZE:
         raise ValueError(f"chunk_size={chunk_size}: the MI355X kernels are built for {CHUNK_SIZE} "
                          "(the result does not depend on the chunk size)")
-    dev = _lib.require_gpu(query, key, value, g, beta, initial_state)
+    dev = _lib.require_gpu(query, key, value, initial_state)
     b, t, hk, dk = query.shape
     hv, dv = value.shape[2], value.shape[3]
-    if key.shape != query.shape or value.shape[:2] != (b, t) or g.shape != (b, t, hv) \
-            or beta.shape != (b, t, hv):
-        raise ValueError(f"shape mismatch: q{tuple(query.shape)} k{tuple(key.shape)} "
-                         f"v{tuple(value.shape)} g{tuple(g.shape)} beta{tuple(beta.shape)}")
+    if key.shape != query.shape or value.shape[:2] != (b, t):
+        raise ValueError(f"shape mismatch: q{tuple(query.shape)} k{tuple(key.shape)} v{tuple(value.shape)}")
     if hv % hk:
         raise ValueError(f"Hv={hv} is not a multiple of Hk={hk}")
     if not (query.dtype == key.dtype == value.dtype):
@@ -86,8 +144,6 @@ def chunk_gated_delta_rule(
     qx, qs = _lib.token_major(query, "query")
     kx, ks = _lib.token_major(key, "key")
     vx, vs = _lib.token_major(value, "value")
-    g32 = g.to(torch.float32).contiguous()
-    beta_c = beta.contiguous() if beta.dtype in _lib.GDN_DTYPE else beta.float().contiguous()
 
     idx = _lib.as_index(ssm_state_indices, dev)
     h0 = h0_idx = None
@@ -115,15 +171,16 @@ def chunk_gated_delta_rule(
     ws_bytes = lib.gdn_chunk_workspace_bytes(n_seqs, total, hv, dk, dv)
     ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=dev)
     o = torch.empty((b, t, hv, dv), dtype=query.dtype, device=dev)
-    st = lib.gdn_chunk_fwd(
+    name, gate_args = gates
+    st = getattr(lib, name)(
         _lib.ptr(qx), _lib.ptr(kx), _lib.ptr(vx), _lib.dtype_code(query, "query"), qs, ks, vs,
-        _lib.ptr(g32), _lib.ptr(beta_c), _lib.dtype_code(beta_c, "beta"),
+        *gate_args,
         _lib.ptr(h0), _lib.ptr(h0_idx), _lib.ptr(hT), _lib.ptr(hT_idx),
         _lib.ptr(o), _lib.dtype_code(o, "o"),
         _lib.ptr(cu), n_seqs, total if cu is not None else t,
         hk, hv, dk, dv, float(scale), int(bool(use_qk_l2norm_in_kernel)),
         _lib.ptr(ws), int(ws_bytes), _lib.stream_of(query))
-    _lib.check(st, "gdn_chunk_fwd")
+    _lib.check(st, name)
     return o, final
 
 

@@ -54,14 +54,74 @@ def fused_recurrent_gated_delta_rule(
 
     Returns ``(o [B, T, Hv, V] in q's dtype, final_state or None)``.
     """
-    dev = _lib.require_gpu(q, k, v, g, beta, initial_state, snapshots)
+    _lib.require_gpu(q, g, beta)
     if beta is None:
         beta = torch.ones_like(g)
+    bsz, t, hv = v.shape[0], v.shape[1], v.shape[2]
+    g32, _ = _lib.per_token(g.to(torch.float32), bsz, t, hv, "g")
+    if beta.dtype not in _lib.GDN_DTYPE:
+        beta = beta.float()
+    beta_c, _ = _lib.per_token(beta, bsz, t, hv, "beta")
+    g32, beta_c = g32.contiguous(), beta_c.contiguous()  # the precomputed-gate ABI takes token stride Hv
+    gates = ("gdn_recurrent_fwd", [_lib.ptr(g32), _lib.ptr(beta_c), _lib.dtype_code(beta_c, "beta")])
+    return _recurrent(q, k, v, gates, scale, initial_state, output_final_state, cu_seqlens,
+                      use_qk_l2norm_in_kernel, ssm_state_indices, inplace_final_state, snapshots)
+
+
+def fused_recurrent_gated_delta_rule_from_projections(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    A_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    scale: Optional[float] = None,
+    initial_state: Optional[torch.Tensor] = None,
+    output_final_state: bool = False,
+    cu_seqlens: Optional[torch.Tensor] = None,
+    use_qk_l2norm_in_kernel: bool = True,
+    ssm_state_indices: Optional[torch.Tensor] = None,
+    inplace_final_state: bool = False,
+    snapshots: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """:func:`fused_recurrent_gated_delta_rule` with the gates computed in
+    the kernel from the GDN layer's raw projections: ``a``, ``b``
+    ``[B, T, Hv]``, ``A_log``, ``dt_bias`` ``[Hv]``; beta = sigmoid(b),
+    g = -exp(A_log) * softplus(a + dt_bias) (transformers
+    modeling_qwen3_5_moe.py:495-497)."""
+    bsz, t, hv = v.shape[0], v.shape[1], v.shape[2]
+    _lib.require_gpu(q, a, b, A_log, dt_bias)
+    if a.dtype not in _lib.GDN_DTYPE:
+        a = a.float()
+    if b.dtype != a.dtype:
+        b = b.to(a.dtype)
+    ax, ast = _lib.per_token(a, bsz, t, hv, "a")
+    bx, bst = _lib.per_token(b, bsz, t, hv, "b")
+    if ast != bst:
+        ax, bx, ast = ax.contiguous(), bx.contiguous(), hv
+    alog = A_log.detach().to(torch.float32).reshape(-1).contiguous()
+    dtb = dt_bias.detach().to(torch.float32).reshape(-1).contiguous()
+    if alog.numel() != hv or dtb.numel() != hv:
+        raise ValueError(f"A_log / dt_bias must have {hv} entries")
+    gates = ("gdn_recurrent_fwd_gated", [_lib.ptr(ax), _lib.ptr(bx), _lib.dtype_code(ax, "a"), ast,
+                                         _lib.ptr(alog), _lib.ptr(dtb)])
+    keep = (ax, bx, alog, dtb)  # alive until the launch is enqueued
+    out = _recurrent(q, k, v, gates, scale, initial_state, output_final_state, cu_seqlens,
+                     use_qk_l2norm_in_kernel, ssm_state_indices, inplace_final_state, snapshots)
+    del keep
+    return out
+
+
+def _recurrent(q, k, v, gates, scale, initial_state, output_final_state, cu_seqlens,
+               use_qk_l2norm_in_kernel, ssm_state_indices, inplace_final_state, snapshots):
+    """Shared body: shape checks, state plumbing and the launch.
+    ``gates`` = (entry point, its gate arguments)."""
+    dev = _lib.require_gpu(q, k, v, initial_state, snapshots)
     b, t, hk, dk = q.shape
     hv, dv = v.shape[2], v.shape[3]
-    if k.shape != q.shape or v.shape[:2] != (b, t) or g.shape != (b, t, hv) or beta.shape != (b, t, hv):
-        raise ValueError(f"shape mismatch: q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)} "
-                         f"g{tuple(g.shape)} beta{tuple(beta.shape)}")
+    if k.shape != q.shape or v.shape[:2] != (b, t):
+        raise ValueError(f"shape mismatch: q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
     if hv % hk:
         raise ValueError(f"Hv={hv} is not a multiple of Hk={hk}")
     if not (q.dtype == k.dtype == v.dtype):
@@ -77,8 +137,6 @@ def fused_recurrent_gated_delta_rule(
     qx, qs = _lib.token_major(q, "q")
     kx, ks = _lib.token_major(k, "k")
     vx, vs = _lib.token_major(v, "v")
-    g32 = g.to(torch.float32).contiguous()
-    beta_c = beta.contiguous() if beta.dtype in _lib.GDN_DTYPE else beta.float().contiguous()
 
     idx = _lib.as_index(ssm_state_indices, dev)
     state_in = state_out = None
@@ -114,14 +172,15 @@ def fused_recurrent_gated_delta_rule(
 
     o = torch.empty((b, t, hv, dv), dtype=q.dtype, device=dev)
     lib = _lib.load()
-    st = lib.gdn_recurrent_fwd(
+    name, gate_args = gates
+    st = getattr(lib, name)(
         _lib.ptr(qx), _lib.ptr(kx), _lib.ptr(vx), _lib.dtype_code(q, "q"), qs, ks, vs,
-        _lib.ptr(g32), _lib.ptr(beta_c), _lib.dtype_code(beta_c, "beta"),
+        *gate_args,
         _lib.ptr(state_in), _lib.ptr(in_idx), _lib.ptr(state_out), _lib.ptr(out_idx),
         _lib.ptr(o), _lib.dtype_code(o, "o"), _lib.ptr(snapshots),
         _lib.ptr(cu), n_seqs, total if cu is not None else t,
         hk, hv, dk, dv, float(scale), int(bool(use_qk_l2norm_in_kernel)), _lib.stream_of(q))
-    _lib.check(st, "gdn_recurrent_fwd")
+    _lib.check(st, name)
     return o, final
 
 

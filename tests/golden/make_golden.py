@@ -9,9 +9,10 @@ fixtures for the GDN path.  Its math is reached through third-party code:
   engine/runtime/cuda_graphs.py:126-135 as the torch decode path;
 * ``causal_conv1d_fn`` / ``causal_conv1d_update`` -- the torch conv paths HF's
   GDN layer falls back to (reference call sites kv_cache.py:153-156,
-  cuda_graphs.py:202).
+  cuda_graphs.py:202);
+* ``Qwen3_5MoeRMSNormGated`` -- the GDN output norm of the same layer.
 
-All four live in transformers' ``models/qwen3_5_moe/modeling_qwen3_5_moe.py``.
+All of them live in transformers' ``models/qwen3_5_moe/modeling_qwen3_5_moe.py``.
 The container has transformers 5.15.0 installed (the reference's uv.lock pins
 4.57.6, but its code needs >= 5.5, engine/model/qwen3_next.py:4-5).  This
 script calls those functions on small seeded inputs and saves inputs and
@@ -81,6 +82,19 @@ def conv_cases(out):
                 "conv_upd.state_after": st_after})
 
 
+def norm_case(out):
+    """HF's RMSNormGated module (the GDN output norm) on fp32 inputs."""
+    gen = torch.Generator().manual_seed(21)
+    mod = hf.Qwen3_5MoeRMSNormGated(128, eps=1e-6)
+    with torch.no_grad():
+        mod.weight.copy_(bf16r(1.0 + 0.3 * torch.randn(128, generator=gen)))
+    x = bf16r(torch.randn(6, 4, 128, generator=gen))
+    z = bf16r(2.0 * torch.randn(6, 4, 128, generator=gen))
+    with torch.no_grad():
+        y = mod(x, z)
+    out.update({"norm_gated.x": x, "norm_gated.z": z, "norm_gated.w": mod.weight.detach(), "norm_gated.y": y})
+
+
 def main():
     torch.manual_seed(0)
     out: dict[str, torch.Tensor] = {}
@@ -93,6 +107,7 @@ def main():
     x = bf16r(torch.randn(3, 5, 128))
     out["l2norm.x"] = x
     out["l2norm.y"] = hf.l2norm(x, dim=-1, eps=1e-6)
+    norm_case(out)
     np.savez_compressed(OUT, **{k: v.detach().cpu().numpy().astype(np.float32) for k, v in out.items()})
     print(f"wrote {OUT}: {len(out)} arrays")
 

@@ -29,7 +29,8 @@ def lib():
 def test_header_lists_the_entry_points():
     assert header_functions() == sorted([
         "causal_conv1d_fwd", "causal_conv1d_update", "gdn_abi_version", "gdn_chunk_fwd",
-        "gdn_chunk_workspace_bytes", "gdn_last_error_string", "gdn_recurrent_fwd", "gdn_state_commit"])
+        "gdn_chunk_fwd_gated", "gdn_chunk_workspace_bytes", "gdn_last_error_string", "gdn_recurrent_fwd",
+        "gdn_recurrent_fwd_gated", "gdn_rmsnorm_gated_fwd", "gdn_state_commit"])
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -40,7 +41,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.gdn_abi_version() == _lib.ABI_VERSION == 1
+    assert lib.gdn_abi_version() == _lib.ABI_VERSION == 2
 
 
 def _rec_call(lib, **over):
@@ -114,3 +115,42 @@ def test_product_path_never_imports_the_oracle():
             if f.endswith(".py"):
                 src = open(os.path.join(root, f)).read()
                 assert "import oracle" not in src and "from oracle" not in src, f
+
+
+def _rec_gated_call(lib, **over):
+    args = dict(q=1, k=1, v=1, qkv_dtype=1, qs=4096, ks=4096, vs=4096, a=1, b=1, ab_dtype=1, ab_stride=32,
+                A_log=1, dt_bias=1, sin=None, sin_idx=None, sout=None, sout_idx=None, o=1, o_dtype=1,
+                snap=None, cu=None, n=2, t=1, hk=32, hv=32, kd=128, vd=128, scale=0.1, l2=1, stream=None)
+    args.update(over)
+    return lib.gdn_recurrent_fwd_gated(*args.values())
+
+
+def test_gated_entry_points_check_their_gate_arguments(lib):
+    assert _rec_gated_call(lib, A_log=None) == 1
+    assert "A_log" in lib.gdn_last_error_string().decode()
+    assert _rec_gated_call(lib, dt_bias=None) == 1
+    assert _rec_gated_call(lib, ab_stride=16) == 1         # stride below Hv
+    assert _rec_gated_call(lib, ab_dtype=7) == 1
+    assert _rec_gated_call(lib, kd=64, vd=64) == 2
+    # chunk variant: same gate checks ahead of its own (A_log, then workspace)
+    chunk = dict(q=256, k=256, v=256, qkv_dtype=1, qs=4096, ks=4096, vs=4096, a=1, b=1, ab_dtype=1, ab_stride=32,
+                 A_log=None, dt_bias=1, h0=None, h0_idx=None, hT=None, hT_idx=None, o=1, o_dtype=1,
+                 cu=None, n=1, t=64, hk=16, hv=32, kd=128, vd=128, scale=0.1, l2=1,
+                 ws=None, ws_bytes=0, stream=None)
+    assert lib.gdn_chunk_fwd_gated(*chunk.values()) == 1
+    chunk.update(A_log=1)
+    assert lib.gdn_chunk_fwd_gated(*chunk.values()) == 3   # workspace missing
+
+
+def test_rmsnorm_gated_rejects_bad_arguments(lib):
+    def call(**over):
+        args = dict(x=256, xdt=1, xs=4096, z=256, zdt=1, zs=4096, w=256, wdt=1, y=256, ydt=1, ys=4096,
+                    n=4, h=32, d=128, eps=1e-6, stream=None)
+        args.update(over)
+        return lib.gdn_rmsnorm_gated_fwd(*args.values())
+    assert call(d=64) == 2
+    assert call(x=None) == 1
+    assert call(xs=100) == 1                               # stride below H*D
+    assert call(x=8) == 1                                  # misaligned rows
+    assert call(eps=-1.0) == 1
+    assert call(n=0) == 0                                  # nothing to do

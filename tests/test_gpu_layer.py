@@ -1,0 +1,168 @@
+"""Row f-1 on the MI355X: the GDN layer glue fused into the kernels.
+
+* gates from raw projections (beta = sigmoid(b), g = -exp(A_log) softplus(a +
+  dt_bias), transformers modeling_qwen3_5_moe.py:495-497) inside the chunk and
+  recurrent kernels, against the oracle's gates + recurrence;
+* the gated RMS norm kernel against the oracle (pinned by HF's module);
+* the whole layer forward (``gated_delta_net_forward``: native GQA, fused
+  gates, HIP conv / core / norm) against HF's own ``Qwen3_5MoeGatedDeltaNet``
+  forward run in fp32 on the CPU with the same (bf16-representable) weights
+  and inputs, for a prefill and for cached decode steps.
+
+Tolerances: core outputs bf16 max abs error <= 2e-2 and fp32 states relative
+error <= 1e-3 (north star); the layer output, after five bf16 roundings of
+intermediate tensors on the GPU path, max abs error <= 3e-2 * max|ref|.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gdn
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not torch.cuda.is_available(), reason="needs an MI355X")]
+
+DEV = "cuda"
+O_TOL, S_TOL, LAYER_TOL = 2e-2, 1e-3, 3e-2
+
+
+def np64(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def bf16r(t):
+    return t.to(torch.bfloat16).to(torch.float32)
+
+
+def raw_gates(gen, b, t, hv):
+    a = bf16r(torch.randn(b, t, hv, generator=gen))
+    bb = bf16r(torch.randn(b, t, hv, generator=gen))
+    A_log = torch.log(torch.empty(hv).uniform_(0.5, 16.0, generator=gen))
+    dt_bias = torch.randn(hv, generator=gen)
+    return a, bb, A_log, dt_bias
+
+
+def test_chunk_from_projections_matches_oracle():
+    from engine.kernels import chunk_gated_delta_rule_from_projections
+    gen = torch.Generator().manual_seed(31)
+    t, hk, hv = 200, 16, 32
+    q = torch.randn(1, t, hk, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(1, t, hk, 128, generator=gen).to(torch.bfloat16)
+    v = torch.randn(1, t, hv, 128, generator=gen).to(torch.bfloat16)
+    a, b, A_log, dt_bias = raw_gates(gen, 1, t, hv)
+    a = a * 0.5 - 3.0  # moderate decays so the state carries across chunks
+    h0 = torch.randn(1, hv, 128, 128, generator=gen) * 0.1
+    o, s = chunk_gated_delta_rule_from_projections(
+        q.to(DEV), k.to(DEV), v.to(DEV), a.to(torch.bfloat16).to(DEV), b.to(torch.bfloat16).to(DEV),
+        A_log.to(DEV), dt_bias.to(DEV), initial_state=h0.to(DEV), output_final_state=True)
+    g, beta = gdn.gdn_gates(np64(a.to(torch.bfloat16)), np64(b.to(torch.bfloat16)), np64(A_log), np64(dt_bias))
+    o_ref, s_ref = gdn.chunk_gated_delta_rule(np64(q), np64(k), np64(v), g, beta, initial_state=np64(h0))
+    err_o, err_s = np.abs(np64(o) - o_ref).max(), gdn.state_rel_err(np64(s), s_ref)
+    print(f"chunk gated: max|o-o_ref|={err_o:.3e} state rel={err_s:.3e}")
+    assert err_o < O_TOL and err_s < S_TOL
+
+
+def test_recurrent_from_projections_matches_oracle_on_a_slot_pool():
+    from engine.kernels import fused_recurrent_gated_delta_rule_from_projections
+    gen = torch.Generator().manual_seed(32)
+    bsz, hk, hv, slots = 8, 16, 32, 12
+    q = torch.randn(bsz, 1, hk, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(bsz, 1, hk, 128, generator=gen).to(torch.bfloat16)
+    v = torch.randn(bsz, 1, hv, 128, generator=gen).to(torch.bfloat16)
+    a, b, A_log, dt_bias = raw_gates(gen, bsz, 1, hv)
+    pool = torch.randn(slots, hv, 128, 128, generator=gen) * 0.1
+    slot_ids = torch.randperm(slots, generator=gen)[:bsz]
+    pool_gpu = pool.to(DEV)
+    o, _ = fused_recurrent_gated_delta_rule_from_projections(
+        q.to(DEV), k.to(DEV), v.to(DEV), a.to(DEV), b.to(DEV), A_log.to(DEV), dt_bias.to(DEV),
+        initial_state=pool_gpu, ssm_state_indices=slot_ids.to(DEV), inplace_final_state=True)
+    g, beta = gdn.gdn_gates(np64(a), np64(b), np64(A_log), np64(dt_bias))
+    o_ref, s_ref = gdn.recurrent_gated_delta_rule(np64(q), np64(k), np64(v), g, beta,
+                                                  initial_state=np64(pool)[slot_ids.numpy()])
+    assert np.abs(np64(o) - o_ref).max() < O_TOL
+    assert gdn.state_rel_err(np64(pool_gpu[slot_ids.to(DEV)]), s_ref) < S_TOL
+    untouched = np.setdiff1d(np.arange(slots), slot_ids.numpy())
+    assert torch.equal(pool_gpu[untouched].cpu(), pool[untouched])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rms_norm_gated_matches_oracle(dtype):
+    from engine.kernels import rms_norm_gated
+    gen = torch.Generator().manual_seed(33)
+    t, h = 37, 32
+    x = (torch.randn(t, h, 128, generator=gen) * 3.0).to(dtype)
+    zz = torch.randn(t, 2 * h * 128, generator=gen).to(dtype)   # z as a strided view of a packed projection
+    z = zz[:, h * 128:].view(t, h, 128)
+    w = (1.0 + 0.3 * torch.randn(128, generator=gen)).to(dtype)
+    y = rms_norm_gated(x.to(DEV), zz.to(DEV)[:, h * 128:].view(t, h, 128), w.to(DEV), eps=1e-6)
+    assert y.dtype == dtype and y.shape == x.shape
+    y_ref = gdn.rms_norm_gated(np64(x), np64(z), np64(w), eps=1e-6)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert np.abs(np64(y) - y_ref).max() < tol * max(1.0, np.abs(y_ref).max())
+
+
+# ---------------------------------------------------------------- the HF layer
+def tiny_layer():
+    from transformers.models.qwen3_5_moe.configuration_qwen3_5_moe import Qwen3_5MoeTextConfig
+    from transformers.models.qwen3_5_moe import modeling_qwen3_5_moe as hf
+    cfg = Qwen3_5MoeTextConfig(hidden_size=64, num_hidden_layers=1, layer_types=["linear_attention"],
+                               linear_num_key_heads=2, linear_num_value_heads=4, linear_key_head_dim=128,
+                               linear_value_head_dim=128, linear_conv_kernel_dim=4, rms_norm_eps=1e-6)
+    torch.manual_seed(34)
+    layer = hf.Qwen3_5MoeGatedDeltaNet(cfg, layer_idx=0).eval()
+    with torch.no_grad():
+        for p in layer.parameters():
+            p.copy_(bf16r(p))
+        layer.norm.weight.copy_(bf16r(1.0 + 0.2 * torch.randn(128)))
+        layer.dt_bias.copy_(bf16r(torch.randn(4)))
+        layer.A_log.copy_(bf16r(torch.log(torch.empty(4).uniform_(0.5, 4.0))))
+    return cfg, hf, layer
+
+
+def hf_torch_paths_intact(hf):
+    # the reference run below must use HF's own torch paths, not patched ones
+    from engine import kernels
+    return all(getattr(hf, n) is not getattr(kernels, m, None) for n, m in (
+        ("torch_chunk_gated_delta_rule", "chunk_gated_delta_rule"),
+        ("torch_recurrent_gated_delta_rule", "recurrent_gated_delta_rule"),
+        ("causal_conv1d_fn", "causal_conv1d_fn"), ("causal_conv1d_update", "causal_conv1d_update")))
+
+
+def test_layer_prefill_matches_hf_module():
+    from engine.kernels import gated_delta_net_forward
+    cfg, hf, layer = tiny_layer()
+    if not hf_torch_paths_intact(hf):
+        pytest.skip("HF module functions were patched in this process")
+    x = bf16r(torch.randn(1, 150, 64, generator=torch.Generator().manual_seed(35)))
+    with torch.no_grad():
+        y_ref = layer(x)                                   # HF forward, fp32, CPU
+        gpu = layer.to(DEV, torch.bfloat16)
+        y = gated_delta_net_forward(gpu, x.to(DEV, torch.bfloat16))
+    err = np.abs(np64(y) - np64(y_ref)).max()
+    print(f"layer prefill: max|y-y_ref|={err:.3e} max|y_ref|={np64(y_ref).__abs__().max():.3e}")
+    assert err < LAYER_TOL * np.abs(np64(y_ref)).max()
+
+
+def test_layer_decode_with_cache_matches_hf_module():
+    from transformers.cache_utils import DynamicCache
+    from engine.kernels import gated_delta_net_forward
+    cfg, hf, layer = tiny_layer()
+    if not hf_torch_paths_intact(hf):
+        pytest.skip("HF module functions were patched in this process")
+    gen = torch.Generator().manual_seed(36)
+    steps = [bf16r(torch.randn(2, 70, 64, generator=gen))] + \
+        [bf16r(torch.randn(2, 1, 64, generator=gen)) for _ in range(3)]
+    cache_ref = DynamicCache(config=cfg)
+    with torch.no_grad():
+        y_ref = [layer(s, cache_params=cache_ref) for s in steps]   # prefill, then 3 cached decode steps
+        gpu = layer.to(DEV, torch.bfloat16)
+        cache = DynamicCache(config=cfg)
+        y = [gated_delta_net_forward(gpu, s.to(DEV, torch.bfloat16), cache_params=cache) for s in steps]
+    for i, (a, r) in enumerate(zip(y, y_ref)):
+        err = np.abs(np64(a) - np64(r)).max()
+        print(f"layer step {i}: max|y-y_ref|={err:.3e}")
+        assert err < LAYER_TOL * np.abs(np64(r)).max(), i
+    s_ref = np64(cache_ref.layers[0].recurrent_states[0])
+    s_gpu = np64(cache.layers[0].recurrent_states[0])
+    assert gdn.state_rel_err(s_gpu, s_ref) < 1e-2   # states after bf16 projections and conv
+    assert np.abs(np64(cache.layers[0].conv_states[0]) - np64(cache_ref.layers[0].conv_states[0])).max() < 2e-2

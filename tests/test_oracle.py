@@ -258,3 +258,35 @@ def test_conv_varlen_equals_per_sequence():
         yi, fi = conv.causal_conv1d_fn(x[cu[i]:cu[i + 1]].T[None], w, initial_state=h0[i:i + 1])
         assert np.allclose(y[cu[i]:cu[i + 1]], yi[0].T)
         assert np.array_equal(fin[i], fi[0])
+
+
+# --------------------------------------------------------------------- layer glue (row f-1)
+def test_rms_norm_gated_matches_hf_golden(golden):
+    a = golden_case(golden, "norm_gated")
+    y = gdn.rms_norm_gated(a["x"], a["z"], a["w"], eps=1e-6)
+    assert np.abs(y - a["y"]).max() < 2e-6 * max(1.0, np.abs(a["y"]).max())
+
+
+def test_rms_norm_gated_invariants():
+    rng = np.random.default_rng(3)
+    x, z, w = rng.standard_normal((5, 128)), rng.standard_normal((5, 128)), rng.standard_normal(128)
+    y = gdn.rms_norm_gated(x, z, w, eps=0.0)
+    assert np.allclose(gdn.rms_norm_gated(7.5 * x, z, w, eps=0.0), y)   # scale-free in x
+    ones = gdn.rms_norm_gated(x, np.full_like(z, 40.0), np.ones(128), eps=0.0)
+    assert np.allclose(np.sqrt((ones * ones).mean(-1)), 40.0)           # silu(40) = 40: rms = 40
+    assert np.allclose(gdn.rms_norm_gated(x, np.zeros_like(z), w), 0.0)  # silu(0) = 0
+
+
+def test_gates_closed_forms():
+    A_log = np.log(np.array([1.0, 2.0, 0.5]))
+    dt = np.array([0.0, 1.0, -1.0])
+    g, beta = gdn.gdn_gates(np.array([[0.0, -1.0, 1.0]]), np.array([[0.0, 100.0, -100.0]]), A_log, dt)
+    assert np.allclose(g, -np.exp(A_log) * np.log(2.0))   # a + dt_bias = 0 everywhere
+    assert np.allclose(beta, [[0.5, 1.0, 0.0]])
+    big = gdn.gdn_gates(np.array([30.0]), np.array([0.0]), np.array([0.0]), np.array([0.0]))[0]
+    assert np.allclose(big, -30.0)                         # softplus threshold: identity above 20
+    small = gdn.gdn_gates(np.array([-30.0]), np.array([0.0]), np.array([0.0]), np.array([0.0]))[0]
+    assert np.allclose(small, -np.exp(-30.0), rtol=1e-9)   # softplus(x) ~ e^x far below 0
+    a = np.linspace(-5, 5, 11)
+    g_line = gdn.gdn_gates(a, np.zeros_like(a), np.zeros(1), np.zeros(1))[0]
+    assert np.all(np.diff(g_line) < 0) and np.all(g_line < 0)   # decay strengthens with a
