@@ -19,6 +19,9 @@ The JSON line also carries
                 dense-equivalent flop rate against the 2.5 PFLOP/s bf16 peak
                 (q/k at 16 heads; prefill_qk_repeated: q/k repeated to 32 heads
                 as HF passes them);
+  layer_glue    the GDN layer glue around the prefill core at configuration 2's
+                shape: HF's torch glue (gates, q/k repeat, RMSNormGated) vs
+                the fused kernels, and the gated-norm kernel's HBM rate;
   cpu_baseline  the CPU oracle (numpy fp32, sequences split over the host's
                 cores) on a bounded sample of the same decode workload.
 """
@@ -55,6 +58,8 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill measurements")
     ap.add_argument("--no-prefill-repeated", action="store_true",
                     help="skip the prefill timing with q/k repeated to 32 heads")
+    ap.add_argument("--no-layer-glue", action="store_true",
+                    help="skip the fused vs torch layer-glue timing (gates, q/k repeat, gated norm)")
     ap.add_argument("--pools", type=int, default=4, help="rotating decode state pools")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 128 MiB device copy (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -178,6 +183,75 @@ def bench_prefill(torch, reps=20, warmup=3, repeat_qk=False):
                      "frac": flop / per / MFMA_BF16_PEAK, "flop_per_call": flop}}
 
 
+def _time(torch, fn, reps, warmup=3):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / reps
+
+
+def bench_layer_glue(torch, reps=20):
+    """Configuration 2's shape through the GDN layer glue (row f-1): the glue as
+    HF's layer forward runs it in torch around the core (gates,
+    modeling_qwen3_5_moe.py:495-497; q/k repeat_interleave, :498-500;
+    RMSNormGated, :169-185 / :535-538) versus the fused path (gates in the
+    chunk kernel's prologue, native 16-head q/k, one-pass norm kernel)."""
+    import torch.nn.functional as F
+    from engine import configs
+    from engine.kernels import chunk_gated_delta_rule, chunk_gated_delta_rule_from_projections, rms_norm_gated
+
+    c = configs.config2()
+    dev = torch.device("cuda", 0)
+    q, k, v = (c[x].to(dev) for x in ("q", "k", "v"))
+    t, hv = v.shape[1], v.shape[2]
+    gen = torch.Generator().manual_seed(41)
+    a = torch.randn(1, t, hv, generator=gen).to(dev, torch.bfloat16)
+    b = torch.randn(1, t, hv, generator=gen).to(dev, torch.bfloat16)
+    A_log = torch.log(torch.empty(hv).uniform_(1, 16, generator=gen)).to(dev)
+    dt_bias = torch.randn(hv, generator=gen).to(dev)
+    z = torch.randn(1, t, hv, 128, generator=gen).to(dev, torch.bfloat16)
+    w = (1 + 0.2 * torch.randn(128, generator=gen)).to(dev, torch.bfloat16)
+
+    def torch_norm(x, gate):  # the module's steps (fp32 variance, weight in the input dtype, silu gate)
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)
+        return (w * xf.to(x.dtype) * F.silu(gate.float())).to(x.dtype)
+
+    def glue_torch():
+        beta = b.sigmoid()
+        g = -A_log.float().exp() * F.softplus(a.float() + dt_bias)
+        rep = hv // q.shape[2]
+        o, s = chunk_gated_delta_rule(q.repeat_interleave(rep, dim=2), k.repeat_interleave(rep, dim=2), v, g, beta,
+                                      output_final_state=True, use_qk_l2norm_in_kernel=True)
+        return torch_norm(o.reshape(-1, 128), z.reshape(-1, 128)), s
+
+    def glue_fused():
+        o, s = chunk_gated_delta_rule_from_projections(q, k, v, a, b, A_log, dt_bias, output_final_state=True)
+        return rms_norm_gated(o, z, w), s
+
+    o_ref = glue_torch()[0].reshape(1, t, hv, 128).float()
+    y = glue_fused()[0].float()
+    dev_err = ((y - o_ref).abs().max() / o_ref.abs().max()).item()
+    t_torch, t_fused = _time(torch, glue_torch, reps), _time(torch, glue_fused, reps)
+    x0 = torch.randn(1, t, hv, 128, generator=gen).to(dev, torch.bfloat16)
+    t_norm = _time(torch, lambda: rms_norm_gated(x0, z, w), 100)
+    t_norm_torch = _time(torch, lambda: torch_norm(x0.reshape(-1, 128), z.reshape(-1, 128)), 100)
+    norm_bytes = 3 * x0.numel() * 2  # x, z in, y out (bf16)
+    return {"config": "configuration 2 shape (T=4096, Hk=16, Hv=32, d=128), bf16; a, b [T, 32] bf16, z [T, 32, 128]",
+            "torch_glue_us": t_torch * 1e6, "fused_us": t_fused * 1e6, "speedup": t_torch / t_fused,
+            "max_diff_vs_torch_glue_rel_to_max": dev_err,
+            "rmsnorm_gated": {"us": t_norm * 1e6, "torch_us": t_norm_torch * 1e6,
+                              "achieved_GBps": norm_bytes / t_norm / 1e9, "peak_GBps": HBM_PEAK / 1e9,
+                              "frac": norm_bytes / t_norm / HBM_PEAK, "bytes": norm_bytes}}
+
+
 def cpu_baseline(budget_s=12.0):
     """CPU oracle (numpy fp32) on a bounded sample of the decode workload, sequences
     split across the host cores this process may use."""
@@ -252,6 +326,8 @@ def main():
         out["prefill"] = bench_prefill(torch)
         if not args.no_prefill_repeated:
             out["prefill_qk_repeated"] = bench_prefill(torch, repeat_qk=True)
+        if not args.no_layer_glue:
+            out["layer_glue"] = bench_layer_glue(torch)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

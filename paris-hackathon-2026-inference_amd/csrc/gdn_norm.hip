@@ -18,7 +18,7 @@ struct NormArgs {
   void *y;
   int x_dt, z_dt, w_dt, y_dt;
   int64_t xs, zs, ys;  // token strides (elements)
-  int64_t rows;        // tokens * H
+  int64_t rows;        // tokens * H (informational)
   int H;
   float eps;
 };
@@ -79,13 +79,15 @@ __device__ __forceinline__ void store8(void *p, int64_t i, int dt, const float (
   }
 }
 
+// Grid: x = token, y = group of 16 heads.  A workgroup normalises 16 rows
+// of one token; 16 lanes per row, 8 values per lane.
 __global__ __launch_bounds__(256) void rmsnorm_gated_kernel(NormArgs a) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * ROWS_PER_WG + (threadIdx.x >> 4);
+  const int64_t t = blockIdx.x;
+  const int hh = static_cast<int>(blockIdx.y) * ROWS_PER_WG + static_cast<int>(threadIdx.x >> 4);
   const int c0 = (threadIdx.x & 15) * 8;  // this lane's 8 columns
-  const bool valid = row < a.rows;        // (all lanes take part in the row reduction)
-  const int64_t t = valid ? row / a.H : 0;
-  const int hh = valid ? static_cast<int>(row % a.H) : 0;
+  const bool valid = hh < a.H;            // (all lanes take part in the row reduction)
   float x[8], z[8], w[8];
+  load8(a.w, c0, a.w_dt, w);
   if (valid) {
     load8(a.x, t * a.xs + static_cast<int64_t>(hh) * ND + c0, a.x_dt, x);
     load8(a.z, t * a.zs + static_cast<int64_t>(hh) * ND + c0, a.z_dt, z);
@@ -93,8 +95,6 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_kernel(NormArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = z[e] = 0.f;
   }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) w[e] = load_elem(a.w, c0 + e, a.w_dt);
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_kernel(NormArgs a) {
   const float r = rsqrtf(ss * (1.f / ND) + a.eps);
   float y[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) y[e] = w[e] * (x[e] * r) * (z[e] / (1.f + expf(-z[e])));
+  for (int e = 0; e < 8; ++e) y[e] = w[e] * (x[e] * r) * (z[e] / (1.f + __expf(-z[e])));
   if (valid) store8(a.y, t * a.ys + static_cast<int64_t>(hh) * ND + c0, a.y_dt, y);
 }
 
@@ -135,11 +135,13 @@ extern "C" int gdn_rmsnorm_gated_fwd(const void *x, int x_dtype, int64_t x_strid
       !aligned_rows(y, y_dtype, y_stride_t))
     return fail(GDN_ERR_INVALID_ARGUMENT,
                 "gdn_rmsnorm_gated_fwd: x/z/y must be 16-byte (32 for fp32) aligned with strides multiple of 8");
-  const int64_t rows = n_tokens * H;
-  const int64_t blocks = (rows + ROWS_PER_WG - 1) / ROWS_PER_WG;
-  if (blocks > 0x7fffffff) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_rmsnorm_gated_fwd: grid too large");
-  NormArgs a{x, z, weight, y, x_dtype, z_dtype, w_dtype, y_dtype, x_stride_t, z_stride_t, y_stride_t, rows, H, eps};
-  hipLaunchKernelGGL(rmsnorm_gated_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), a);
+  if (n_tokens > 0x7fffffff || H > 65535 * ROWS_PER_WG)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_rmsnorm_gated_fwd: grid too large");
+  if (reinterpret_cast<uintptr_t>(weight) % (w_dtype == GDN_DTYPE_F32 ? 32 : 16))
+    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_rmsnorm_gated_fwd: weight must be 16-byte (32 for fp32) aligned");
+  NormArgs a{x, z, weight, y, x_dtype, z_dtype, w_dtype, y_dtype, x_stride_t, z_stride_t, y_stride_t,
+             n_tokens * H, H, eps};
+  const dim3 grid(static_cast<unsigned>(n_tokens), static_cast<unsigned>((H + ROWS_PER_WG - 1) / ROWS_PER_WG));
+  hipLaunchKernelGGL(rmsnorm_gated_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
   return check_launch("gdn_rmsnorm_gated_fwd");
 }

@@ -61,6 +61,8 @@ def rms_norm_gated(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: 
     if w.dtype not in _lib.GDN_DTYPE:
         w = w.float()
     w = w.contiguous()
+    if w.data_ptr() % 32:  # the kernel reads the weight as 16-byte (fp32: 32-byte) vectors
+        w = w.clone()
     n_tok, h = x4.shape[1], x4.shape[2]
     y = torch.empty((n_tok, h, d), dtype=out_dtype, device=dev)
     lib = _lib.load()
