@@ -543,22 +543,23 @@ __device__ __forceinline__ void load_u(f32x4 (&u)[4], __amdgpu_buffer_rsrc_t r, 
     u[p] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + p * 1024, 0, 0));
 }
 
-// Output of one chunk: lane (g, c) holds rows 16p + 4g + e of its column.  The
-// buffer resource starts at the chunk's first token and ends after its last
-// valid row, so stores past the sequence end are dropped by the hardware
-// range check (which covers the VGPR offset: voff0 + row * row_bytes, with
-// voff0 the byte offset of row 4g of this lane's column).
+// Output of one chunk, this wave's two row tiles: lane (g, c) holds rows
+// 16pp + 4g + e (pp < 2) of its output half.  The buffer resource starts at the
+// chunk's first token and ends after its last valid row, so stores past the
+// sequence end are dropped by the hardware range check (which covers the VGPR
+// offset: voff0 + row * row_bytes, voff0 = byte offset of row 4g of this
+// lane's column in this wave's half).
 template <bool BF16_OUT>
-__device__ __forceinline__ void store_chunk(const f32x4 (&o)[4], __amdgpu_buffer_rsrc_t r, int voff0, int row_bytes) {
+__device__ __forceinline__ void store_chunk(const f32x4 (&o)[2], __amdgpu_buffer_rsrc_t r, int voff0, int row_bytes) {
 #pragma unroll
-  for (int p = 0; p < 4; ++p)
+  for (int pp = 0; pp < 2; ++pp)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int off = voff0 + (16 * p + e) * row_bytes;
+      const int off = voff0 + (16 * pp + e) * row_bytes;
       if constexpr (BF16_OUT)
-        __builtin_amdgcn_raw_buffer_store_b16(bf16_rne(o[p][e]), r, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b16(bf16_rne(o[pp][e]), r, off, 0, 0);
       else
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, o[p][e]), r, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, o[pp][e]), r, off, 0, 0);
     }
 }
 
@@ -567,25 +568,44 @@ constexpr int SG_VALU = 0x2, SG_MFMA = 0x8, SG_VMEM_RD = 0x20, SG_VMEM_WR = 0x40
 #define GDN_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 #define GDN_GROUP(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
 
-// One chunk of the scan for this wave's 16 state columns, in three
-// scheduling regions.  The scan runs one wave per SIMD, so the vector ALU
-// work is interleaved with the MFMAs by hand (sched_group_barrier patterns):
-//   R1  V' = U - W S            16 MFMAs | S *= e^{gamma_63}, previous chunk's
-//                                          output stores; reads Q, scales
-//   R2  acc = Q S               16 MFMAs | V' to bf16, V'' = sk V' split hi + lo;
-//                                          reads A, K^T
-//   R3  S += K^T V'' (hi, lo)   32 MFMAs | O = sq acc, then O += A V' (6 MFMAs),
-//                                          next chunk's bf16 state operands
-// sb holds the state as bf16 B operands (k-steps over the 128 state rows);
-// on return it holds the updated state, o holds this chunk's output.
-template <int NW, bool BF16_OUT>
-__device__ __forceinline__ void scan_chunk(const u32x4 *st, const f32x4 (&u)[4], f32x4 (&S)[8], bf16x8 (&sb)[4],
-                                           f32x4 (&o)[4], __amdgpu_buffer_rsrc_t prev_out, int voff0, int row_bytes,
-                                           u32x4 *st_next, const StageSrc &src_next, f32x4 (&u_next)[4],
-                                           __amdgpu_buffer_rsrc_t u_rsrc_next, int u_voff, int wave, int lane) {
+// The scan is K-split: a pair of waves shares 16 state columns, wave X of
+// the pair (X = 0, 1) keeping state rows 64X..64X+63 (tiles 4X..4X+3) in its
+// MFMA accumulators and writing output rows 32X..32X+31.  The two halves of
+// the state are exchanged as bf16 MFMA operands through LDS at the chunk
+// barrier, so each wave sees the whole state and computes the full
+// V' = U - W S (its state update needs V' at all 64 positions), its own rows
+// of O and its own half of the state update.  A wave reads 39 KiB of operands
+// from LDS per chunk (W 16, Q 8, K^T 8, A <= 4, scales, the partner's state
+// 2) instead of the 62 KiB of an unsplit 16-column wave, and one wave's LDS
+// read rate (about 25 B/clk) is what bounds a chunk.
+//
+// One chunk in three scheduling regions (VALU work interleaved with the
+// MFMAs by sched_group_barrier patterns; the scan runs one wave per SIMD):
+//   R1  V' = U - W S (all rows)   16 MFMAs | S *= e^{gamma_63}, previous chunk's
+//                                           output stores, U prefetch, stage copies
+//   R2  acc = Q S (own rows)       8 MFMAs | V' to bf16, V'' = sk V' split hi + lo,
+//                                           stage copies
+//   R3  S += K^T V'' (own rows)   16 MFMAs | O = sq acc + A V' (2 or 4 MFMAs),
+//                                           next chunk's bf16 state half
+// sbh / sbp: this wave's / the partner's bf16 state half (k-steps 2X, 2X+1 /
+// the other two); on return sbh holds the updated half, o this chunk's rows.
+template <int NW, int X, bool BF16_OUT>
+__device__ __forceinline__ void scan_chunk(const u32x4 *st, const f32x4 (&u)[4], f32x4 (&S)[4], bf16x8 (&sbh)[2],
+                                           const bf16x8 (&sbp)[2], f32x4 (&o)[2], __amdgpu_buffer_rsrc_t prev_out,
+                                           int voff0, int row_bytes, u32x4 *st_next, const StageSrc &src_next,
+                                           f32x4 (&u_next)[4], __amdgpu_buffer_rsrc_t u_rsrc_next, int u_voff,
+                                           int wave, int lane) {
+  // copies issued in R1 | R2 (measured: all in R1 stalls R1 on the vector-
+  // memory queue; in R3 they land after the chunk ends)
+  constexpr int D1 = Dma<NW>::n / 2, D2 = Dma<NW>::n;
+  constexpr int NA = X ? 4 : 2;                        // A blocks of this wave's output rows
   const int g4 = lane >> 4;
   const float *sc = reinterpret_cast<const float *>(st + ST_SC);
-  constexpr int D1 = Dma<NW>::n / 2, D2 = Dma<NW>::n;  // copies issued in R1 | R2 (R3 none: its copies would land late)
+  bf16x8 sb[4];  // the whole state as bf16 B operands, by k-step
+  sb[2 * X] = sbh[0];
+  sb[2 * X + 1] = sbh[1];
+  sb[2 - 2 * X] = sbp[0];
+  sb[3 - 2 * X] = sbp[1];
 
   // ---- R1
   u32x4 wb[16];
@@ -595,12 +615,23 @@ __device__ __forceinline__ void scan_chunk(const u32x4 *st, const f32x4 (&u)[4],
 #pragma unroll
   for (int p = 0; p < 4; ++p) vp[p] = u[p];
   const float eL = sc[2 * CK];
-  u32x4 qb[16];
+  u32x4 qb[8], ab[NA];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) qb[i] = st[ST_Q + i * 64 + lane];
-  f32x4 sk[4];
+  for (int pp = 0; pp < 2; ++pp)
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) qb[4 * pp + s2] = st[ST_Q + (4 * (2 * X + pp) + s2) * 64 + lane];
+  if constexpr (X == 0) {  // rows p = 0, 1: A blocks (0, 0) and (1, 0)
+    ab[0] = st[ST_A + 0 * 64 + lane];
+    ab[1] = st[ST_A + 2 * 64 + lane];
+  } else {                 // rows p = 2, 3: A blocks (2, 0), (2, 1), (3, 0), (3, 1)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ab[i] = st[ST_A + (4 + i) * 64 + lane];
+  }
+  f32x4 sk[4], sq[2];
 #pragma unroll
   for (int p = 0; p < 4; ++p) sk[p] = *reinterpret_cast<const f32x4 *>(sc + CK + 16 * p + 4 * g4);
+#pragma unroll
+  for (int pp = 0; pp < 2; ++pp) sq[pp] = *reinterpret_cast<const f32x4 *>(sc + 16 * (2 * X + pp) + 4 * g4);
   store_chunk<BF16_OUT>(o, prev_out, voff0, row_bytes);
   load_u(u_next, u_rsrc_next, u_voff);
 #pragma unroll
@@ -610,40 +641,33 @@ __device__ __forceinline__ void scan_chunk(const u32x4 *st, const f32x4 (&u)[4],
 #pragma unroll
     for (int p = 0; p < 4; ++p) vp[p] = mfma(as_bf16x8(wb[4 * p + s2]), sb[s2], vp[p]);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) S[i] = S[i] * eL;
-  GDN_GROUP(SG_DS_RD, 17);
+  for (int t = 0; t < 4; ++t) S[t] = S[t] * eL;
+  GDN_GROUP(SG_DS_RD, 16);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     GDN_GROUP(SG_MFMA, 1);
     GDN_GROUP(SG_DS_RD, 1);
-    GDN_GROUP(SG_VALU, 3);
+    GDN_GROUP(SG_VALU, 2);
     GDN_GROUP(SG_VMEM_WR, 1);
     GDN_GROUP(SG_VMEM_RD, 1);
   }
   GDN_SCHED_FENCE();
 
   // ---- R2
-  u32x4 ab[6], kb[16];  // A blocks 0, 2, 4, 5, 6, 7 (the others are zero); K^T tiles
-  ab[0] = st[ST_A + 0 * 64 + lane];
-  ab[1] = st[ST_A + 2 * 64 + lane];
-  ab[2] = st[ST_A + 4 * 64 + lane];
-  ab[3] = st[ST_A + 5 * 64 + lane];
-  ab[4] = st[ST_A + 6 * 64 + lane];
-  ab[5] = st[ST_A + 7 * 64 + lane];
+  u32x4 kb[8];  // K^T tiles 4X + t, k-steps s: block 2 (4X + t) + s
 #pragma unroll
-  for (int i = 0; i < 16; ++i) kb[i] = st[ST_KT + i * 64 + lane];
-  f32x4 sq[4];
+  for (int t = 0; t < 4; ++t)
 #pragma unroll
-  for (int p = 0; p < 4; ++p) sq[p] = *reinterpret_cast<const f32x4 *>(sc + 16 * p + 4 * g4);
+    for (int s2 = 0; s2 < 2; ++s2) kb[2 * t + s2] = st[ST_KT + (2 * (4 * X + t) + s2) * 64 + lane];
 #pragma unroll
   for (int i = D1; i < D2; ++i) dma_copy<NW>(i, st_next, src_next, wave, lane);
-  f32x4 acc[4];
+  f32x4 acc[2];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) acc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int pp = 0; pp < 2; ++pp) acc[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s2 = 0; s2 < 4; ++s2)
 #pragma unroll
-    for (int p = 0; p < 4; ++p) acc[p] = mfma(as_bf16x8(qb[4 * p + s2]), sb[s2], acc[p]);
+    for (int pp = 0; pp < 2; ++pp) acc[pp] = mfma(as_bf16x8(qb[4 * pp + s2]), sb[s2], acc[pp]);
   bf16x8 vb[2], vh[2], vl[2];
   vb[0] = pack_hi(vp[0], vp[1]);
   vb[1] = pack_hi(vp[2], vp[3]);
@@ -651,54 +675,61 @@ __device__ __forceinline__ void scan_chunk(const u32x4 *st, const f32x4 (&u)[4],
   for (int p2 = 0; p2 < 2; ++p2)  // V'' = diag(e^{gamma_63 - gamma} nk) V', hi + lo
     pack_hilo(vp[2 * p2] * sk[2 * p2], vp[2 * p2 + 1] * sk[2 * p2 + 1], vh[p2], vl[p2]);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < 8; ++i) {
     GDN_GROUP(SG_MFMA, 1);
-    GDN_GROUP(SG_DS_RD, 2);
-    GDN_GROUP(SG_VALU, 4);
+    GDN_GROUP(SG_DS_RD, 1);
+    GDN_GROUP(SG_VALU, 6);
     GDN_GROUP(SG_VMEM_RD, 1);
   }
   GDN_SCHED_FENCE();
 
   // ---- R3
 #pragma unroll
-  for (int half = 0; half < 2; ++half)
+  for (int s2 = 0; s2 < 2; ++s2) {
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
+    for (int t = 0; t < 4; ++t) S[t] = mfma(as_bf16x8(kb[2 * t + s2]), vh[s2], S[t]);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) S[4 * half + t] = mfma(as_bf16x8(kb[2 * (4 * half + t) + s2]), vh[s2], S[4 * half + t]);
+    for (int t = 0; t < 4; ++t) S[t] = mfma(as_bf16x8(kb[2 * t + s2]), vl[s2], S[t]);
+  }
 #pragma unroll
-      for (int t = 0; t < 4; ++t) S[4 * half + t] = mfma(as_bf16x8(kb[2 * (4 * half + t) + s2]), vl[s2], S[4 * half + t]);
-    }
+  for (int pp = 0; pp < 2; ++pp) o[pp] = acc[pp] * sq[pp];
+  if constexpr (X == 0) {
+    o[0] = mfma(as_bf16x8(ab[0]), vb[0], o[0]);
+    o[1] = mfma(as_bf16x8(ab[1]), vb[0], o[1]);
+  } else {
+    o[0] = mfma(as_bf16x8(ab[0]), vb[0], o[0]);
+    o[1] = mfma(as_bf16x8(ab[2]), vb[0], o[1]);
+    o[0] = mfma(as_bf16x8(ab[1]), vb[1], o[0]);
+    o[1] = mfma(as_bf16x8(ab[3]), vb[1], o[1]);
+  }
+  sbh[0] = pack_hi(S[0], S[1]);
+  sbh[1] = pack_hi(S[2], S[3]);
 #pragma unroll
-  for (int p = 0; p < 4; ++p) o[p] = acc[p] * sq[p];
-  o[0] = mfma(as_bf16x8(ab[0]), vb[0], o[0]);
-  o[1] = mfma(as_bf16x8(ab[1]), vb[0], o[1]);
-  o[2] = mfma(as_bf16x8(ab[2]), vb[0], o[2]);
-  o[3] = mfma(as_bf16x8(ab[4]), vb[0], o[3]);
-  o[2] = mfma(as_bf16x8(ab[3]), vb[1], o[2]);
-  o[3] = mfma(as_bf16x8(ab[5]), vb[1], o[3]);
-#pragma unroll
-  for (int s2 = 0; s2 < 4; ++s2) sb[s2] = pack_hi(S[2 * s2], S[2 * s2 + 1]);
-#pragma unroll
-  for (int i = D2; i < Dma<NW>::n; ++i) dma_copy<NW>(i, st_next, src_next, wave, lane);
-#pragma unroll
-  for (int i = 0; i < 38; ++i) {
+  for (int i = 0; i < 16 + NA; ++i) {
     GDN_GROUP(SG_MFMA, 1);
     GDN_GROUP(SG_VALU, 1);
-    GDN_GROUP(SG_VMEM_RD, 1);
   }
   GDN_SCHED_FENCE();
 }
 
-// Workgroup = NW waves = 16*NW state columns of one (sequence, v-head).  The
-// two LDS stages leave room for one workgroup per CU, so each SIMD runs one
-// wave and may use the whole register file.
+// Workgroup = NW waves = NW/2 column slices x 2 state-row halves = 8 NW
+// state columns of one (sequence, v-head).  The two LDS stages and the state
+// exchange leave room for one workgroup per CU, so each wave has a SIMD and
+// the whole register file to itself.  Measured on MI355X at T=4096, 32
+// v-heads: 2 waves (256 workgroups, one per CU) 88 us, 4 waves 96 us; fewer
+// waves per CU leave more of the CU's LDS and vector-memory bandwidth to each.
+constexpr int SCAN_WAVES = 2;
+constexpr int SCAN_COLS = 8 * SCAN_WAVES;  // state columns per workgroup
+
 template <int NW, bool BF16_OUT>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1))) void chunk_scan_kernel(ChunkArgs a) {
   __shared__ u32x4 stage0[ST_U4];
   __shared__ u32x4 stage1[ST_U4];
+  __shared__ u32x4 xch[2][NW][2 * 64];  // bf16 state halves by (chunk parity, wave, k-step), lane order
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int X = wave & 1;    // state-row half of this wave
+  const int sl = wave >> 1;  // column slice within the workgroup
   const int g4 = lane >> 4;
   const int r16 = lane & 15;
   const int nh = a.n_seqs * a.Hv;
@@ -707,8 +738,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
   const int n = rest / a.Hv;
   const int h = rest % a.Hv;
   const int hk = h / (a.Hv / a.Hk);
-  const int col = 16 * NW * ct + 16 * wave + r16;
-  const int u_voff = ((4 * NW * ct + 4 * wave) * 64 + lane) * 16;  // this wave's U blocks in a chunk's U region
+  const int col = 8 * NW * ct + 16 * sl + r16;
+  const int u_voff = ((4 * (NW / 2 * ct + sl)) * 64 + lane) * 16;  // U blocks of this column slice in a chunk's U region
 
   // Values read from memory are workgroup-uniform; readfirstlane tells the
   // compiler so (buffer resources built from them must live in SGPRs).
@@ -726,14 +757,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
   const int64_t in_row = a.h0 ? uniform64(a.h0_idx ? a.h0_idx[n] : n) : -1;
   const int64_t out_row = a.hT ? uniform64(a.hT_idx ? a.hT_idx[n] : n) : -1;
   const int64_t kv = static_cast<int64_t>(DK) * DV;
+  const int row0 = 64 * X;  // first state row of this wave's half
   if (cs == ce) {  // empty sequence: the final state is the initial one (handled once)
     if (a.seg_begin == 0 && out_row >= 0) {
       float *dst = a.hT + (out_row * a.Hv + h) * kv + col;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int r = 16 * i + 4 * g4 + e;
+          const int r = row0 + 16 * t + 4 * g4 + e;
           dst[r * DV] = in_row >= 0 ? a.h0[(in_row * a.Hv + h) * kv + r * DV + col] : 0.f;
         }
     }
@@ -745,26 +777,26 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
   const int64_t seq_off = static_cast<int64_t>(lo - cs) * CK;  // its first token within the sequence
   float *carry = a.carry + (static_cast<int64_t>(n) * a.Hv + h) * kv + col;
 
-  f32x4 S[8];
+  f32x4 S[4];  // state rows row0 + 16t + 4g + e of this lane's column
   const float *src = lo == cs ? (in_row >= 0 ? a.h0 + (in_row * a.Hv + h) * kv + col : nullptr) : carry;
   if (src) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) S[i][e] = src[(16 * i + 4 * g4 + e) * DV];
+      for (int e = 0; e < 4; ++e) S[t][e] = src[(row0 + 16 * t + 4 * g4 + e) * DV];
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) S[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < 4; ++t) S[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  bf16x8 sb[4];
-#pragma unroll
-  for (int s2 = 0; s2 < 4; ++s2) sb[s2] = pack_hi(S[2 * s2], S[2 * s2 + 1]);
+  bf16x8 sbh[2], sbp[2];
+  sbh[0] = pack_hi(S[0], S[1]);
+  sbh[1] = pack_hi(S[2], S[3]);
 
-  // Output addressing: byte offsets of rows 16p + 4g + e within a chunk.
+  // Output addressing: byte offsets of this wave's rows 32X + 16pp + 4g + e within a chunk.
   typedef typename std::conditional<BF16_OUT, uint16_t, float>::type OT;
   const int64_t ostep = static_cast<int64_t>(a.Hv) * DV;  // elements per token
   const int row_bytes = static_cast<int>(ostep * sizeof(OT));
-  const int voff0 = static_cast<int>((4 * g4 * ostep + h * DV + col) * sizeof(OT));
+  const int voff0 = static_cast<int>(((32 * X + 4 * g4) * ostep + h * DV + col) * sizeof(OT));
   auto out_rsrc = [&](int c) {  // chunk c of this launch: rows [0, min(64, rest of sequence))
     const int64_t toff = seq_off + static_cast<int64_t>(c) * CK;
     const int rows = static_cast<int>(min<int64_t>(CK, slen - toff));
@@ -773,9 +805,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
   };
   // Before the first chunk there is no output to store: a zero-sized range.
   __amdgpu_buffer_rsrc_t prev = __builtin_amdgcn_make_buffer_rsrc(a.o, 0, 0, BUF_DWORD3);
-  f32x4 o[4];
+  f32x4 o[2];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) o[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int pp = 0; pp < 2; ++pp) o[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Chunk cidx of this launch (clamped: after the last chunk the "next"
   // copies reload the last chunk into the idle stage).
@@ -784,46 +816,63 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
   auto u_rsrc_of = [&](int cidx) {
     return __builtin_amdgcn_make_buffer_rsrc(a.Ut + (chunk_of(cidx) * a.Hv + h) * (DV * CK), 0, DV * CK * 4, BUF_DWORD3);
   };
+  // the state exchange: write this wave's half, (barrier), read the partner's
+  auto put_half = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) xch[buf][wave][j * 64 + lane] = __builtin_bit_cast(u32x4, sbh[j]);
+  };
+  auto get_half = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) sbp[j] = __builtin_bit_cast(bf16x8, xch[buf][wave ^ 1][j * 64 + lane]);
+  };
+  auto run = [&](const u32x4 *st, const f32x4 (&u)[4], u32x4 *st_next, int next, f32x4 (&u_next)[4]) {
+    if (X)
+      scan_chunk<NW, 1, BF16_OUT>(st, u, S, sbh, sbp, o, prev, voff0, row_bytes, st_next, src_of(next), u_next,
+                              u_rsrc_of(next), u_voff, wave, lane);
+    else
+      scan_chunk<NW, 0, BF16_OUT>(st, u, S, sbh, sbp, o, prev, voff0, row_bytes, st_next, src_of(next), u_next,
+                              u_rsrc_of(next), u_voff, wave, lane);
+  };
   f32x4 u0[4], u1[4];
   {
-    const StageSrc src = src_of(0);
+    const StageSrc src0 = src_of(0);
 #pragma unroll
-    for (int i = 0; i < Dma<NW>::n; ++i) dma_copy<NW>(i, stage0, src, wave, lane);
+    for (int i = 0; i < Dma<NW>::n; ++i) dma_copy<NW>(i, stage0, src0, wave, lane);
     load_u(u0, u_rsrc_of(0), u_voff);
   }
+  put_half(0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  get_half(0);
   // A chunk's output is stored during the next chunk (vmcnt counts stores
   // too, so the wait at the end of each chunk then finds them long done).
+  // Chunk c reads the state exchange buffer c % 2 and writes (c + 1) % 2; a
+  // buffer is rewritten only after the barrier that follows its last read.
   for (int c = 0; c < nch; c += 2) {
-    scan_chunk<NW, BF16_OUT>(stage0, u0, S, sb, o, prev, voff0, row_bytes, stage1, src_of(c + 1), u1, u_rsrc_of(c + 1), u_voff,
-                             wave, lane);
+    run(stage0, u0, stage1, c + 1, u1);
     prev = out_rsrc(c);
+    put_half(1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    get_half(1);
     if (c + 1 >= nch) break;
-    scan_chunk<NW, BF16_OUT>(stage1, u1, S, sb, o, prev, voff0, row_bytes, stage0, src_of(c + 2), u0, u_rsrc_of(c + 2), u_voff,
-                             wave, lane);
+    run(stage1, u1, stage0, c + 2, u0);
     prev = out_rsrc(c + 1);
+    put_half(0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    get_half(0);
   }
   store_chunk<BF16_OUT>(o, prev, voff0, row_bytes);
 
   float *dst = hi == ce ? (out_row >= 0 ? a.hT + (out_row * a.Hv + h) * kv + col : nullptr) : carry;
   if (dst) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) dst[(16 * i + 4 * g4 + e) * DV] = S[i][e];
+      for (int e = 0; e < 4; ++e) dst[(row0 + 16 * t + 4 * g4 + e) * DV] = S[t][e];
   }
 }
-
-// Scan workgroup shape (measured on MI355X at T=4096, 32 v-heads): 4 waves =
-// 64 state columns per workgroup.  With 8 waves per workgroup every wave
-// re-reads the whole operand stage from LDS and the LDS bandwidth becomes the
-// limit; with 2 the stage is streamed four times.
-constexpr int SCAN_WAVES = 4;
 
 // Chunks per prep + scan segment.  One segment's operand workspace (about
 // 2.3 MiB per chunk at 32 v-heads, so ~150 MB) stays resident in the 256 MB
@@ -951,7 +1000,7 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
   if (reinterpret_cast<uintptr_t>(workspace) % 256)
     return fail(GDN_ERR_WORKSPACE, "%s: workspace must be 256-byte aligned", name);
   if (nc > 65535) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: %lld chunks exceed one launch", name, (long long)nc);
-  const int64_t scan_blocks = static_cast<int64_t>(n_seqs) * Hv * (DV / (16 * SCAN_WAVES));
+  const int64_t scan_blocks = static_cast<int64_t>(n_seqs) * Hv * (DV / SCAN_COLS);
   if (scan_blocks > 0x7fffffff) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: grid too large", name);
   char *ws = static_cast<char *>(workspace);
   ChunkArgs a{static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
