@@ -494,15 +494,15 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
 }
 
 // ------------------------------------------------------------------ phase B
-// LDS stage: one chunk's shared scan operands, the v-head region then the
-// k-head region (57 blocks of 1 KiB).  U is per wave and goes straight from
-// global memory to registers.
+// LDS stage: one chunk's operands that both waves of a pair read, the
+// v-head region then the k-head region's Q blocks (41 blocks of 1 KiB).  U
+// and the K^T blocks of a wave's state half are read by that wave alone and
+// go straight from global memory to its registers, one chunk ahead.
 constexpr int ST_W = VH_W * 64;
 constexpr int ST_A = VH_A * 64;
 constexpr int ST_SC = VH_SC * 64;
 constexpr int ST_Q = (NB_VH + KH_Q) * 64;
-constexpr int ST_KT = (NB_VH + KH_KT) * 64;
-constexpr int ST_U4 = (NB_VH + NB_KH) * 64;  // stage size in 16-byte units
+constexpr int ST_U4 = (NB_VH + NB_Q) * 64;  // stage size in 16-byte units
 
 constexpr int BUF_DWORD3 = 0x00020000;  // raw (untyped) buffer resource word 3 on CDNA
 
@@ -518,7 +518,7 @@ struct StageSrc {
 };
 template <int NW> struct Dma {
   static constexpr int vh = (NB_VH + NW - 1) / NW;
-  static constexpr int kh = (NB_KH + NW - 1) / NW;
+  static constexpr int kh = (NB_Q + NW - 1) / NW;
   static constexpr int n = vh + kh;  // copies per wave per chunk
 };
 template <int NW>
@@ -527,7 +527,7 @@ __device__ __forceinline__ void dma_copy(int i, u32x4 *dst, const StageSrc &src,
     const int t = min(i * NW + wave, NB_VH - 1);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(src.vh, dst + t * 64, 16, lane * 16, t * 1024, 0, 0);
   } else {
-    const int t = min((i - Dma<NW>::vh) * NW + wave, NB_KH - 1);
+    const int t = KH_Q + min((i - Dma<NW>::vh) * NW + wave, NB_Q - 1);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(src.kh, dst + (NB_VH + t) * 64, 16, lane * 16, t * 1024, 0, 0);
   }
 }
@@ -541,6 +541,16 @@ __device__ __forceinline__ void load_u(f32x4 (&u)[4], __amdgpu_buffer_rsrc_t r, 
 #pragma unroll
   for (int p = 0; p < 4; ++p)
     u[p] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + p * 1024, 0, 0));
+}
+// K^T blocks of state-row half X of one chunk: tiles 4X + t, k-steps s2,
+// block 2 (4X + t) + s2 of the k-head region's K^T part, lane order.
+template <int X>
+__device__ __forceinline__ void load_kt(u32x4 (&kb)[8], __amdgpu_buffer_rsrc_t r, int lane) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+      kb[2 * t + s2] = __builtin_amdgcn_raw_buffer_load_b128(r, ((KH_KT + 2 * (4 * X + t) + s2) * 64 + lane) * 16, 0, 0);
 }
 
 // Output of one chunk, this wave's two row tiles: lane (g, c) holds rows
@@ -574,10 +584,11 @@ constexpr int SG_VALU = 0x2, SG_MFMA = 0x8, SG_VMEM_RD = 0x20, SG_VMEM_WR = 0x40
 // the state are exchanged as bf16 MFMA operands through LDS at the chunk
 // barrier, so each wave sees the whole state and computes the full
 // V' = U - W S (its state update needs V' at all 64 positions), its own rows
-// of O and its own half of the state update.  A wave reads 39 KiB of operands
-// from LDS per chunk (W 16, Q 8, K^T 8, A <= 4, scales, the partner's state
-// 2) instead of the 62 KiB of an unsplit 16-column wave, and one wave's LDS
-// read rate (about 25 B/clk) is what bounds a chunk.
+// of O and its own half of the state update.  A wave reads 31 KiB of operands
+// from LDS per chunk (W 16, Q 8, A <= 4, scales, the partner's state 2; its
+// K^T half and U come from global memory) instead of the 62 KiB of an
+// unsplit 16-column wave; one wave's LDS read rate (about 25 B/clk) bounds a
+// chunk.
 //
 // One chunk in three scheduling regions (VALU work interleaved with the
 // MFMAs by sched_group_barrier patterns; the scan runs one wave per SIMD):
@@ -594,7 +605,7 @@ __device__ __forceinline__ void scan_chunk(const u32x4 *st, const f32x4 (&u)[4],
                                            const bf16x8 (&sbp)[2], f32x4 (&o)[2], __amdgpu_buffer_rsrc_t prev_out,
                                            int voff0, int row_bytes, u32x4 *st_next, const StageSrc &src_next,
                                            f32x4 (&u_next)[4], __amdgpu_buffer_rsrc_t u_rsrc_next, int u_voff,
-                                           int wave, int lane) {
+                                           const u32x4 (&kb)[8], u32x4 (&kb_next)[8], int wave, int lane) {
   // copies issued in R1 | R2 (measured: all in R1 stalls R1 on the vector-
   // memory queue; in R3 they land after the chunk ends)
   constexpr int D1 = Dma<NW>::n / 2, D2 = Dma<NW>::n;
@@ -634,6 +645,7 @@ __device__ __forceinline__ void scan_chunk(const u32x4 *st, const f32x4 (&u)[4],
   for (int pp = 0; pp < 2; ++pp) sq[pp] = *reinterpret_cast<const f32x4 *>(sc + 16 * (2 * X + pp) + 4 * g4);
   store_chunk<BF16_OUT>(o, prev_out, voff0, row_bytes);
   load_u(u_next, u_rsrc_next, u_voff);
+  load_kt<X>(kb_next, src_next.kh, lane);
 #pragma unroll
   for (int i = 0; i < D1; ++i) dma_copy<NW>(i, st_next, src_next, wave, lane);
 #pragma unroll
@@ -649,16 +661,11 @@ __device__ __forceinline__ void scan_chunk(const u32x4 *st, const f32x4 (&u)[4],
     GDN_GROUP(SG_DS_RD, 1);
     GDN_GROUP(SG_VALU, 2);
     GDN_GROUP(SG_VMEM_WR, 1);
-    GDN_GROUP(SG_VMEM_RD, 1);
+    GDN_GROUP(SG_VMEM_RD, 2);
   }
   GDN_SCHED_FENCE();
 
   // ---- R2
-  u32x4 kb[8];  // K^T tiles 4X + t, k-steps s: block 2 (4X + t) + s
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) kb[2 * t + s2] = st[ST_KT + (2 * (4 * X + t) + s2) * 64 + lane];
 #pragma unroll
   for (int i = D1; i < D2; ++i) dma_copy<NW>(i, st_next, src_next, wave, lane);
   f32x4 acc[2];
@@ -677,7 +684,6 @@ __device__ __forceinline__ void scan_chunk(const u32x4 *st, const f32x4 (&u)[4],
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     GDN_GROUP(SG_MFMA, 1);
-    GDN_GROUP(SG_DS_RD, 1);
     GDN_GROUP(SG_VALU, 6);
     GDN_GROUP(SG_VMEM_RD, 1);
   }
@@ -825,20 +831,23 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 #pragma unroll
     for (int j = 0; j < 2; ++j) sbp[j] = __builtin_bit_cast(bf16x8, xch[buf][wave ^ 1][j * 64 + lane]);
   };
-  auto run = [&](const u32x4 *st, const f32x4 (&u)[4], u32x4 *st_next, int next, f32x4 (&u_next)[4]) {
+  auto run = [&](const u32x4 *st, const f32x4 (&u)[4], const u32x4 (&kb)[8], u32x4 *st_next, int next,
+                 f32x4 (&u_next)[4], u32x4 (&kb_next)[8]) {
     if (X)
       scan_chunk<NW, 1, BF16_OUT>(st, u, S, sbh, sbp, o, prev, voff0, row_bytes, st_next, src_of(next), u_next,
-                              u_rsrc_of(next), u_voff, wave, lane);
+                                  u_rsrc_of(next), u_voff, kb, kb_next, wave, lane);
     else
       scan_chunk<NW, 0, BF16_OUT>(st, u, S, sbh, sbp, o, prev, voff0, row_bytes, st_next, src_of(next), u_next,
-                              u_rsrc_of(next), u_voff, wave, lane);
+                                  u_rsrc_of(next), u_voff, kb, kb_next, wave, lane);
   };
   f32x4 u0[4], u1[4];
+  u32x4 k0[8], k1[8];  // K^T blocks of this wave's state half, current / next chunk
   {
     const StageSrc src0 = src_of(0);
 #pragma unroll
     for (int i = 0; i < Dma<NW>::n; ++i) dma_copy<NW>(i, stage0, src0, wave, lane);
     load_u(u0, u_rsrc_of(0), u_voff);
+    if (X) load_kt<1>(k0, src0.kh, lane); else load_kt<0>(k0, src0.kh, lane);
   }
   put_half(0);
   __builtin_amdgcn_s_waitcnt(0);
@@ -849,14 +858,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
   // Chunk c reads the state exchange buffer c % 2 and writes (c + 1) % 2; a
   // buffer is rewritten only after the barrier that follows its last read.
   for (int c = 0; c < nch; c += 2) {
-    run(stage0, u0, stage1, c + 1, u1);
+    run(stage0, u0, k0, stage1, c + 1, u1, k1);
     prev = out_rsrc(c);
     put_half(1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     get_half(1);
     if (c + 1 >= nch) break;
-    run(stage1, u1, stage0, c + 2, u0);
+    run(stage1, u1, k1, stage0, c + 2, u0, k0);
     prev = out_rsrc(c + 1);
     put_half(0);
     __builtin_amdgcn_s_waitcnt(0);
