@@ -19,11 +19,14 @@
 //                       (ds_read_b64_tr_b16).  Every operand the scan needs is
 //                       written pre-swizzled: one 1 KiB block per (MFMA, wave),
 //                       lane l's 16 bytes at offset 16 l.
-//   chunk_scan_kernel   one wave per (sequence, v-head, 16 state columns),
-//                       serial over the chunks; the state slice lives in MFMA
-//                       accumulators for the whole sequence.  The next chunk's
-//                       operand blocks stream into a second LDS buffer with
-//                       buffer_load ... lds while the current chunk computes.
+//   chunk_scan_kernel   one workgroup per (sequence, v-head, 16 state
+//                       columns), serial over the chunks: four compute waves,
+//                       each owning 16 chunk positions and 32 state rows (its
+//                       state slice lives in MFMA accumulators for the whole
+//                       sequence), exchange V'' and the state through LDS;
+//                       two loader waves stream the operand blocks of the
+//                       chunk after next into a double-buffered LDS stage
+//                       with buffer_load ... lds.
 // Inputs longer than one segment (64 chunks) run prep / scan per segment,
 // the next segment's prep on a side stream.
 // Precision (checked against an fp64 restatement at T=4096): the state is fed
@@ -35,7 +38,9 @@
 // accumulator tile pair (rows 0-15, 16-31 of a 32-long reduction) is reused
 // as the B operand of the next product, lane group g = l/16 holds reduction
 // indices {4g..4g+3, 16+4g..16+4g+3} ("pi" order); the scan's A-operand
-// blocks are stored in the same order, so no accumulator goes through LDS.
+// blocks are stored in the same order, so an accumulator becomes an operand
+// by conversion to bf16 alone (in the scan, between waves, through LDS
+// without any reordering).
 #include <algorithm>
 #include <mutex>
 #include <type_traits>
@@ -494,281 +499,282 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
 }
 
 // ------------------------------------------------------------------ phase B
-// LDS stage: one chunk's operands that both waves of a pair read, the
-// v-head region then the k-head region's Q blocks (41 blocks of 1 KiB).  U
-// and the K^T blocks of a wave's state half are read by that wave alone and
-// go straight from global memory to its registers, one chunk ahead.
-constexpr int ST_W = VH_W * 64;
-constexpr int ST_A = VH_A * 64;
-constexpr int ST_SC = VH_SC * 64;
-constexpr int ST_Q = (NB_VH + KH_Q) * 64;
-constexpr int ST_U4 = (NB_VH + NB_Q) * 64;  // stage size in 16-byte units
-
 constexpr int BUF_DWORD3 = 0x00020000;  // raw (untyped) buffer resource word 3 on CDNA
-
-// The next chunk's stage is copied with buffer_load ... lds (64 lanes x 16
-// bytes per instruction, uniform base, range-checked), spread over the
-// current chunk's MFMA work: a CU's vector-memory path moves 64 B/clk, so
-// issuing all of a chunk's copies at once would stall every wave for about
-// a thousand cycles.  Wave w copies blocks w, w + NW, ... of each region; a
-// wave with no block left in the last round copies the region's last block
-// again (same bytes to the same LDS address), which keeps it branch-free.
-struct StageSrc {
-  __amdgpu_buffer_rsrc_t vh, kh;
-};
-template <int NW> struct Dma {
-  static constexpr int vh = (NB_VH + NW - 1) / NW;
-  static constexpr int kh = (NB_Q + NW - 1) / NW;
-  static constexpr int n = vh + kh;  // copies per wave per chunk
-};
-template <int NW>
-__device__ __forceinline__ void dma_copy(int i, u32x4 *dst, const StageSrc &src, int wave, int lane) {
-  if (i < Dma<NW>::vh) {
-    const int t = min(i * NW + wave, NB_VH - 1);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(src.vh, dst + t * 64, 16, lane * 16, t * 1024, 0, 0);
-  } else {
-    const int t = KH_Q + min((i - Dma<NW>::vh) * NW + wave, NB_Q - 1);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(src.kh, dst + (NB_VH + t) * 64, 16, lane * 16, t * 1024, 0, 0);
-  }
-}
-template <int NW>
-__device__ __forceinline__ StageSrc stage_src(const ChunkArgs &a, size_t ch, size_t chk) {
-  return StageSrc{__builtin_amdgcn_make_buffer_rsrc(a.vh + ch * (NB_VH * 64), 0, NB_VH * 1024, BUF_DWORD3),
-                  __builtin_amdgcn_make_buffer_rsrc(a.kh + chk * (NB_KH * 64), 0, NB_KH * 1024, BUF_DWORD3)};
-}
-// This wave's U rows of one chunk (4 blocks of 1 KiB, lane l's 16 bytes at 16 l).
-__device__ __forceinline__ void load_u(f32x4 (&u)[4], __amdgpu_buffer_rsrc_t r, int voff) {
-#pragma unroll
-  for (int p = 0; p < 4; ++p)
-    u[p] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + p * 1024, 0, 0));
-}
-// K^T blocks of state-row half X of one chunk: tiles 4X + t, k-steps s2,
-// block 2 (4X + t) + s2 of the k-head region's K^T part, lane order.
-template <int X>
-__device__ __forceinline__ void load_kt(u32x4 (&kb)[8], __amdgpu_buffer_rsrc_t r, int lane) {
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-      kb[2 * t + s2] = __builtin_amdgcn_raw_buffer_load_b128(r, ((KH_KT + 2 * (4 * X + t) + s2) * 64 + lane) * 16, 0, 0);
-}
-
-// Output of one chunk, this wave's two row tiles: lane (g, c) holds rows
-// 16pp + 4g + e (pp < 2) of its output half.  The buffer resource starts at the
-// chunk's first token and ends after its last valid row, so stores past the
-// sequence end are dropped by the hardware range check (which covers the VGPR
-// offset: voff0 + row * row_bytes, voff0 = byte offset of row 4g of this
-// lane's column in this wave's half).
-template <bool BF16_OUT>
-__device__ __forceinline__ void store_chunk(const f32x4 (&o)[2], __amdgpu_buffer_rsrc_t r, int voff0, int row_bytes) {
-#pragma unroll
-  for (int pp = 0; pp < 2; ++pp)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int off = voff0 + (16 * pp + e) * row_bytes;
-      if constexpr (BF16_OUT)
-        __builtin_amdgcn_raw_buffer_store_b16(bf16_rne(o[pp][e]), r, off, 0, 0);
-      else
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, o[pp][e]), r, off, 0, 0);
-    }
-}
 
 // sched_group_barrier masks
 constexpr int SG_VALU = 0x2, SG_MFMA = 0x8, SG_VMEM_RD = 0x20, SG_VMEM_WR = 0x40, SG_DS_RD = 0x100;
 #define GDN_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 #define GDN_GROUP(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
 
-// The scan is K-split: a pair of waves shares 16 state columns, wave X of
-// the pair (X = 0, 1) keeping state rows 64X..64X+63 (tiles 4X..4X+3) in its
-// MFMA accumulators and writing output rows 32X..32X+31.  The two halves of
-// the state are exchanged as bf16 MFMA operands through LDS at the chunk
-// barrier, so each wave sees the whole state and computes the full
-// V' = U - W S (its state update needs V' at all 64 positions), its own rows
-// of O and its own half of the state update.  A wave reads 31 KiB of operands
-// from LDS per chunk (W 16, Q 8, A <= 4, scales, the partner's state 2; its
-// K^T half and U come from global memory) instead of the 62 KiB of an
-// unsplit 16-column wave; one wave's LDS read rate (about 25 B/clk) bounds a
-// chunk.
+// ------------------------------------------------------------ row-split scan
+// Workgroup = 6 waves for one (sequence, v-head, 16 state columns):
 //
-// One chunk in three scheduling regions (VALU work interleaved with the
-// MFMAs by sched_group_barrier patterns; the scan runs one wave per SIMD):
-//   R1  V' = U - W S (all rows)   16 MFMAs | S *= e^{gamma_63}, previous chunk's
-//                                           output stores, U prefetch, stage copies
-//   R2  acc = Q S (own rows)       8 MFMAs | V' to bf16, V'' = sk V' split hi + lo,
-//                                           stage copies
-//   R3  S += K^T V'' (own rows)   16 MFMAs | O = sq acc + A V' (2 or 4 MFMAs),
-//                                           next chunk's bf16 state half
-// sbh / sbp: this wave's / the partner's bf16 state half (k-steps 2X, 2X+1 /
-// the other two); on return sbh holds the updated half, o this chunk's rows.
-template <int NW, int X, bool BF16_OUT>
-__device__ __forceinline__ void scan_chunk(const u32x4 *st, const f32x4 (&u)[4], f32x4 (&S)[4], bf16x8 (&sbh)[2],
-                                           const bf16x8 (&sbp)[2], f32x4 (&o)[2], __amdgpu_buffer_rsrc_t prev_out,
-                                           int voff0, int row_bytes, u32x4 *st_next, const StageSrc &src_next,
-                                           f32x4 (&u_next)[4], __amdgpu_buffer_rsrc_t u_rsrc_next, int u_voff,
-                                           const u32x4 (&kb)[8], u32x4 (&kb_next)[8], int wave, int lane) {
-  // copies issued in R1 | R2 (measured: all in R1 stalls R1 on the vector-
-  // memory queue; in R3 they land after the chunk ends)
-  constexpr int D1 = Dma<NW>::n / 2, D2 = Dma<NW>::n;
-  constexpr int NA = X ? 4 : 2;                        // A blocks of this wave's output rows
-  const int g4 = lane >> 4;
-  const float *sc = reinterpret_cast<const float *>(st + ST_SC);
-  bf16x8 sb[4];  // the whole state as bf16 B operands, by k-step
-  sb[2 * X] = sbh[0];
-  sb[2 * X + 1] = sbh[1];
-  sb[2 - 2 * X] = sbp[0];
-  sb[3 - 2 * X] = sbp[1];
+// * compute waves q = 0..3.  Wave q owns chunk positions 16q..16q+15 (its
+//   rows of V' and O) and state rows 32q..32q+31 (state tiles 2q, 2q+1:
+//   k-step q of every product with S).  No operand one compute wave reads is
+//   read by another, and LDS carries the two exchanges of each chunk:
+//     xv  after V' = U - W S:   V' (bf16) and V'' = diag(sk) V' (bf16 hi + lo)
+//     xs  after S += K^T V'':   the updated state rows (bf16)
+//   each followed by a barrier.  A compute wave runs 17-18 MFMAs per chunk.
+// * loader waves 4, 5 stream each chunk's operands (61 KiB: the v-head
+//   region, the k-head region and this column tile's U blocks) from global
+//   memory into a double-buffered LDS stage with buffer_load ... lds, two
+//   chunks ahead, so that the CU's vector-memory path (about 55 B/clk with
+//   two waves issuing) runs the whole time instead of in bursts between the
+//   barriers; the compute waves read their operands from the stage one chunk
+//   ahead (LDS reads, about 39 B/clk per wave).
+//
+// Stage buffer c % 2 holds chunk c.  Loaders: during chunk c they copy
+// chunk c + 2 into buffer c % 2 (half before barrier 1, half before barrier
+// 2) and, before barrier 1, wait for chunk c + 1's copies.  Compute waves:
+// between barriers 1 and 2 of chunk c they read chunk c + 1's operands from
+// buffer (c + 1) % 2.  So a buffer is rewritten only after the barrier that
+// follows its last read, and read only after the barrier that follows the
+// wait for its copies.  The barriers fence LDS only (the loaders wait for
+// their copies with an explicit vmcnt).
+constexpr int RS_VH = 0, RS_KH = NB_VH, RS_U = NB_VH + NB_KH, RS_BLOCKS = RS_U + 4;  // 61 blocks of 1 KiB
+constexpr int RS_LOADER0 = NB_VH + 4;  // loader 0: v-head region + U blocks; loader 1: k-head region
+constexpr int RS_LOADER1 = NB_KH;
+constexpr int SCAN_WAVES = 6;
+constexpr int SCAN_COLS = 16;  // state columns per workgroup
 
+struct RowOps {     // one chunk's operands of one compute wave
+  u32x4 w[4];       // -W rows 16q.., k-steps 0..3
+  u32x4 qm[4];      // Q rows 16q.., k-steps 0..3
+  u32x4 kt[4];      // K^T tiles 2q + t, k-steps s: [2t + s]
+  u32x4 am[2];      // A rows 16q.., k-steps 0, 1 (the second only for q >= 2)
+  f32x4 u, sk;      // U rows 16q + 4g + e of this lane's column; their V'' scales
+  float sq, eL;     // output scale of position 16q + (lane % 16); e^{gamma_63}
+};
+struct RowSrc {     // one chunk's operand regions in the workspace (per v-head, per k-head, U)
+  __amdgpu_buffer_rsrc_t vh, kh, ut;
+};
+__device__ __forceinline__ RowSrc row_src(const ChunkArgs &a, size_t ch, size_t chk) {
+  return RowSrc{__builtin_amdgcn_make_buffer_rsrc(a.vh + ch * (NB_VH * 64), 0, NB_VH * 1024, BUF_DWORD3),
+                __builtin_amdgcn_make_buffer_rsrc(a.kh + chk * (NB_KH * 64), 0, NB_KH * 1024, BUF_DWORD3),
+                __builtin_amdgcn_make_buffer_rsrc(a.Ut + ch * (DV * CK), 0, DV * CK * 4, BUF_DWORD3)};
+}
+
+// Loader ld's copies [i0, i1) of one chunk into stage st (1 KiB each, lane l's 16 bytes at 16 l).
+template <int LD>
+__device__ __forceinline__ void stage_copy(u32x4 *st, const RowSrc &r, int ct, int i0, int i1, int lane) {
+  for (int i = i0; i < i1; ++i) {
+    if constexpr (LD == 0) {
+      if (i < NB_VH)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r.vh, st + (RS_VH + i) * 64, 16, lane * 16, i * 1024, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r.ut, st + (RS_U + i - NB_VH) * 64, 16, lane * 16,
+                                                 (4 * ct + i - NB_VH) * 1024, 0, 0);
+    } else {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r.kh, st + (RS_KH + i) * 64, 16, lane * 16, i * 1024, 0, 0);
+    }
+  }
+}
+
+// A compute wave's operands of one chunk from its stage buffer, in groups
+// read at different points of the previous chunk.
+template <int G>
+__device__ __forceinline__ void read_rows(RowOps &op, const u32x4 *st, int q, int lane) {
+  const float *sc = reinterpret_cast<const float *>(st + (RS_VH + VH_SC) * 64);
+  if constexpr (G == 0) {  // V' = U - W S and its scales
+#pragma unroll
+    for (int s = 0; s < 4; ++s) op.w[s] = st[(RS_VH + VH_W + 4 * q + s) * 64 + lane];
+    op.u = __builtin_bit_cast(f32x4, st[(RS_U + q) * 64 + lane]);
+    op.sk = *reinterpret_cast<const f32x4 *>(sc + CK + 16 * q + 4 * (lane >> 4));
+    op.eL = sc[2 * CK];
+  } else if constexpr (G == 1) {  // Q S
+#pragma unroll
+    for (int s = 0; s < 4; ++s) op.qm[s] = st[(RS_KH + KH_Q + 4 * q + s) * 64 + lane];
+  } else if constexpr (G == 2) {  // S += K^T V''
+#pragma unroll
+    for (int j = 0; j < 4; ++j) op.kt[j] = st[(RS_KH + KH_KT + 4 * q + j) * 64 + lane];
+  } else {  // the output
+    op.am[0] = st[(RS_VH + VH_A + 2 * q) * 64 + lane];
+    op.am[1] = st[(RS_VH + VH_A + 2 * q + 1) * 64 + lane];  // (unused for q < 2)
+    op.sq = sc[16 * q + (lane & 15)];
+  }
+}
+
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+__device__ __forceinline__ u32x2 pack4(f32x4 x) {
+  bf16x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = static_cast<__bf16>(x[i]);
+  return __builtin_bit_cast(u32x2, r);
+}
+
+// One chunk of compute wave q (TWO_A: q >= 2, whose output rows see V' rows
+// of both k-steps).  sb: the whole state as bf16 B operands by k-step; S:
+// this wave's state rows (fp32).  On return sb and S hold the updated state
+// and store_out(o) has been called with the chunk's output rows.  nst: the
+// stage buffer of the next chunk, whose operands are read into nx here.
+//
+// The chain that carries the state from chunk to chunk -- V' = U - W S, V''
+// to LDS, barrier, S += K^T V'', S to LDS, barrier, S back from LDS -- runs
+// first in each of three regions; the products off that chain (Q S and the
+// output) and the operand reads fill its waits:
+//   R1  V' (4 MFMAs), V'' to LDS
+//   R2  (after barrier 1, V'' reads in flight) Q S (4 MFMAs), then
+//       S += K^T V'' (8 MFMAs) | next chunk's operands from the stage
+//   R3  (after barrier 2, state reads in flight) O (1-2 MFMAs), its store
+// xv[kind][k-step][lane] holds, per lane, 4 bf16 of wave 2 k-step and then 4
+// of wave 2 k-step + 1: a B operand in pi order.
+//
+// O is computed transposed, O^T = (S^T Q^T) diag(sq) + V'^T A^T: the
+// registers of an A operand are those of the transposed B operand, so sb,
+// the V' exchange and the Q and A blocks serve unchanged, and lane (g, r)
+// ends with O[16q + r][4g .. 4g + 3], one 8-byte store.
+template <bool TWO_A, class StoreOut>
+__device__ __forceinline__ void scan_rows_chunk(const RowOps &op, RowOps &nx, const u32x4 *nst, bf16x8 (&sb)[4],
+                                                f32x4 (&S)[2], u32x2 (*xv)[2][64][2], u32x4 (*xs)[64], int q,
+                                                int lane, const StoreOut &store_out) {
   // ---- R1
-  u32x4 wb[16];
+  f32x4 vp = op.u;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) wb[i] = st[ST_W + i * 64 + lane];
-  f32x4 vp[4];  // V' rows 16p + 4g + e
+  for (int s = 0; s < 4; ++s) vp = mfma(as_bf16x8(op.w[s]), sb[s], vp);
 #pragma unroll
-  for (int p = 0; p < 4; ++p) vp[p] = u[p];
-  const float eL = sc[2 * CK];
-  u32x4 qb[8], ab[NA];
+  for (int t = 0; t < 2; ++t) S[t] = S[t] * op.eL;
+  {
+    const f32x4 v2 = vp * op.sk;
+    f32x4 hf;
+    bf16x4 h, l;
 #pragma unroll
-  for (int pp = 0; pp < 2; ++pp)
-#pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) qb[4 * pp + s2] = st[ST_Q + (4 * (2 * X + pp) + s2) * 64 + lane];
-  if constexpr (X == 0) {  // rows p = 0, 1: A blocks (0, 0) and (1, 0)
-    ab[0] = st[ST_A + 0 * 64 + lane];
-    ab[1] = st[ST_A + 2 * 64 + lane];
-  } else {                 // rows p = 2, 3: A blocks (2, 0), (2, 1), (3, 0), (3, 1)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ab[i] = st[ST_A + (4 + i) * 64 + lane];
+    for (int i = 0; i < 4; ++i) {
+      h[i] = static_cast<__bf16>(v2[i]);
+      hf[i] = static_cast<float>(h[i]);
+      l[i] = static_cast<__bf16>(v2[i] - hf[i]);
+    }
+    xv[0][q >> 1][lane][q & 1] = pack4(vp);
+    xv[1][q >> 1][lane][q & 1] = __builtin_bit_cast(u32x2, h);
+    xv[2][q >> 1][lane][q & 1] = __builtin_bit_cast(u32x2, l);
   }
-  f32x4 sk[4], sq[2];
-#pragma unroll
-  for (int p = 0; p < 4; ++p) sk[p] = *reinterpret_cast<const f32x4 *>(sc + CK + 16 * p + 4 * g4);
-#pragma unroll
-  for (int pp = 0; pp < 2; ++pp) sq[pp] = *reinterpret_cast<const f32x4 *>(sc + 16 * (2 * X + pp) + 4 * g4);
-  store_chunk<BF16_OUT>(o, prev_out, voff0, row_bytes);
-  load_u(u_next, u_rsrc_next, u_voff);
-  load_kt<X>(kb_next, src_next.kh, lane);
-#pragma unroll
-  for (int i = 0; i < D1; ++i) dma_copy<NW>(i, st_next, src_next, wave, lane);
-#pragma unroll
-  for (int s2 = 0; s2 < 4; ++s2)
-#pragma unroll
-    for (int p = 0; p < 4; ++p) vp[p] = mfma(as_bf16x8(wb[4 * p + s2]), sb[s2], vp[p]);
-#pragma unroll
-  for (int t = 0; t < 4; ++t) S[t] = S[t] * eL;
-  GDN_GROUP(SG_DS_RD, 16);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    GDN_GROUP(SG_MFMA, 1);
-    GDN_GROUP(SG_DS_RD, 1);
-    GDN_GROUP(SG_VALU, 2);
-    GDN_GROUP(SG_VMEM_WR, 1);
-    GDN_GROUP(SG_VMEM_RD, 2);
-  }
-  GDN_SCHED_FENCE();
+  lds_barrier();
 
   // ---- R2
+  bf16x8 vh[2], vl[2], vb[2];
 #pragma unroll
-  for (int i = D1; i < D2; ++i) dma_copy<NW>(i, st_next, src_next, wave, lane);
-  f32x4 acc[2];
+  for (int s = 0; s < 2; ++s) {
+    vh[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(&xv[1][s][lane][0]));
+    vl[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(&xv[2][s][lane][0]));
+  }
+  vb[0] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(&xv[0][0][lane][0]));
+  if constexpr (TWO_A) vb[1] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(&xv[0][1][lane][0]));
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int pp = 0; pp < 2; ++pp) acc[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < 4; ++s) acc = mfma(sb[s], as_bf16x8(op.qm[s]), acc);
+  read_rows<0>(nx, nst, q, lane);
+  GDN_SCHED_FENCE();
 #pragma unroll
-  for (int s2 = 0; s2 < 4; ++s2)
+  for (int s = 0; s < 2; ++s) {
 #pragma unroll
-    for (int pp = 0; pp < 2; ++pp) acc[pp] = mfma(as_bf16x8(qb[4 * pp + s2]), sb[s2], acc[pp]);
-  bf16x8 vb[2], vh[2], vl[2];
-  vb[0] = pack_hi(vp[0], vp[1]);
-  vb[1] = pack_hi(vp[2], vp[3]);
+    for (int t = 0; t < 2; ++t) S[t] = mfma(as_bf16x8(op.kt[2 * t + s]), vh[s], S[t]);
 #pragma unroll
-  for (int p2 = 0; p2 < 2; ++p2)  // V'' = diag(e^{gamma_63 - gamma} nk) V', hi + lo
-    pack_hilo(vp[2 * p2] * sk[2 * p2], vp[2 * p2 + 1] * sk[2 * p2 + 1], vh[p2], vl[p2]);
+    for (int t = 0; t < 2; ++t) S[t] = mfma(as_bf16x8(op.kt[2 * t + s]), vl[s], S[t]);
+  }
+  read_rows<1>(nx, nst, q, lane);
+  read_rows<2>(nx, nst, q, lane);
+  read_rows<3>(nx, nst, q, lane);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     GDN_GROUP(SG_MFMA, 1);
-    GDN_GROUP(SG_VALU, 6);
-    GDN_GROUP(SG_VMEM_RD, 1);
+    GDN_GROUP(SG_DS_RD, 2);
   }
   GDN_SCHED_FENCE();
+  xs[q][lane] = __builtin_bit_cast(u32x4, pack_hi(S[0], S[1]));
+  lds_barrier();
 
   // ---- R3
 #pragma unroll
-  for (int s2 = 0; s2 < 2; ++s2) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) S[t] = mfma(as_bf16x8(kb[2 * t + s2]), vh[s2], S[t]);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) S[t] = mfma(as_bf16x8(kb[2 * t + s2]), vl[s2], S[t]);
-  }
-#pragma unroll
-  for (int pp = 0; pp < 2; ++pp) o[pp] = acc[pp] * sq[pp];
-  if constexpr (X == 0) {
-    o[0] = mfma(as_bf16x8(ab[0]), vb[0], o[0]);
-    o[1] = mfma(as_bf16x8(ab[1]), vb[0], o[1]);
-  } else {
-    o[0] = mfma(as_bf16x8(ab[0]), vb[0], o[0]);
-    o[1] = mfma(as_bf16x8(ab[2]), vb[0], o[1]);
-    o[0] = mfma(as_bf16x8(ab[1]), vb[1], o[0]);
-    o[1] = mfma(as_bf16x8(ab[3]), vb[1], o[1]);
-  }
-  sbh[0] = pack_hi(S[0], S[1]);
-  sbh[1] = pack_hi(S[2], S[3]);
-#pragma unroll
-  for (int i = 0; i < 16 + NA; ++i) {
-    GDN_GROUP(SG_MFMA, 1);
-    GDN_GROUP(SG_VALU, 1);
-  }
+  for (int s = 0; s < 4; ++s) sb[s] = __builtin_bit_cast(bf16x8, xs[s][lane]);
+  f32x4 o = acc * op.sq;
+  o = mfma(vb[0], as_bf16x8(op.am[0]), o);
+  if constexpr (TWO_A) o = mfma(vb[1], as_bf16x8(op.am[1]), o);
+  store_out(o);
   GDN_SCHED_FENCE();
 }
 
-// Workgroup = NW waves = NW/2 column slices x 2 state-row halves = 8 NW
-// state columns of one (sequence, v-head).  The two LDS stages and the state
-// exchange leave room for one workgroup per CU, so each wave has a SIMD and
-// the whole register file to itself.  Measured on MI355X at T=4096, 32
-// v-heads: 2 waves (256 workgroups, one per CU) 88 us, 4 waves 96 us; fewer
-// waves per CU leave more of the CU's LDS and vector-memory bandwidth to each.
-constexpr int SCAN_WAVES = 2;
-constexpr int SCAN_COLS = 8 * SCAN_WAVES;  // state columns per workgroup
+// s_waitcnt operand that waits for vmcnt <= n only (lgkmcnt and expcnt at their maxima)
+constexpr int vmcnt_only(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 
-template <int NW, bool BF16_OUT>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1))) void chunk_scan_kernel(ChunkArgs a) {
-  __shared__ u32x4 stage0[ST_U4];
-  __shared__ u32x4 stage1[ST_U4];
-  __shared__ u32x4 xch[2][NW][2 * 64];  // bf16 state halves by (chunk parity, wave, k-step), lane order
+// A loader wave's part of the scan (LD = 0, 1): the copies and the barriers,
+// matching the compute waves' barrier for barrier.  A loader touches LDS only
+// through its copies, whose completion it waits for explicitly, so its
+// barriers carry no fence (a release fence would wait for every copy in
+// flight, including those for the chunk after next).
+template <int LD>
+__device__ __forceinline__ void scan_rows_loader(u32x4 (*stage)[RS_BLOCKS * 64], int nch, int ct, int lane,
+                                                 const ChunkArgs &a, int c0, int h, int hk) {
+  constexpr int N = LD == 0 ? RS_LOADER0 : RS_LOADER1;  // copies per chunk
+  constexpr int H = N / 2;                               // of which before barrier 1
+  auto src_of = [&](int c) {
+    const size_t j = static_cast<size_t>(c0 + c);
+    return row_src(a, j * a.Hv + h, j * a.Hk + hk);
+  };
+  stage_copy<LD>(stage[0], src_of(0), ct, 0, N, lane);
+  if (nch > 1) {
+    stage_copy<LD>(stage[1], src_of(1), ct, 0, N, lane);
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(N));  // chunk 0 landed
+  } else {
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+  }
+  __builtin_amdgcn_s_barrier();  // state exchange; chunk 0 staged
+  __builtin_amdgcn_s_barrier();  // compute waves have read chunk 0
+  for (int c = 0; c < nch; ++c) {
+    if (c + 2 < nch) {
+      const RowSrc r = src_of(c + 2);
+      stage_copy<LD>(stage[c & 1], r, ct, 0, H, lane);
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(H));  // chunk c + 1 landed
+      __builtin_amdgcn_s_barrier();
+      stage_copy<LD>(stage[c & 1], r, ct, H, N, lane);
+    } else {
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+      __builtin_amdgcn_s_barrier();
+    }
+    __builtin_amdgcn_s_barrier();
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+}
+
+template <bool BF16_OUT>
+__global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_kernel(ChunkArgs a) {
+  __shared__ u32x4 stage[2][RS_BLOCKS * 64];  // 122 KiB
+  __shared__ u32x4 xs[4][64];                 // state rows by k-step (bf16), lane order
+  __shared__ u32x2 xv[3][2][64][2];           // V', V'' hi, V'' lo by k-step, lane, half
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int X = wave & 1;    // state-row half of this wave
-  const int sl = wave >> 1;  // column slice within the workgroup
+  const int q = wave & 3;
   const int g4 = lane >> 4;
-  const int r16 = lane & 15;
   const int nh = a.n_seqs * a.Hv;
   const int ct = blockIdx.x / nh;    // the column tiles of one head share bid % 8,
   const int rest = blockIdx.x % nh;  // i.e. one XCD and its L2
   const int n = rest / a.Hv;
   const int h = rest % a.Hv;
   const int hk = h / (a.Hv / a.Hk);
-  const int col = 8 * NW * ct + 16 * sl + r16;
-  const int u_voff = ((4 * (NW / 2 * ct + sl)) * 64 + lane) * 16;  // U blocks of this column slice in a chunk's U region
+  const int col = 16 * ct + (lane & 15);
 
-  // Values read from memory are workgroup-uniform; readfirstlane tells the
-  // compiler so (buffer resources built from them must live in SGPRs).
   int64_t s0;
   int slen;
   seq_bounds(a, n, &s0, &slen);
   s0 = uniform64(s0);
   slen = __builtin_amdgcn_readfirstlane(slen);
-  // Chunks [cs, ce) of sequence n; this launch covers global chunks
-  // [seg_begin, seg_end).  chunk_start is built from clamped lengths, so it
-  // never exceeds the workspace bound; the min() keeps that true here too.
   const int cs = __builtin_amdgcn_readfirstlane(chunk_start_at(a, n));
   const int ce = __builtin_amdgcn_readfirstlane(max(cs, min(chunk_start_at(a, n + 1), a.max_chunks)));
   const int lo = max(cs, a.seg_begin), hi = min(ce, a.seg_end);
   const int64_t in_row = a.h0 ? uniform64(a.h0_idx ? a.h0_idx[n] : n) : -1;
   const int64_t out_row = a.hT ? uniform64(a.hT_idx ? a.hT_idx[n] : n) : -1;
   const int64_t kv = static_cast<int64_t>(DK) * DV;
-  const int row0 = 64 * X;  // first state row of this wave's half
+  const int row0 = 32 * q;  // first state row of a compute wave
   if (cs == ce) {  // empty sequence: the final state is the initial one (handled once)
-    if (a.seg_begin == 0 && out_row >= 0) {
+    if (wave < 4 && a.seg_begin == 0 && out_row >= 0) {
       float *dst = a.hT + (out_row * a.Hv + h) * kv + col;
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = row0 + 16 * t + 4 * g4 + e;
@@ -781,103 +787,76 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
   const int nch = hi - lo;
   const int c0 = lo - a.seg_begin;                             // first chunk, workspace-local
   const int64_t seq_off = static_cast<int64_t>(lo - cs) * CK;  // its first token within the sequence
+  if (wave >= 4) {
+    if (wave == 4)
+      scan_rows_loader<0>(stage, nch, ct, lane, a, c0, h, hk);
+    else
+      scan_rows_loader<1>(stage, nch, ct, lane, a, c0, h, hk);
+    return;
+  }
   float *carry = a.carry + (static_cast<int64_t>(n) * a.Hv + h) * kv + col;
 
-  f32x4 S[4];  // state rows row0 + 16t + 4g + e of this lane's column
+  f32x4 S[2];  // state rows row0 + 16t + 4g + e of this lane's column
   const float *src = lo == cs ? (in_row >= 0 ? a.h0 + (in_row * a.Hv + h) * kv + col : nullptr) : carry;
   if (src) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int e = 0; e < 4; ++e) S[t][e] = src[(row0 + 16 * t + 4 * g4 + e) * DV];
   } else {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) S[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < 2; ++t) S[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  bf16x8 sbh[2], sbp[2];
-  sbh[0] = pack_hi(S[0], S[1]);
-  sbh[1] = pack_hi(S[2], S[3]);
 
-  // Output addressing: byte offsets of this wave's rows 32X + 16pp + 4g + e within a chunk.
+  // Output addressing: byte offset of this lane's row 16q + r, columns
+  // 16 ct + 4g .. +3, within a chunk (rows past the sequence end fall outside
+  // the buffer range and are dropped).
   typedef typename std::conditional<BF16_OUT, uint16_t, float>::type OT;
   const int64_t ostep = static_cast<int64_t>(a.Hv) * DV;  // elements per token
-  const int row_bytes = static_cast<int>(ostep * sizeof(OT));
-  const int voff0 = static_cast<int>(((32 * X + 4 * g4) * ostep + h * DV + col) * sizeof(OT));
-  auto out_rsrc = [&](int c) {  // chunk c of this launch: rows [0, min(64, rest of sequence))
+  const int voff = static_cast<int>(((16 * q + (lane & 15)) * ostep + h * DV + 16 * ct + 4 * g4) * sizeof(OT));
+  auto store_out = [&](const f32x4 &o, int c) {  // chunk c of this launch: rows [0, min(64, rest of sequence))
     const int64_t toff = seq_off + static_cast<int64_t>(c) * CK;
     const int rows = static_cast<int>(min<int64_t>(CK, slen - toff));
     OT *base = static_cast<OT *>(a.o) + (s0 + toff) * ostep;
-    return __builtin_amdgcn_make_buffer_rsrc(base, 0, static_cast<int>(rows * ostep * sizeof(OT)), BUF_DWORD3);
-  };
-  // Before the first chunk there is no output to store: a zero-sized range.
-  __amdgpu_buffer_rsrc_t prev = __builtin_amdgcn_make_buffer_rsrc(a.o, 0, 0, BUF_DWORD3);
-  f32x4 o[2];
-#pragma unroll
-  for (int pp = 0; pp < 2; ++pp) o[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // Chunk cidx of this launch (clamped: after the last chunk the "next"
-  // copies reload the last chunk into the idle stage).
-  auto chunk_of = [&](int cidx) { return static_cast<size_t>(c0 + min(cidx, nch - 1)); };
-  auto src_of = [&](int cidx) { const size_t j = chunk_of(cidx); return stage_src<NW>(a, j * a.Hv + h, j * a.Hk + hk); };
-  auto u_rsrc_of = [&](int cidx) {
-    return __builtin_amdgcn_make_buffer_rsrc(a.Ut + (chunk_of(cidx) * a.Hv + h) * (DV * CK), 0, DV * CK * 4, BUF_DWORD3);
-  };
-  // the state exchange: write this wave's half, (barrier), read the partner's
-  auto put_half = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) xch[buf][wave][j * 64 + lane] = __builtin_bit_cast(u32x4, sbh[j]);
-  };
-  auto get_half = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) sbp[j] = __builtin_bit_cast(bf16x8, xch[buf][wave ^ 1][j * 64 + lane]);
-  };
-  auto run = [&](const u32x4 *st, const f32x4 (&u)[4], const u32x4 (&kb)[8], u32x4 *st_next, int next,
-                 f32x4 (&u_next)[4], u32x4 (&kb_next)[8]) {
-    if (X)
-      scan_chunk<NW, 1, BF16_OUT>(st, u, S, sbh, sbp, o, prev, voff0, row_bytes, st_next, src_of(next), u_next,
-                                  u_rsrc_of(next), u_voff, kb, kb_next, wave, lane);
+    const auto r = __builtin_amdgcn_make_buffer_rsrc(base, 0, static_cast<int>(rows * ostep * sizeof(OT)), BUF_DWORD3);
+    if constexpr (BF16_OUT)
+      __builtin_amdgcn_raw_buffer_store_b64(pack4(o), r, voff, 0, 0);
     else
-      scan_chunk<NW, 0, BF16_OUT>(st, u, S, sbh, sbp, o, prev, voff0, row_bytes, st_next, src_of(next), u_next,
-                                  u_rsrc_of(next), u_voff, kb, kb_next, wave, lane);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), r, voff, 0, 0);
   };
-  f32x4 u0[4], u1[4];
-  u32x4 k0[8], k1[8];  // K^T blocks of this wave's state half, current / next chunk
-  {
-    const StageSrc src0 = src_of(0);
+  bf16x8 sb[4];  // the whole state as bf16 B operands, by k-step
+  auto chunk = [&](const RowOps &op, RowOps &nx, int c) {
+    // (after the last chunk the "next" reads take the idle buffer's stale contents, unused)
+    const u32x4 *nst = stage[(c + 1) & 1];
+    auto out = [&](const f32x4 &o) { store_out(o, c); };
+    if (q >= 2)
+      scan_rows_chunk<true>(op, nx, nst, sb, S, xv, xs, q, lane, out);
+    else
+      scan_rows_chunk<false>(op, nx, nst, sb, S, xv, xs, q, lane, out);
+  };
+
+  RowOps op0, op1;
+  xs[q][lane] = __builtin_bit_cast(u32x4, pack_hi(S[0], S[1]));
+  lds_barrier();  // state exchange; chunk 0 staged
 #pragma unroll
-    for (int i = 0; i < Dma<NW>::n; ++i) dma_copy<NW>(i, stage0, src0, wave, lane);
-    load_u(u0, u_rsrc_of(0), u_voff);
-    if (X) load_kt<1>(k0, src0.kh, lane); else load_kt<0>(k0, src0.kh, lane);
-  }
-  put_half(0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  get_half(0);
-  // A chunk's output is stored during the next chunk (vmcnt counts stores
-  // too, so the wait at the end of each chunk then finds them long done).
-  // Chunk c reads the state exchange buffer c % 2 and writes (c + 1) % 2; a
-  // buffer is rewritten only after the barrier that follows its last read.
+  for (int s = 0; s < 4; ++s) sb[s] = __builtin_bit_cast(bf16x8, xs[s][lane]);
+  read_rows<0>(op0, stage[0], q, lane);
+  read_rows<1>(op0, stage[0], q, lane);
+  read_rows<2>(op0, stage[0], q, lane);
+  read_rows<3>(op0, stage[0], q, lane);
+  lds_barrier();  // chunk 0 read: its buffer may be refilled
+  // xv and xs are each written after the barrier that follows their last
+  // read, so one buffer of each suffices.
   for (int c = 0; c < nch; c += 2) {
-    run(stage0, u0, k0, stage1, c + 1, u1, k1);
-    prev = out_rsrc(c);
-    put_half(1);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    get_half(1);
+    chunk(op0, op1, c);
     if (c + 1 >= nch) break;
-    run(stage1, u1, k1, stage0, c + 2, u0, k0);
-    prev = out_rsrc(c + 1);
-    put_half(0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    get_half(0);
+    chunk(op1, op0, c + 1);
   }
-  store_chunk<BF16_OUT>(o, prev, voff0, row_bytes);
 
   float *dst = hi == ce ? (out_row >= 0 ? a.hT + (out_row * a.Hv + h) * kv + col : nullptr) : carry;
   if (dst) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int e = 0; e < 4; ++e) dst[(row0 + 16 * t + 4 * g4 + e) * DV] = S[t][e];
   }
@@ -1033,10 +1012,10 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
   };
   auto launch_scan = [&](hipStream_t st) {
     if (o_dtype == GDN_DTYPE_BF16)
-      hipLaunchKernelGGL((chunk_scan_kernel<SCAN_WAVES, true>), dim3(static_cast<unsigned>(scan_blocks)),
+      hipLaunchKernelGGL((chunk_scan_kernel<true>), dim3(static_cast<unsigned>(scan_blocks)),
                          dim3(64 * SCAN_WAVES), 0, st, a);
     else
-      hipLaunchKernelGGL((chunk_scan_kernel<SCAN_WAVES, false>), dim3(static_cast<unsigned>(scan_blocks)),
+      hipLaunchKernelGGL((chunk_scan_kernel<false>), dim3(static_cast<unsigned>(scan_blocks)),
                          dim3(64 * SCAN_WAVES), 0, st, a);
   };
   hipStream_t s = static_cast<hipStream_t>(stream);
