@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 2
+#define GDN_ABI_VERSION 3
 
 typedef enum {
   GDN_OK = 0,
@@ -242,6 +242,21 @@ int causal_conv1d_update(const void *x, int64_t x_stride_t, void *conv_state,
 int gdn_state_commit(float *pool, const int64_t *slot_ids, const float *snapshots,
                      const int32_t *accepted_len, int32_t n_seqs, int32_t T,
                      int32_t H, int32_t K, int32_t V, void *stream);
+
+/*
+ * Speculative-verify commit of the causal-conv window:
+ *   pool[slot_ids[b]][c][j] = hist[b][c][a + j]   (j < S, a = min(accepted_len[b], L - S))
+ * where hist[b] is the verify step's conv history: the S-column window
+ * before the step followed by the step's L - S inputs, so columns
+ * [a, a + S) are the window after the first a tokens.  accepted_len[b] <= 0
+ * or slot_ids[b] < 0 leaves the slot untouched.  Rolls back the conv state
+ * that engine/runtime/spec_decode.py:81-87 leaves without a rollback.
+ *   pool [*, C, S] and hist [n_seqs, C, L] of dtype (bf16 or fp32)
+ *   slot_ids int64 [n_seqs];  accepted_len int32 [n_seqs]
+ */
+int gdn_conv_state_commit(void *pool, const int64_t *slot_ids, const void *hist,
+                          const int32_t *accepted_len, int32_t n_seqs, int32_t C, int32_t S,
+                          int32_t L, int32_t dtype, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1,6 +1,9 @@
 // Speculative-verify commit: copy the snapshot of the last accepted draft
 // token into the slot pool.  A pure 64 KiB-per-(sequence, head) copy, so
-// each workgroup streams one state with 16-byte loads and stores.
+// each workgroup streams one state with 16-byte loads and stores.  The conv
+// window commit does the same for the causal-conv state: the window after
+// the accepted tokens is a slice of the verify step's history (the window
+// before the step followed by the step's inputs), one thread per channel.
 //
 // No reference implementation: engine/runtime/spec_decode.py:81-87 and
 // :99-103 record that GDN rollback "requires saving state snapshots".
@@ -26,8 +29,45 @@ __global__ __launch_bounds__(COMMIT_NT) void commit_kernel(float *pool, const in
   for (int64_t i = threadIdx.x; i < n4; i += COMMIT_NT) dst[i] = src[i];
 }
 
+template <typename T>
+__global__ __launch_bounds__(COMMIT_NT) void conv_commit_kernel(T *pool, const int64_t *slot_ids, const T *hist,
+                                                                const int32_t *acc, int C, int S, int L, int steps) {
+  const int b = blockIdx.y;
+  const int c = blockIdx.x * COMMIT_NT + threadIdx.x;
+  const int64_t slot = slot_ids[b];
+  const int a = acc[b];
+  if (c >= C || slot < 0 || a <= 0) return;
+  const int first = a > steps ? steps : a;  // window after `first` tokens: history columns [first, first + S)
+  const T *src = hist + (static_cast<int64_t>(b) * C + c) * L + first;
+  T *dst = pool + (slot * C + c) * S;
+  for (int j = 0; j < S; ++j) dst[j] = src[j];
+}
+
 }  // namespace
 }  // namespace gdn
+
+extern "C" int gdn_conv_state_commit(void *pool, const int64_t *slot_ids, const void *hist,
+                                     const int32_t *accepted_len, int32_t n_seqs, int32_t C, int32_t S,
+                                     int32_t L, int32_t dtype, void *stream) {
+  using namespace gdn;
+  if (n_seqs < 0 || C <= 0 || S <= 0 || L <= S || n_seqs > 65535)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_conv_state_commit: bad sizes n_seqs=%d C=%d S=%d L=%d", n_seqs, C,
+                S, L);
+  if (dtype != GDN_DTYPE_BF16 && dtype != GDN_DTYPE_F32)
+    return fail(GDN_ERR_UNSUPPORTED, "gdn_conv_state_commit: dtype %d (bf16 or fp32)", dtype);
+  if (n_seqs == 0) return ok();
+  if (!pool || !slot_ids || !hist || !accepted_len)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_conv_state_commit: null pointer");
+  const dim3 grid((C + COMMIT_NT - 1) / COMMIT_NT, n_seqs);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == GDN_DTYPE_BF16)
+    hipLaunchKernelGGL(conv_commit_kernel<uint16_t>, grid, dim3(COMMIT_NT), 0, st, static_cast<uint16_t *>(pool),
+                       slot_ids, static_cast<const uint16_t *>(hist), accepted_len, C, S, L, L - S);
+  else
+    hipLaunchKernelGGL(conv_commit_kernel<float>, grid, dim3(COMMIT_NT), 0, st, static_cast<float *>(pool), slot_ids,
+                       static_cast<const float *>(hist), accepted_len, C, S, L, L - S);
+  return check_launch("gdn_conv_state_commit");
+}
 
 extern "C" int gdn_state_commit(float *pool, const int64_t *slot_ids, const float *snapshots,
                                 const int32_t *accepted_len, int32_t n_seqs, int32_t T,

@@ -10,13 +10,17 @@ third-party packages (fla, causal-conv1d) via HF:
 - ``fused_recurrent_gated_delta_rule``  decode / spec-verify recurrence
 - ``recurrent_gated_delta_rule``        HF-signature adapter of the above
 - ``causal_conv1d_fn``, ``causal_conv1d_update``
-- ``gdn_state_commit``, ``LinearAttentionSlotPool``
+- ``gdn_state_commit``, ``gdn_conv_state_commit``, ``LinearAttentionSlotPool``
 - ``chunk_gated_delta_rule_from_projections``,
   ``fused_recurrent_gated_delta_rule_from_projections``  gates computed in
   the kernels from the layer's raw a / b projections
 - ``rms_norm_gated``                    the GDN output norm in one pass
 - ``gated_delta_net_forward``, ``install_gdn_layer_patch``  HF's GDN layer
   forward on these kernels (native GQA, fused gates and norm)
+
+The engine side (slot-indexed pools in place of the reference cache's
+gather/scatter, and the speculative-verify rollback) is
+:mod:`engine.runtime.slot_pools`.
 
 All of them run hand-written HIP kernels from ``libgdn_mi355x.so`` through
 a C ABI (include/gdn_capi.h); there is no CPU or Triton fallback.
@@ -27,7 +31,7 @@ from .delta_rule import (chunk_gated_delta_rule, chunk_gated_delta_rule_from_pro
 from .fused_recurrent import (fused_recurrent_gated_delta_rule, fused_recurrent_gated_delta_rule_from_projections,
                               recurrent_gated_delta_rule)
 from .gdn_layer import gated_delta_net_forward, install_gdn_layer_patch, rms_norm_gated
-from .state_pool import LinearAttentionSlotPool, gdn_state_commit
+from .state_pool import LinearAttentionSlotPool, gdn_conv_state_commit, gdn_state_commit
 
 __all__ = [
     "chunk_gated_delta_rule",
@@ -37,6 +41,7 @@ __all__ = [
     "causal_conv1d_fn",
     "causal_conv1d_update",
     "gdn_state_commit",
+    "gdn_conv_state_commit",
     "LinearAttentionSlotPool",
     "chunk_gated_delta_rule_from_projections",
     "fused_recurrent_gated_delta_rule_from_projections",

@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libgdn_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 GDN_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
@@ -97,6 +97,9 @@ SIGNATURES = {
     "gdn_state_commit": (_int, [
         _c_void_p, _c_void_p, _c_void_p, _c_void_p,
         _i32, _i32, _i32, _i32, _i32, _c_void_p]),
+    "gdn_conv_state_commit": (_int, [
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # pool slot_ids hist accepted_len
+        _i32, _i32, _i32, _i32, _int, _c_void_p]),   # n_seqs C S L dtype stream
 }
 
 _LIB: Optional[ctypes.CDLL] = None

@@ -12,7 +12,10 @@ kernels.  Differences from the reference entry, all additive:
 * q/k may carry fewer heads than v (native GQA, v-head j uses k-head
   j // (Hv // Hk)), so HF's ``repeat_interleave`` copy is optional;
 * ``initial_state`` may be a slot pool addressed by ``ssm_state_indices``,
-  and ``inplace_final_state=True`` writes the final states back into it.
+  and ``inplace_final_state=True`` writes the final states back into it;
+  ``has_initial_state`` [N] bool starts the sequences marked False from a
+  zero state (a fresh prefill into its slot) while their final states still
+  land in the pool.
 
 The reference's opt-out variable ``PARIS_DISABLE_HELION_DELTA=1`` keeps its
 meaning for :func:`install_delta_rule_monkeypatch` (nothing is patched);
@@ -48,6 +51,7 @@ def chunk_gated_delta_rule(
     scale: Optional[float] = None,
     ssm_state_indices: Optional[torch.Tensor] = None,
     inplace_final_state: bool = False,
+    has_initial_state: Optional[torch.Tensor] = None,
     **_ignored,
 ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """Chunk-64 (WY/UT) gated delta rule forward.
@@ -70,7 +74,8 @@ def chunk_gated_delta_rule(
     g32, beta_c = g32.contiguous(), beta_c.contiguous()  # the precomputed-gate ABI takes token stride Hv
     gates = ("gdn_chunk_fwd", [_lib.ptr(g32), _lib.ptr(beta_c), _lib.dtype_code(beta_c, "beta")])
     return _chunk(query, key, value, gates, chunk_size, initial_state, output_final_state,
-                  use_qk_l2norm_in_kernel, cu_seqlens, scale, ssm_state_indices, inplace_final_state)
+                  use_qk_l2norm_in_kernel, cu_seqlens, scale, ssm_state_indices, inplace_final_state,
+                  has_initial_state)
 
 
 def chunk_gated_delta_rule_from_projections(
@@ -88,6 +93,7 @@ def chunk_gated_delta_rule_from_projections(
     scale: Optional[float] = None,
     ssm_state_indices: Optional[torch.Tensor] = None,
     inplace_final_state: bool = False,
+    has_initial_state: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """:func:`chunk_gated_delta_rule` with the gates computed inside the
     kernel from the GDN layer's raw projections (``a``, ``b`` ``[B, T, Hv]``,
@@ -112,13 +118,15 @@ def chunk_gated_delta_rule_from_projections(
                                      _lib.ptr(alog), _lib.ptr(dtb)])
     keep = (ax, bx, alog, dtb)  # alive until the launch is enqueued
     out = _chunk(query, key, value, gates, CHUNK_SIZE, initial_state, output_final_state,
-                 use_qk_l2norm_in_kernel, cu_seqlens, scale, ssm_state_indices, inplace_final_state)
+                 use_qk_l2norm_in_kernel, cu_seqlens, scale, ssm_state_indices, inplace_final_state,
+                 has_initial_state)
     del keep
     return out
 
 
 def _chunk(query, key, value, gates, chunk_size, initial_state, output_final_state,
-           use_qk_l2norm_in_kernel, cu_seqlens, scale, ssm_state_indices, inplace_final_state):
+           use_qk_l2norm_in_kernel, cu_seqlens, scale, ssm_state_indices, inplace_final_state,
+           has_initial_state=None):
     """Shared body: shape checks, state / workspace plumbing and the launch.
     ``gates`` = (entry point, its gate arguments)."""
     if chunk_size != CHUNK_SIZE:
@@ -164,6 +172,14 @@ def _chunk(query, key, value, gates, chunk_size, initial_state, output_final_sta
         if h0 is None:
             raise ValueError("inplace_final_state needs initial_state (the pool)")
         final, hT, hT_idx = h0, h0, idx
+    if has_initial_state is not None:
+        if h0 is None:
+            raise ValueError("has_initial_state needs initial_state")
+        has = has_initial_state.to(device=dev, dtype=torch.bool).reshape(-1)
+        if has.numel() != n_seqs:
+            raise ValueError(f"has_initial_state has {has.numel()} entries for {n_seqs} sequences")
+        rows = idx if idx is not None else torch.arange(n_seqs, device=dev, dtype=torch.int64)
+        h0_idx = torch.where(has, rows, torch.full_like(rows, -1))
     elif output_final_state:
         final = hT = torch.empty((n_seqs, hv, dk, dv), dtype=torch.float32, device=dev)
 

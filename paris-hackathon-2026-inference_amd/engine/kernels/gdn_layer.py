@@ -16,8 +16,11 @@ the kernel prologues (``*_from_projections``), q/k passed at their 16 heads
 (native GQA), and the norm as one HIP pass (:func:`rms_norm_gated`).  The
 projections stay torch matmuls (hipBLASLt) and the conv runs the HIP
 ``causal_conv1d`` kernels; the cache calls are HF's own, in HF's order, so
-the layer works with the transformers cache unchanged.
-:func:`install_gdn_layer_patch` swaps it in for the HF layer classes.
+the layer works with the transformers cache unchanged.  With an engine
+slot-pool cache (``cache_params.gdn_slot_pools``, see
+:mod:`engine.runtime.slot_pools`) the kernels address the pools by slot id
+instead.  :func:`install_gdn_layer_patch` swaps it in for the HF layer
+classes.
 """
 from __future__ import annotations
 
@@ -80,6 +83,9 @@ def gated_delta_net_forward(self, hidden_states: torch.Tensor, cache_params=None
     transformers qwen3_5_moe / qwen3_5 / qwen3_next) on the MI355X kernels.
     Same inputs, cache protocol and output as the HF method
     (modeling_qwen3_5_moe.py:430-541)."""
+    pools = getattr(cache_params, "gdn_slot_pools", None) if cache_params is not None else None
+    if pools is not None:
+        return _forward_on_pools(self, hidden_states, pools, attention_mask)
     hf = sys.modules[type(self).__module__]
     hidden_states = hf.apply_mask_to_padding_states(hidden_states, attention_mask)
     batch_size, seq_len, _ = hidden_states.shape
@@ -127,6 +133,63 @@ def gated_delta_net_forward(self, hidden_states: torch.Tensor, cache_params=None
             output_final_state=cache_params is not None, use_qk_l2norm_in_kernel=True, cu_seqlens=cu)
         if cache_params is not None:
             cache_params.update_recurrent_state(last, self.layer_idx)
+
+    z = z.reshape(batch_size, seq_len, -1, self.head_v_dim)
+    out = rms_norm_gated(core, z, self.norm.weight, self.norm.variance_epsilon)
+    return self.out_proj(out.reshape(batch_size, seq_len, -1))
+
+
+# decode steps longer than this (a continued prefill) take the chunk kernels
+_RECURRENT_MAX_T = 16
+
+
+def _forward_on_pools(self, hidden_states: torch.Tensor, pools, attention_mask: Optional[torch.Tensor]) -> torch.Tensor:
+    """The layer forward on slot pools (:class:`engine.runtime.slot_pools.GDNSlotPools`):
+    conv and recurrent state are read from and written to ``pool[slot]`` by
+    the kernels, rows as bound by ``pools.bind``.  Prefill rows start from
+    a zero state and leave their final state and conv window in their slot;
+    decode rows continue from their slot; a bound verify step also records
+    the snapshots and conv history that ``pools.commit_verify`` rolls back to."""
+    hf = sys.modules[type(self).__module__]
+    hidden_states = hf.apply_mask_to_padding_states(hidden_states, attention_mask)
+    batch_size, seq_len, _ = hidden_states.shape
+    conv_pool, rec_pool = pools.layer(self.layer_idx)
+    slots = pools.slots()
+    if slots.numel() != batch_size:
+        raise ValueError(f"pools bound for {slots.numel()} rows, forward has {batch_size}")
+    verify = pools.verify_tokens
+    if verify and seq_len != verify:
+        raise ValueError(f"verify step bound for {verify} tokens, forward has {seq_len}")
+
+    mixed_qkv = self.in_proj_qkv(hidden_states).transpose(1, 2)  # [B, conv_dim, L]
+    z = self.in_proj_z(hidden_states)
+    b = self.in_proj_b(hidden_states)
+    a = self.in_proj_a(hidden_states)
+    conv_w = self.conv1d.weight.squeeze(1)
+    if pools.decode and seq_len == 1:
+        mixed_qkv = causal_conv1d_update(mixed_qkv, conv_pool, conv_w, self.conv1d.bias, self.activation,
+                                         conv_state_indices=slots)
+    else:
+        if verify:
+            pools.record_conv(self.layer_idx, mixed_qkv)
+        mixed_qkv = causal_conv1d_fn(mixed_qkv, conv_w, self.conv1d.bias, activation=self.activation,
+                                     conv_states=conv_pool, cache_indices=slots, has_initial_state=pools.has_state())
+
+    mixed_qkv = mixed_qkv.transpose(1, 2)
+    query, key, value = torch.split(mixed_qkv, [self.key_dim, self.key_dim, self.value_dim], dim=-1)
+    query = query.reshape(batch_size, seq_len, -1, self.head_k_dim)
+    key = key.reshape(batch_size, seq_len, -1, self.head_k_dim)
+    value = value.reshape(batch_size, seq_len, -1, self.head_v_dim)
+    if pools.decode and seq_len <= _RECURRENT_MAX_T:
+        core, _ = fused_recurrent_gated_delta_rule_from_projections(
+            query, key, value, a, b, self.A_log, self.dt_bias, initial_state=rec_pool,
+            use_qk_l2norm_in_kernel=True, ssm_state_indices=slots, inplace_final_state=True,
+            snapshots=pools.snapshots(self.layer_idx) if verify else None)
+    else:
+        core, _ = chunk_gated_delta_rule_from_projections(
+            query, key, value, a, b, self.A_log, self.dt_bias, initial_state=rec_pool,
+            use_qk_l2norm_in_kernel=True, ssm_state_indices=slots, inplace_final_state=True,
+            has_initial_state=pools.has_state())
 
     z = z.reshape(batch_size, seq_len, -1, self.head_v_dim)
     out = rms_norm_gated(core, z, self.norm.weight, self.norm.variance_epsilon)

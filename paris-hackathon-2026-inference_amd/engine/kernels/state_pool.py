@@ -44,6 +44,37 @@ def gdn_state_commit(pool: torch.Tensor, slot_ids: torch.Tensor, snapshots: torc
     return pool
 
 
+def gdn_conv_state_commit(pool: torch.Tensor, slot_ids: torch.Tensor, hist: torch.Tensor,
+                          accepted_len: torch.Tensor) -> torch.Tensor:
+    """Roll a causal-conv state pool back to the window after each
+    sequence's accepted tokens, on the GPU, in place.
+
+    ``hist`` ``[N, C, S + T]`` is a verify step's conv history: the S-column
+    window before the step, then the step's T inputs; the window after the
+    first ``a = accepted_len[b]`` tokens is ``hist[b, :, a:a + S]`` (a clamped
+    to T).  ``accepted_len[b] <= 0`` or a negative slot leaves that slot
+    untouched.  The conv half of the rollback that
+    engine/runtime/spec_decode.py:81-87 leaves unimplemented.
+    """
+    dev = _lib.require_gpu(pool, hist)
+    if pool.dtype != hist.dtype or pool.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("pool and hist must share a dtype, bf16 or fp32")
+    if not pool.is_contiguous() or not hist.is_contiguous():
+        raise ValueError("pool and hist must be contiguous")
+    n, c, length = hist.shape
+    s = pool.shape[2]
+    if pool.shape[1] != c or length <= s:
+        raise ValueError(f"hist {tuple(hist.shape)} does not extend pool windows {tuple(pool.shape)}")
+    idx = _lib.as_index(slot_ids, dev)
+    acc = accepted_len.to(device=dev, dtype=torch.int32).contiguous()
+    if idx.numel() != n or acc.numel() != n:
+        raise ValueError("slot_ids and accepted_len need one entry per sequence")
+    st = _lib.load().gdn_conv_state_commit(_lib.ptr(pool), _lib.ptr(idx), _lib.ptr(hist), _lib.ptr(acc),
+                                           n, c, s, length, _lib.GDN_DTYPE[pool.dtype], _lib.stream_of(pool))
+    _lib.check(st, "gdn_conv_state_commit")
+    return pool
+
+
 class LinearAttentionSlotPool:
     """One GDN layer's pooled state, addressed by slot id (no gather/scatter).
 

@@ -30,7 +30,7 @@ def test_header_lists_the_entry_points():
     assert header_functions() == sorted([
         "causal_conv1d_fwd", "causal_conv1d_update", "gdn_abi_version", "gdn_chunk_fwd",
         "gdn_chunk_fwd_gated", "gdn_chunk_workspace_bytes", "gdn_last_error_string", "gdn_recurrent_fwd",
-        "gdn_recurrent_fwd_gated", "gdn_rmsnorm_gated_fwd", "gdn_state_commit"])
+        "gdn_recurrent_fwd_gated", "gdn_rmsnorm_gated_fwd", "gdn_state_commit", "gdn_conv_state_commit"])
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -41,7 +41,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.gdn_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.gdn_abi_version() == _lib.ABI_VERSION == 3
 
 
 def _rec_call(lib, **over):
@@ -82,6 +82,10 @@ def test_conv_rejects_bad_shapes(lib):
 def test_commit_rejects_bad_sizes(lib):
     assert lib.gdn_state_commit(1, 1, 1, 1, 2, 0, 32, 128, 128, None) == 1
     assert lib.gdn_state_commit(None, 1, 1, 1, 2, 4, 32, 128, 128, None) == 1
+    assert lib.gdn_conv_state_commit(1, 1, 1, 1, 2, 8192, 4, 4, 1, None) == 1   # L must exceed S
+    assert lib.gdn_conv_state_commit(None, 1, 1, 1, 2, 8192, 4, 8, 1, None) == 1
+    assert lib.gdn_conv_state_commit(1, 1, 1, 1, 2, 8192, 4, 8, 3, None) == 2   # dtype
+    assert lib.gdn_conv_state_commit(None, None, None, None, 0, 8192, 4, 8, 1, None) == 0  # nothing to do
 
 
 def test_chunk_workspace_is_host_arithmetic(lib):
