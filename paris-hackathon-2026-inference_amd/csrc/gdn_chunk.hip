@@ -139,6 +139,18 @@ __device__ __forceinline__ int chunk_start_at(const ChunkArgs &a, int n) {
   return a.cu ? a.chunk_start[n] : n * ((a.T + CK - 1) / CK);
 }
 
+// Workgroup order that keeps the workgroups reading one k-head's q and k
+// (its R = Hv / Hk v-heads, GQA; and for the scan their column tiles) on one
+// XCD, so that they share its L2: the dispatcher hands workgroup `bid` to XCD
+// bid % 8, so bid = x + 8 t with t = per * gq + m serves group g = 8 gq + x,
+// member m < per.  Needs the group count to be a multiple of 8 (else the
+// caller keeps its plain order).
+__device__ __forceinline__ void xcd_group_order(int bid, int per, int *g, int *m) {
+  const int x = bid & 7, t = bid >> 3;
+  *g = 8 * (t / per) + x;
+  *m = t % per;
+}
+
 // ------------------------------------------------------------------ chunk table
 __global__ __launch_bounds__(256) void chunk_table_kernel(ChunkArgs a) {
   __shared__ int32_t part[256];
@@ -218,17 +230,29 @@ __device__ __forceinline__ f32x4 mm16(f32x4 a, f32x4 b, f32x4 acc) {
 
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
-__global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void chunk_prep_kernel(ChunkArgs a) {
   __shared__ __align__(16) uint16_t kn[CK * DK];  // K rows (swizzled)
-  __shared__ __align__(16) uint16_t vn[CK * DV];  // V rows (swizzled)
-  __shared__ __align__(16) f32x4 lbuf[4 * 64];    // diagonal blocks of L, row layout by lane
-  __shared__ __align__(16) f32x4 dxch[4 * 64];    // diagonal blocks of T, D layout by lane
-  __shared__ __align__(16) f32x4 txch[3 * 64];    // T[1][0], T[2][1], T[2][0], D layout by lane
-  __shared__ __align__(16) float dtr[4][16 * 20];  // D layout -> row layout transposes
+  // V rows (swizzled) share 16 KiB with the solve's exchange buffers: V is
+  // first read by the W/U products, after the solve's last exchange, and
+  // waits in registers until then.  (4 workgroups fit a CU's LDS instead of 3.)
+  __shared__ __align__(16) f32x4 shared16k[1024];
+  uint16_t *vn = reinterpret_cast<uint16_t *>(shared16k);
+  f32x4 *lbuf = shared16k;                // [4 * 64] diagonal blocks of L, row layout by lane
+  f32x4 *dxch = shared16k + 4 * 64;       // [4 * 64] diagonal blocks of T, D layout by lane
+  f32x4 *txch = shared16k + 8 * 64;       // [3 * 64] T[1][0], T[2][1], T[2][0], D layout by lane
+  float(*dtr)[16 * 20] = reinterpret_cast<float(*)[16 * 20]>(shared16k + 11 * 64);  // D -> row layout
+  static_assert(CK * DV * 2 == sizeof(f32x4) * 1024 && (11 * 64) * 16 + 4 * 16 * 20 * 4 == 16384, "layout");
   __shared__ __align__(16) float gam_s[CK], beta_s[CK], nk_s[CK], nq_s[CK], colw_s[CK];
 
-  const int h = blockIdx.x;
-  const int j = a.seg_begin + static_cast<int>(blockIdx.y);  // global chunk index
+  const int ratio = a.Hv / a.Hk;
+  int h = blockIdx.x, jl = blockIdx.y;  // v-head; chunk index within the segment's workspace
+  if ((a.Hk * static_cast<int>(gridDim.y)) % 8 == 0) {  // the v-heads of one k-head on one XCD
+    int g, m;
+    xcd_group_order(blockIdx.x + gridDim.x * blockIdx.y, ratio, &g, &m);
+    h = (g % a.Hk) * ratio + m;
+    jl = g / a.Hk;
+  }
+  const int j = a.seg_begin + jl;  // global chunk index
   if (j >= a.seg_end || j >= chunk_start_at(a, a.n_seqs)) return;
   int lo = 0, hi = a.n_seqs;  // sequence owning chunk j: last n with chunk_start[n] <= j
   if (!a.cu) {
@@ -247,7 +271,6 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
   const int64_t t0 = s0 + static_cast<int64_t>(c) * CK;
   const int len = min(CK, slen - c * CK);
   if (len <= 0) return;
-  const int ratio = a.Hv / a.Hk;
   const int hk = h / ratio;
   const bool khead_writer = (h % ratio) == 0;
 
@@ -256,7 +279,6 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
   const int p = tid >> 6;  // this wave's row block
   const int g4 = lane >> 4;
   const int r16 = lane & 15;
-  const int jl = static_cast<int>(blockIdx.y);  // chunk index within the segment's workspace
   const size_t ch = static_cast<size_t>(jl) * a.Hv + h;
   const size_t chk = static_cast<size_t>(jl) * a.Hk + hk;
   const int irow = 16 * p + r16;  // this lane's chunk row in row-layout / pi fragments
@@ -296,7 +318,6 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
   for (int it = 0; it < 4; ++it) {
     const int row = (tid >> 4) + 16 * it;
     *reinterpret_cast<u32x4 *>(kn + nsw(row, seg * 8)) = ku[it];
-    *reinterpret_cast<u32x4 *>(vn + nsw(row, seg * 8)) = vu[it];
     float sk = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -450,6 +471,11 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(ChunkArgs a) {
     x = mm16(lf[2], txch[2 * 64 + lane], x);  // T[2][0]
     trow[0] = -mm16(x, drow, z4);
   }
+  __syncthreads();  // the exchange buffers are free: V rows take their place
+#pragma unroll
+  for (int it = 0; it < 4; ++it)
+    *reinterpret_cast<u32x4 *>(vn + nsw((tid >> 4) + 16 * it, seg * 8)) = vu[it];
+  __syncthreads();
 
   // ---- A.4: W^T = K^T (T diag(colw))^T and U = T diag(beta) V on bf16 MFMA,
   // with the T factors split into bf16 hi + lo.  Reduction over chunk
@@ -751,11 +777,18 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_kernel(ChunkArgs a
   const int q = wave & 3;
   const int g4 = lane >> 4;
   const int nh = a.n_seqs * a.Hv;
-  const int ct = blockIdx.x / nh;    // the column tiles of one head share bid % 8,
-  const int rest = blockIdx.x % nh;  // i.e. one XCD and its L2
+  const int ratio = a.Hv / a.Hk;
+  int ct = blockIdx.x / nh;    // plain order: the column tiles of one head share bid % 8,
+  int rest = blockIdx.x % nh;  // i.e. one XCD and its L2
+  if ((a.n_seqs * a.Hk) % 8 == 0) {  // also the v-heads of one k-head
+    int g, m;
+    xcd_group_order(blockIdx.x, ratio * (DV / SCAN_COLS), &g, &m);
+    ct = m % (DV / SCAN_COLS);
+    rest = (g / a.Hk) * a.Hv + (g % a.Hk) * ratio + m / (DV / SCAN_COLS);
+  }
   const int n = rest / a.Hv;
   const int h = rest % a.Hv;
-  const int hk = h / (a.Hv / a.Hk);
+  const int hk = h / ratio;
   const int col = 16 * ct + (lane & 15);
 
   int64_t s0;
