@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 3
+#define GDN_ABI_VERSION 4
 
 typedef enum {
   GDN_OK = 0,
@@ -77,9 +77,14 @@ const char *gdn_last_error_string(void);
  *   q, k      [tokens, Hk, K] (qkv_dtype, token stride q_stride_t/k_stride_t)
  *   v         [tokens, Hv, V] (qkv_dtype, token stride v_stride_t)
  *   g         [tokens, Hv] fp32 log-decay;  beta [tokens, Hv] (beta_dtype)
- *   state_in  fp32 pool, rows selected by state_in_idx (may be NULL: zero state)
- *   state_out fp32 pool, rows selected by state_out_idx (may be NULL: not
- *             written).  state_out == state_in updates the pool in place.
+ *   state_in  fp32 pool of state_in_rows rows, rows selected by state_in_idx
+ *             (may be NULL: zero state)
+ *   state_out fp32 pool of state_out_rows rows, rows selected by
+ *             state_out_idx (may be NULL: not written).  state_out ==
+ *             state_in updates the pool in place.
+ *   (every *_idx: int64 [n_seqs] on the device, or NULL for row n; an id
+ *    outside [0, rows) -- negative ones included -- selects no row: zero
+ *    state in, nothing written.  Without ids, rows must be >= n_seqs.)
  *   o         [tokens, Hv, V] (o_dtype, contiguous)
  *   snapshots fp32 [n_seqs, T, Hv, K, V] or NULL; snapshot t = state after
  *             token t (requires cu_seqlens == NULL)
@@ -90,8 +95,8 @@ const char *gdn_last_error_string(void);
 int gdn_recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
                       int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
                       const float *g, const void *beta, int beta_dtype,
-                      const float *state_in, const int64_t *state_in_idx,
-                      float *state_out, const int64_t *state_out_idx,
+                      const float *state_in, const int64_t *state_in_idx, int64_t state_in_rows,
+                      float *state_out, const int64_t *state_out_idx, int64_t state_out_rows,
                       void *o, int o_dtype, float *snapshots,
                       const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
                       int32_t Hk, int32_t Hv, int32_t K, int32_t V,
@@ -112,8 +117,8 @@ int gdn_recurrent_fwd_gated(const void *q, const void *k, const void *v, int qkv
                             int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
                             const void *a, const void *b, int ab_dtype, int64_t ab_stride_t,
                             const float *A_log, const float *dt_bias,
-                            const float *state_in, const int64_t *state_in_idx,
-                            float *state_out, const int64_t *state_out_idx,
+                            const float *state_in, const int64_t *state_in_idx, int64_t state_in_rows,
+                            float *state_out, const int64_t *state_out_idx, int64_t state_out_rows,
                             void *o, int o_dtype, float *snapshots,
                             const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
                             int32_t Hk, int32_t Hv, int32_t K, int32_t V,
@@ -129,8 +134,9 @@ int gdn_recurrent_fwd_gated(const void *q, const void *k, const void *v, int qkv
  *
  *   q, k, v, g, beta as for gdn_recurrent_fwd; tokens = n_seqs*T, or
  *   cu_seqlens[n_seqs] when cu_seqlens (int32, device) is given.
- *   h0  fp32 initial states (rows by h0_idx) or NULL for zero
- *   hT  fp32 final states (rows by hT_idx) or NULL; hT may equal h0.
+ *   h0  fp32 initial states (h0_rows rows, selected by h0_idx) or NULL for zero
+ *   hT  fp32 final states (hT_rows rows, selected by hT_idx) or NULL; hT may
+ *       equal h0.  Ids as for gdn_recurrent_fwd.
  *   o   [tokens, Hv, V] o_dtype, contiguous
  *   workspace  device scratch of at least gdn_chunk_workspace_bytes(...)
  * Requires K == V == 128 and q/k/v in bf16.
@@ -138,8 +144,8 @@ int gdn_recurrent_fwd_gated(const void *q, const void *k, const void *v, int qkv
 int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
                   int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
                   const float *g, const void *beta, int beta_dtype,
-                  const float *h0, const int64_t *h0_idx,
-                  float *hT, const int64_t *hT_idx,
+                  const float *h0, const int64_t *h0_idx, int64_t h0_rows,
+                  float *hT, const int64_t *hT_idx, int64_t hT_rows,
                   void *o, int o_dtype,
                   const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
                   int32_t Hk, int32_t Hv, int32_t K, int32_t V,
@@ -155,8 +161,8 @@ int gdn_chunk_fwd_gated(const void *q, const void *k, const void *v, int qkv_dty
                         int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
                         const void *a, const void *b, int ab_dtype, int64_t ab_stride_t,
                         const float *A_log, const float *dt_bias,
-                        const float *h0, const int64_t *h0_idx,
-                        float *hT, const int64_t *hT_idx,
+                        const float *h0, const int64_t *h0_idx, int64_t h0_rows,
+                        float *hT, const int64_t *hT_idx, int64_t hT_rows,
                         void *o, int o_dtype,
                         const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
                         int32_t Hk, int32_t Hv, int32_t K, int32_t V,
@@ -196,17 +202,18 @@ int gdn_rmsnorm_gated_fwd(const void *x, int x_dtype, int64_t x_stride_t,
  *   x      [tokens, C] (dtype, token stride x_stride_t, channels contiguous)
  *   w      [C, width] (dtype);  bias [C] (dtype) or NULL
  *   y      [tokens, C] (dtype, token stride y_stride_t)
- *   state_in  [*, C, state_len] (dtype) history rows by state_in_idx, or NULL
- *             for zero history
- *   state_out [*, C, state_len] (dtype) rows by state_out_idx, or NULL: the
- *             last state_len inputs of cat(history, x) per sequence
+ *   state_in  [state_in_rows, C, state_len] (dtype) history rows by
+ *             state_in_idx, or NULL for zero history
+ *   state_out [state_out_rows, C, state_len] (dtype) rows by state_out_idx,
+ *             or NULL: the last state_len inputs of cat(history, x) per
+ *             sequence.  Ids as for gdn_recurrent_fwd.
  *   cu_seqlens int32 [n_seqs+1] or NULL for n_seqs x T tokens
  * Requires width <= state_len + 1, state_len <= 8, C % 8 == 0.
  */
 int causal_conv1d_fwd(const void *x, int64_t x_stride_t, const void *w, const void *bias,
                       void *y, int64_t y_stride_t,
-                      const void *state_in, const int64_t *state_in_idx,
-                      void *state_out, const int64_t *state_out_idx,
+                      const void *state_in, const int64_t *state_in_idx, int64_t state_in_rows,
+                      void *state_out, const int64_t *state_out_idx, int64_t state_out_rows,
                       const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
                       int32_t C, int32_t width, int32_t state_len,
                       int silu, int dtype, void *stream);
@@ -221,25 +228,27 @@ int causal_conv1d_fwd(const void *x, int64_t x_stride_t, const void *w, const vo
  * 142-146) addressed by slot index instead of gathered.
  *
  *   x [n_seqs*T, C] (token stride x_stride_t), y likewise (y_stride_t)
- *   conv_state [*, C, state_len], rows by state_idx (NULL: row n); updated
- *   in place.  Negative slot ids: zero window, nothing written.
+ *   conv_state [state_rows, C, state_len], rows by state_idx (NULL: row n);
+ *   updated in place.  Ids outside [0, state_rows): zero window, nothing
+ *   written.
  */
 int causal_conv1d_update(const void *x, int64_t x_stride_t, void *conv_state,
-                         const int64_t *state_idx, const void *w, const void *bias,
+                         const int64_t *state_idx, int64_t state_rows, const void *w, const void *bias,
                          void *y, int64_t y_stride_t, int32_t n_seqs, int32_t T,
                          int32_t C, int32_t width, int32_t state_len,
                          int silu, int dtype, void *stream);
 
 /*
  * Speculative-verify commit: pool[slot_ids[b]] = snapshots[b, accepted_len[b]-1].
- * accepted_len[b] <= 0 or slot_ids[b] < 0 leaves the slot untouched.
+ * accepted_len[b] <= 0 or slot_ids[b] outside [0, pool_rows) leaves the
+ * slot untouched.
  *
  * No reference implementation exists; engine/runtime/spec_decode.py:81-87
  * and :99-103 document the missing GDN rollback this provides.
- *   pool fp32 [*, H, K, V];  snapshots fp32 [n_seqs, T, H, K, V]
+ *   pool fp32 [pool_rows, H, K, V];  snapshots fp32 [n_seqs, T, H, K, V]
  *   slot_ids int64 [n_seqs];  accepted_len int32 [n_seqs]
  */
-int gdn_state_commit(float *pool, const int64_t *slot_ids, const float *snapshots,
+int gdn_state_commit(float *pool, const int64_t *slot_ids, int64_t pool_rows, const float *snapshots,
                      const int32_t *accepted_len, int32_t n_seqs, int32_t T,
                      int32_t H, int32_t K, int32_t V, void *stream);
 
@@ -249,12 +258,12 @@ int gdn_state_commit(float *pool, const int64_t *slot_ids, const float *snapshot
  * where hist[b] is the verify step's conv history: the S-column window
  * before the step followed by the step's L - S inputs, so columns
  * [a, a + S) are the window after the first a tokens.  accepted_len[b] <= 0
- * or slot_ids[b] < 0 leaves the slot untouched.  Rolls back the conv state
+ * or slot_ids[b] outside [0, pool_rows) leaves the slot untouched.  Rolls back the conv state
  * that engine/runtime/spec_decode.py:81-87 leaves without a rollback.
- *   pool [*, C, S] and hist [n_seqs, C, L] of dtype (bf16 or fp32)
+ *   pool [pool_rows, C, S] and hist [n_seqs, C, L] of dtype (bf16 or fp32)
  *   slot_ids int64 [n_seqs];  accepted_len int32 [n_seqs]
  */
-int gdn_conv_state_commit(void *pool, const int64_t *slot_ids, const void *hist,
+int gdn_conv_state_commit(void *pool, const int64_t *slot_ids, int64_t pool_rows, const void *hist,
                           const int32_t *accepted_len, int32_t n_seqs, int32_t C, int32_t S,
                           int32_t L, int32_t dtype, void *stream);
 

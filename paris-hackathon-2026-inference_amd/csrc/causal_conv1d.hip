@@ -69,8 +69,10 @@ struct ConvArgs {
   int64_t ys;
   const void *st_in;
   const int64_t *in_idx;
+  int64_t in_rows;
   void *st_out;
   const int64_t *out_idx;
+  int64_t out_rows;
   const int32_t *cu;
   int n_seqs, T, C, width, silu;
   int64_t total;
@@ -87,7 +89,7 @@ __device__ __forceinline__ float history_at(const ConvArgs &a, int64_t row, int 
 }
 
 __device__ __forceinline__ int64_t in_row_of(const ConvArgs &a, int n) {
-  return a.st_in ? (a.in_idx ? a.in_idx[n] : n) : -1;
+  return a.st_in ? pool_row(a.in_idx, n, a.in_rows) : -1;
 }
 
 template <typename T, int SL>
@@ -200,7 +202,7 @@ __global__ __launch_bounds__(CONV_NT) void conv_final_state_kernel(ConvArgs a) {
   const int c = blockIdx.x * CONV_NT + threadIdx.x;
   const int n = blockIdx.y;
   if (c >= a.C) return;
-  const int64_t row = a.out_idx ? a.out_idx[n] : n;
+  const int64_t row = pool_row(a.out_idx, n, a.out_rows);
   if (row < 0) return;
   int64_t s_beg;
   int len;
@@ -224,6 +226,7 @@ struct UpdArgs {
   int64_t xs;
   void *st;
   const int64_t *idx;
+  int64_t rows;
   const void *w, *bias;
   void *y;
   int64_t ys;
@@ -235,7 +238,7 @@ __global__ __launch_bounds__(CONV_NT) void conv_update_kernel(UpdArgs a) {
   const int c = blockIdx.x * CONV_NT + threadIdx.x;
   const int n = blockIdx.y;
   if (c >= a.C) return;
-  const int64_t row = a.idx ? a.idx[n] : n;
+  const int64_t row = pool_row(a.idx, n, a.rows);
   T *st = row >= 0 ? static_cast<T *>(a.st) + (row * a.C + c) * SL : nullptr;
   float full[SL + 1];  // cached window (oldest first) followed by the new input
 #pragma unroll
@@ -284,8 +287,8 @@ int launch_upd(const UpdArgs &a, hipStream_t s) {
 
 extern "C" int causal_conv1d_fwd(const void *x, int64_t x_stride_t, const void *w, const void *bias,
                                  void *y, int64_t y_stride_t,
-                                 const void *state_in, const int64_t *state_in_idx,
-                                 void *state_out, const int64_t *state_out_idx,
+                                 const void *state_in, const int64_t *state_in_idx, int64_t state_in_rows,
+                                 void *state_out, const int64_t *state_out_idx, int64_t state_out_rows,
                                  const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
                                  int32_t C, int32_t width, int32_t state_len,
                                  int silu, int dtype, void *stream) {
@@ -302,9 +305,13 @@ extern "C" int causal_conv1d_fwd(const void *x, int64_t x_stride_t, const void *
   if (!x || !w || !y) return fail(GDN_ERR_INVALID_ARGUMENT, "causal_conv1d_fwd: null x/w/y");
   if (x_stride_t < C || y_stride_t < C || (x_stride_t % CPT) || (y_stride_t % CPT))
     return fail(GDN_ERR_INVALID_ARGUMENT, "causal_conv1d_fwd: token strides must be >= C and multiples of 8");
+  if (!rows_cover(state_in, state_in_idx, state_in_rows, n_seqs) ||
+      !rows_cover(state_out, state_out_idx, state_out_rows, n_seqs))
+    return fail(GDN_ERR_INVALID_ARGUMENT, "causal_conv1d_fwd: state rows (%lld in, %lld out) do not cover %d sequences",
+                static_cast<long long>(state_in_rows), static_cast<long long>(state_out_rows), n_seqs);
   if (n_seqs == 0) return ok();
-  ConvArgs a{x, x_stride_t, w, bias, y, y_stride_t, state_in, state_in_idx, state_out, state_out_idx,
-             cu_seqlens, n_seqs, T, C, width, silu};
+  ConvArgs a{x, x_stride_t, w, bias, y, y_stride_t, state_in, state_in_idx, state_in_rows, state_out, state_out_idx,
+             state_out_rows, cu_seqlens, n_seqs, T, C, width, silu};
   a.total = cu_seqlens ? static_cast<int64_t>(T) : static_cast<int64_t>(n_seqs) * T;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == GDN_DTYPE_BF16)
@@ -313,7 +320,7 @@ extern "C" int causal_conv1d_fwd(const void *x, int64_t x_stride_t, const void *
 }
 
 extern "C" int causal_conv1d_update(const void *x, int64_t x_stride_t, void *conv_state,
-                                    const int64_t *state_idx, const void *w, const void *bias,
+                                    const int64_t *state_idx, int64_t state_rows, const void *w, const void *bias,
                                     void *y, int64_t y_stride_t, int32_t n_seqs, int32_t T,
                                     int32_t C, int32_t width, int32_t state_len,
                                     int silu, int dtype, void *stream) {
@@ -326,9 +333,12 @@ extern "C" int causal_conv1d_update(const void *x, int64_t x_stride_t, void *con
   if (C <= 0 || n_seqs < 0 || T < 0 || x_stride_t < C || y_stride_t < C)
     return fail(GDN_ERR_INVALID_ARGUMENT, "causal_conv1d_update: bad sizes");
   if (!x || !w || !y || !conv_state) return fail(GDN_ERR_INVALID_ARGUMENT, "causal_conv1d_update: null pointer");
+  if (!rows_cover(conv_state, state_idx, state_rows, n_seqs))
+    return fail(GDN_ERR_INVALID_ARGUMENT, "causal_conv1d_update: %lld state rows do not cover %d sequences",
+                static_cast<long long>(state_rows), n_seqs);
   if (n_seqs == 0) return ok();
   if (n_seqs > 65535) return fail(GDN_ERR_INVALID_ARGUMENT, "causal_conv1d_update: n_seqs > 65535");
-  UpdArgs a{x, x_stride_t, conv_state, state_idx, w, bias, y, y_stride_t, n_seqs, T, C, width, silu};
+  UpdArgs a{x, x_stride_t, conv_state, state_idx, state_rows, w, bias, y, y_stride_t, n_seqs, T, C, width, silu};
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == GDN_DTYPE_BF16)
     return state_len == 4 ? launch_upd<uint16_t, 4>(a, s) : launch_upd<uint16_t, 3>(a, s);

@@ -111,8 +111,10 @@ struct ChunkArgs {
   GateArgs gate;
   const float *h0;
   const int64_t *h0_idx;
+  int64_t h0_rows;
   float *hT;
   const int64_t *hT_idx;
+  int64_t hT_rows;
   void *o;
   int o_dt;
   const int32_t *cu;
@@ -799,8 +801,8 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_kernel(ChunkArgs a
   const int cs = __builtin_amdgcn_readfirstlane(chunk_start_at(a, n));
   const int ce = __builtin_amdgcn_readfirstlane(max(cs, min(chunk_start_at(a, n + 1), a.max_chunks)));
   const int lo = max(cs, a.seg_begin), hi = min(ce, a.seg_end);
-  const int64_t in_row = a.h0 ? uniform64(a.h0_idx ? a.h0_idx[n] : n) : -1;
-  const int64_t out_row = a.hT ? uniform64(a.hT_idx ? a.hT_idx[n] : n) : -1;
+  const int64_t in_row = a.h0 ? uniform64(pool_row(a.h0_idx, n, a.h0_rows)) : -1;
+  const int64_t out_row = a.hT ? uniform64(pool_row(a.hT_idx, n, a.hT_rows)) : -1;
   const int64_t kv = static_cast<int64_t>(DK) * DV;
   const int row0 = 32 * q;  // first state row of a compute wave
   if (cs == ce) {  // empty sequence: the final state is the initial one (handled once)
@@ -991,8 +993,8 @@ namespace {
 
 int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
               int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t, const GateArgs &gate,
-              const float *h0, const int64_t *h0_idx, float *hT, const int64_t *hT_idx,
-              void *o, int o_dtype, const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
+              const float *h0, const int64_t *h0_idx, int64_t h0_rows, float *hT, const int64_t *hT_idx,
+              int64_t hT_rows, void *o, int o_dtype, const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
               int32_t Hk, int32_t Hv, int32_t K, int32_t V, float scale, int l2norm_qk,
               void *workspace, size_t workspace_bytes, void *stream, const char *name) {
   if (K != DK || V != DV) return fail(GDN_ERR_UNSUPPORTED, "%s: K=%d V=%d; only K=V=128 is built", name, K, V);
@@ -1008,6 +1010,9 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
     return fail(GDN_ERR_INVALID_ARGUMENT, "%s: null q/k/v/gate/o", name);
   if (gate.A_log && !gate.dt_bias) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: null dt_bias", name);
   if (gate.stride < Hv) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: gate token stride smaller than Hv", name);
+  if (!rows_cover(h0, h0_idx, h0_rows, n_seqs) || !rows_cover(hT, hT_idx, hT_rows, n_seqs))
+    return fail(GDN_ERR_INVALID_ARGUMENT, "%s: state rows (%lld in, %lld out) do not cover %d sequences", name,
+                static_cast<long long>(h0_rows), static_cast<long long>(hT_rows), n_seqs);
   if (q_stride_t < Hk * K || k_stride_t < Hk * K || v_stride_t < Hv * V || (q_stride_t | k_stride_t | v_stride_t) % 8)
     return fail(GDN_ERR_INVALID_ARGUMENT, "%s: token strides must cover a row and be multiples of 8", name);
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) % 16)
@@ -1025,7 +1030,7 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
   if (scan_blocks > 0x7fffffff) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: grid too large", name);
   char *ws = static_cast<char *>(workspace);
   ChunkArgs a{static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
-              q_stride_t, k_stride_t, v_stride_t, gate, h0, h0_idx, hT, hT_idx, o, o_dtype,
+              q_stride_t, k_stride_t, v_stride_t, gate, h0, h0_idx, h0_rows, hT, hT_idx, hT_rows, o, o_dtype,
               cu_seqlens, n_seqs, T, Hk, Hv, total, scale, l2norm_qk, static_cast<int>(nc), 0, 0,
               reinterpret_cast<int32_t *>(ws + l.chunk_start), nullptr, nullptr, nullptr,
               reinterpret_cast<float *>(ws + l.carry)};
@@ -1098,15 +1103,15 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
 extern "C" int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
                              int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
                              const float *g, const void *beta, int beta_dtype,
-                             const float *h0, const int64_t *h0_idx,
-                             float *hT, const int64_t *hT_idx,
+                             const float *h0, const int64_t *h0_idx, int64_t h0_rows,
+                             float *hT, const int64_t *hT_idx, int64_t hT_rows,
                              void *o, int o_dtype,
                              const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
                              int32_t Hk, int32_t Hv, int32_t K, int32_t V,
                              float scale, int l2norm_qk,
                              void *workspace, size_t workspace_bytes, void *stream) {
   const gdn::GateArgs gate{g, beta, beta_dtype, Hv, nullptr, nullptr};
-  return gdn::chunk_fwd(q, k, v, qkv_dtype, q_stride_t, k_stride_t, v_stride_t, gate, h0, h0_idx, hT, hT_idx, o,
+  return gdn::chunk_fwd(q, k, v, qkv_dtype, q_stride_t, k_stride_t, v_stride_t, gate, h0, h0_idx, h0_rows, hT, hT_idx, hT_rows, o,
                         o_dtype, cu_seqlens, n_seqs, T, Hk, Hv, K, V, scale, l2norm_qk, workspace, workspace_bytes,
                         stream, "gdn_chunk_fwd");
 }
@@ -1115,8 +1120,8 @@ extern "C" int gdn_chunk_fwd_gated(const void *q, const void *k, const void *v, 
                                    int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
                                    const void *a, const void *b, int ab_dtype, int64_t ab_stride_t,
                                    const float *A_log, const float *dt_bias,
-                                   const float *h0, const int64_t *h0_idx,
-                                   float *hT, const int64_t *hT_idx,
+                                   const float *h0, const int64_t *h0_idx, int64_t h0_rows,
+                                   float *hT, const int64_t *hT_idx, int64_t hT_rows,
                                    void *o, int o_dtype,
                                    const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
                                    int32_t Hk, int32_t Hv, int32_t K, int32_t V,
@@ -1124,7 +1129,7 @@ extern "C" int gdn_chunk_fwd_gated(const void *q, const void *k, const void *v, 
                                    void *workspace, size_t workspace_bytes, void *stream) {
   if (!A_log) return gdn::fail(GDN_ERR_INVALID_ARGUMENT, "gdn_chunk_fwd_gated: null A_log");
   const gdn::GateArgs gate{a, b, ab_dtype, ab_stride_t, A_log, dt_bias};
-  return gdn::chunk_fwd(q, k, v, qkv_dtype, q_stride_t, k_stride_t, v_stride_t, gate, h0, h0_idx, hT, hT_idx, o,
+  return gdn::chunk_fwd(q, k, v, qkv_dtype, q_stride_t, k_stride_t, v_stride_t, gate, h0, h0_idx, h0_rows, hT, hT_idx, hT_rows, o,
                         o_dtype, cu_seqlens, n_seqs, T, Hk, Hv, K, V, scale, l2norm_qk, workspace, workspace_bytes,
                         stream, "gdn_chunk_fwd_gated");
 }

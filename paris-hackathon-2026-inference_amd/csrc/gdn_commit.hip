@@ -14,12 +14,12 @@ namespace {
 
 constexpr int COMMIT_NT = 256;
 
-__global__ __launch_bounds__(COMMIT_NT) void commit_kernel(float *pool, const int64_t *slot_ids,
+__global__ __launch_bounds__(COMMIT_NT) void commit_kernel(float *pool, const int64_t *slot_ids, int64_t rows,
                                                            const float *snaps, const int32_t *acc,
                                                            int T, int H, int64_t kv) {
   const int h = blockIdx.x % H;
   const int b = blockIdx.x / H;
-  const int64_t slot = slot_ids[b];
+  const int64_t slot = pool_row(slot_ids, b, rows);
   const int a = acc[b];
   if (slot < 0 || a <= 0) return;
   const int t = a > T ? T - 1 : a - 1;
@@ -30,11 +30,12 @@ __global__ __launch_bounds__(COMMIT_NT) void commit_kernel(float *pool, const in
 }
 
 template <typename T>
-__global__ __launch_bounds__(COMMIT_NT) void conv_commit_kernel(T *pool, const int64_t *slot_ids, const T *hist,
-                                                                const int32_t *acc, int C, int S, int L, int steps) {
+__global__ __launch_bounds__(COMMIT_NT) void conv_commit_kernel(T *pool, const int64_t *slot_ids, int64_t rows,
+                                                                const T *hist, const int32_t *acc, int C, int S, int L,
+                                                                int steps) {
   const int b = blockIdx.y;
   const int c = blockIdx.x * COMMIT_NT + threadIdx.x;
-  const int64_t slot = slot_ids[b];
+  const int64_t slot = pool_row(slot_ids, b, rows);
   const int a = acc[b];
   if (c >= C || slot < 0 || a <= 0) return;
   const int first = a > steps ? steps : a;  // window after `first` tokens: history columns [first, first + S)
@@ -46,7 +47,7 @@ __global__ __launch_bounds__(COMMIT_NT) void conv_commit_kernel(T *pool, const i
 }  // namespace
 }  // namespace gdn
 
-extern "C" int gdn_conv_state_commit(void *pool, const int64_t *slot_ids, const void *hist,
+extern "C" int gdn_conv_state_commit(void *pool, const int64_t *slot_ids, int64_t pool_rows, const void *hist,
                                      const int32_t *accepted_len, int32_t n_seqs, int32_t C, int32_t S,
                                      int32_t L, int32_t dtype, void *stream) {
   using namespace gdn;
@@ -56,20 +57,21 @@ extern "C" int gdn_conv_state_commit(void *pool, const int64_t *slot_ids, const 
   if (dtype != GDN_DTYPE_BF16 && dtype != GDN_DTYPE_F32)
     return fail(GDN_ERR_UNSUPPORTED, "gdn_conv_state_commit: dtype %d (bf16 or fp32)", dtype);
   if (n_seqs == 0) return ok();
-  if (!pool || !slot_ids || !hist || !accepted_len)
-    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_conv_state_commit: null pointer");
+  if (!pool || !slot_ids || !hist || !accepted_len || pool_rows < 0)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_conv_state_commit: null pointer or negative pool_rows");
   const dim3 grid((C + COMMIT_NT - 1) / COMMIT_NT, n_seqs);
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == GDN_DTYPE_BF16)
     hipLaunchKernelGGL(conv_commit_kernel<uint16_t>, grid, dim3(COMMIT_NT), 0, st, static_cast<uint16_t *>(pool),
-                       slot_ids, static_cast<const uint16_t *>(hist), accepted_len, C, S, L, L - S);
+                       slot_ids, static_cast<int64_t>(pool_rows), static_cast<const uint16_t *>(hist), accepted_len,
+                       C, S, L, L - S);
   else
     hipLaunchKernelGGL(conv_commit_kernel<float>, grid, dim3(COMMIT_NT), 0, st, static_cast<float *>(pool), slot_ids,
-                       static_cast<const float *>(hist), accepted_len, C, S, L, L - S);
+                       static_cast<int64_t>(pool_rows), static_cast<const float *>(hist), accepted_len, C, S, L, L - S);
   return check_launch("gdn_conv_state_commit");
 }
 
-extern "C" int gdn_state_commit(float *pool, const int64_t *slot_ids, const float *snapshots,
+extern "C" int gdn_state_commit(float *pool, const int64_t *slot_ids, int64_t pool_rows, const float *snapshots,
                                 const int32_t *accepted_len, int32_t n_seqs, int32_t T,
                                 int32_t H, int32_t K, int32_t V, void *stream) {
   using namespace gdn;
@@ -77,12 +79,13 @@ extern "C" int gdn_state_commit(float *pool, const int64_t *slot_ids, const floa
     return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_state_commit: bad sizes n_seqs=%d T=%d H=%d K=%d V=%d",
                 n_seqs, T, H, K, V);
   if (n_seqs == 0) return ok();
-  if (!pool || !slot_ids || !snapshots || !accepted_len)
-    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_state_commit: null pointer");
+  if (!pool || !slot_ids || !snapshots || !accepted_len || pool_rows < 0)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_state_commit: null pointer or negative pool_rows");
   const int64_t blocks = static_cast<int64_t>(n_seqs) * H;
   if (blocks > 0x7fffffff) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_state_commit: grid too large");
   hipLaunchKernelGGL(commit_kernel, dim3(static_cast<unsigned>(blocks)), dim3(COMMIT_NT), 0,
-                     static_cast<hipStream_t>(stream), pool, slot_ids, snapshots, accepted_len, T, H,
+                     static_cast<hipStream_t>(stream), pool, slot_ids, static_cast<int64_t>(pool_rows), snapshots,
+                     accepted_len, T, H,
                      static_cast<int64_t>(K) * V);
   return check_launch("gdn_state_commit");
 }

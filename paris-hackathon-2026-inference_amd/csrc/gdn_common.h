@@ -22,6 +22,14 @@ int check_launch(const char *what);
 inline bool valid_dtype(int dt) { return dt == GDN_DTYPE_F32 || dt == GDN_DTYPE_BF16 || dt == GDN_DTYPE_F16; }
 inline size_t dtype_size(int dt) { return dt == GDN_DTYPE_F32 ? 4 : 2; }
 
+// A state tensor of `rows` rows (a slot pool, or one row per sequence)
+// addressed per sequence through `idx` (NULL: row n).  Host check: without
+// indices, the rows must cover the sequences; with them, out-of-range ids are
+// handled on the device (pool_row).
+inline bool rows_cover(const void *state, const int64_t *idx, int64_t rows, int32_t n_seqs) {
+  return !state || (rows >= 0 && (idx || rows >= n_seqs));
+}
+
 // ---------------------------------------------------------------- device side
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
@@ -96,6 +104,14 @@ __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
   return x;
+}
+
+// Row of sequence n in a state tensor of `rows` rows addressed through `idx`
+// (NULL: row n).  An id outside [0, rows) means no row, like a negative slot
+// id: zero state in, nothing written.
+__device__ __forceinline__ int64_t pool_row(const int64_t *idx, int64_t n, int64_t rows) {
+  const int64_t r = idx ? idx[n] : n;
+  return (r >= 0 && r < rows) ? r : -1;
 }
 
 // Sequence n's token range [*t0, *t0 + *len), clamped to the [0, total)

@@ -30,8 +30,10 @@ struct RecArgs {
   GateArgs gate;
   const float *state_in;
   const int64_t *in_idx;
+  int64_t in_rows;
   float *state_out;
   const int64_t *out_idx;
+  int64_t out_rows;
   void *o;
   float *snap;
   const int32_t *cu;
@@ -72,8 +74,8 @@ __global__ __launch_bounds__(2 * VT) void recurrent_kernel(RecArgs a) {
   int len;
   seq_range(a.cu, n, a.T, a.total, &t0, &len);
 
-  const int64_t in_row = a.state_in ? (a.in_idx ? a.in_idx[n] : n) : -1;
-  const int64_t out_row = a.state_out ? (a.out_idx ? a.out_idx[n] : n) : -1;
+  const int64_t in_row = a.state_in ? pool_row(a.in_idx, n, a.in_rows) : -1;
+  const int64_t out_row = a.state_out ? pool_row(a.out_idx, n, a.out_rows) : -1;
 
   // The state is touched exactly once per launch: non-temporal loads and
   // stores keep it from displacing reusable lines in the caches.
@@ -200,8 +202,8 @@ namespace {
 
 int recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
                   int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t, const GateArgs &gate,
-                  const float *state_in, const int64_t *state_in_idx,
-                  float *state_out, const int64_t *state_out_idx,
+                  const float *state_in, const int64_t *state_in_idx, int64_t state_in_rows,
+                  float *state_out, const int64_t *state_out_idx, int64_t state_out_rows,
                   void *o, int o_dtype, float *snapshots,
                   const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
                   int32_t Hk, int32_t Hv, int32_t K, int32_t V,
@@ -219,13 +221,17 @@ int recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
   if (gate.stride < Hv) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: gate token stride smaller than Hv", name);
   if (snapshots && cu_seqlens)
     return fail(GDN_ERR_INVALID_ARGUMENT, "%s: snapshots need equal-length sequences", name);
+  if (!rows_cover(state_in, state_in_idx, state_in_rows, n_seqs) ||
+      !rows_cover(state_out, state_out_idx, state_out_rows, n_seqs))
+    return fail(GDN_ERR_INVALID_ARGUMENT, "%s: state rows (%lld in, %lld out) do not cover %d sequences", name,
+                static_cast<long long>(state_in_rows), static_cast<long long>(state_out_rows), n_seqs);
   if (q_stride_t < Hk * K || k_stride_t < Hk * K || v_stride_t < Hv * V)
     return fail(GDN_ERR_INVALID_ARGUMENT, "%s: token stride smaller than a row", name);
   const int64_t n_blocks = static_cast<int64_t>(n_seqs) * Hv * (VD / 32);
   if (n_blocks > 0x7fffffff) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: grid too large", name);
 
-  RecArgs a{q, k, v, q_stride_t, k_stride_t, v_stride_t, gate, state_in, state_in_idx,
-            state_out, state_out_idx, o, snapshots, cu_seqlens, n_seqs, T, Hk, Hv,
+  RecArgs a{q, k, v, q_stride_t, k_stride_t, v_stride_t, gate, state_in, state_in_idx, state_in_rows,
+            state_out, state_out_idx, state_out_rows, o, snapshots, cu_seqlens, n_seqs, T, Hk, Hv,
             cu_seqlens ? static_cast<int64_t>(T) : static_cast<int64_t>(n_seqs) * T,
             scale, l2norm_qk, qkv_dtype, o_dtype};
   hipLaunchKernelGGL(recurrent_kernel<32>, dim3(static_cast<unsigned>(n_blocks)), dim3(64), 0,
@@ -239,15 +245,15 @@ int recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
 extern "C" int gdn_recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
                                  int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
                                  const float *g, const void *beta, int beta_dtype,
-                                 const float *state_in, const int64_t *state_in_idx,
-                                 float *state_out, const int64_t *state_out_idx,
+                                 const float *state_in, const int64_t *state_in_idx, int64_t state_in_rows,
+                                 float *state_out, const int64_t *state_out_idx, int64_t state_out_rows,
                                  void *o, int o_dtype, float *snapshots,
                                  const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
                                  int32_t Hk, int32_t Hv, int32_t K, int32_t V,
                                  float scale, int l2norm_qk, void *stream) {
   const gdn::GateArgs gate{g, beta, beta_dtype, Hv, nullptr, nullptr};
   return gdn::recurrent_fwd(q, k, v, qkv_dtype, q_stride_t, k_stride_t, v_stride_t, gate, state_in, state_in_idx,
-                            state_out, state_out_idx, o, o_dtype, snapshots, cu_seqlens, n_seqs, T, Hk, Hv, K, V,
+                            state_in_rows, state_out, state_out_idx, state_out_rows, o, o_dtype, snapshots, cu_seqlens, n_seqs, T, Hk, Hv, K, V,
                             scale, l2norm_qk, stream, "gdn_recurrent_fwd");
 }
 
@@ -255,8 +261,8 @@ extern "C" int gdn_recurrent_fwd_gated(const void *q, const void *k, const void 
                                        int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
                                        const void *a, const void *b, int ab_dtype, int64_t ab_stride_t,
                                        const float *A_log, const float *dt_bias,
-                                       const float *state_in, const int64_t *state_in_idx,
-                                       float *state_out, const int64_t *state_out_idx,
+                                       const float *state_in, const int64_t *state_in_idx, int64_t state_in_rows,
+                                       float *state_out, const int64_t *state_out_idx, int64_t state_out_rows,
                                        void *o, int o_dtype, float *snapshots,
                                        const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
                                        int32_t Hk, int32_t Hv, int32_t K, int32_t V,
@@ -264,6 +270,6 @@ extern "C" int gdn_recurrent_fwd_gated(const void *q, const void *k, const void 
   if (!A_log) return gdn::fail(GDN_ERR_INVALID_ARGUMENT, "gdn_recurrent_fwd_gated: null A_log");
   const gdn::GateArgs gate{a, b, ab_dtype, ab_stride_t, A_log, dt_bias};
   return gdn::recurrent_fwd(q, k, v, qkv_dtype, q_stride_t, k_stride_t, v_stride_t, gate, state_in, state_in_idx,
-                            state_out, state_out_idx, o, o_dtype, snapshots, cu_seqlens, n_seqs, T, Hk, Hv, K, V,
+                            state_in_rows, state_out, state_out_idx, state_out_rows, o, o_dtype, snapshots, cu_seqlens, n_seqs, T, Hk, Hv, K, V,
                             scale, l2norm_qk, stream, "gdn_recurrent_fwd_gated");
 }

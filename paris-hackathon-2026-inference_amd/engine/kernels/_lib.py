@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libgdn_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 GDN_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
@@ -35,8 +35,8 @@ SIGNATURES = {
         _c_void_p, _c_void_p, _c_void_p, _int,      # q k v qkv_dtype
         _i64, _i64, _i64,                           # token strides
         _c_void_p, _c_void_p, _int,                 # g beta beta_dtype
-        _c_void_p, _c_void_p,                       # state_in, state_in_idx
-        _c_void_p, _c_void_p,                       # state_out, state_out_idx
+        _c_void_p, _c_void_p, _i64,                 # state_in, state_in_idx, rows
+        _c_void_p, _c_void_p, _i64,                 # state_out, state_out_idx, rows
         _c_void_p, _int, _c_void_p,                 # o, o_dtype, snapshots
         _c_void_p, _i32, _i32,                      # cu_seqlens n_seqs T
         _i32, _i32, _i32, _i32,                     # Hk Hv K V
@@ -45,8 +45,8 @@ SIGNATURES = {
         _c_void_p, _c_void_p, _c_void_p, _int,
         _i64, _i64, _i64,
         _c_void_p, _c_void_p, _int,
-        _c_void_p, _c_void_p,                       # h0, h0_idx
-        _c_void_p, _c_void_p,                       # hT, hT_idx
+        _c_void_p, _c_void_p, _i64,                 # h0, h0_idx, rows
+        _c_void_p, _c_void_p, _i64,                 # hT, hT_idx, rows
         _c_void_p, _int,                            # o, o_dtype
         _c_void_p, _i32, _i32,
         _i32, _i32, _i32, _i32,
@@ -58,8 +58,8 @@ SIGNATURES = {
         _i64, _i64, _i64,                           # token strides
         _c_void_p, _c_void_p, _int, _i64,           # a b ab_dtype ab_stride
         _c_void_p, _c_void_p,                       # A_log dt_bias
-        _c_void_p, _c_void_p,                       # state_in, state_in_idx
-        _c_void_p, _c_void_p,                       # state_out, state_out_idx
+        _c_void_p, _c_void_p, _i64,                 # state_in, state_in_idx, rows
+        _c_void_p, _c_void_p, _i64,                 # state_out, state_out_idx, rows
         _c_void_p, _int, _c_void_p,                 # o, o_dtype, snapshots
         _c_void_p, _i32, _i32,                      # cu_seqlens n_seqs T
         _i32, _i32, _i32, _i32,                     # Hk Hv K V
@@ -69,8 +69,8 @@ SIGNATURES = {
         _i64, _i64, _i64,
         _c_void_p, _c_void_p, _int, _i64,           # a b ab_dtype ab_stride
         _c_void_p, _c_void_p,                       # A_log dt_bias
-        _c_void_p, _c_void_p,                       # h0, h0_idx
-        _c_void_p, _c_void_p,                       # hT, hT_idx
+        _c_void_p, _c_void_p, _i64,                 # h0, h0_idx, rows
+        _c_void_p, _c_void_p, _i64,                 # hT, hT_idx, rows
         _c_void_p, _int,                            # o, o_dtype
         _c_void_p, _i32, _i32,
         _i32, _i32, _i32, _i32,
@@ -85,20 +85,22 @@ SIGNATURES = {
     "causal_conv1d_fwd": (_int, [
         _c_void_p, _i64, _c_void_p, _c_void_p,      # x x_stride w bias
         _c_void_p, _i64,                            # y y_stride
-        _c_void_p, _c_void_p, _c_void_p, _c_void_p, # state_in idx state_out idx
+        _c_void_p, _c_void_p, _i64,                 # state_in idx rows
+        _c_void_p, _c_void_p, _i64,                 # state_out idx rows
         _c_void_p, _i32, _i32,                      # cu n_seqs T
         _i32, _i32, _i32,                           # C width state_len
         _int, _int, _c_void_p]),                    # silu dtype stream
     "causal_conv1d_update": (_int, [
         _c_void_p, _i64, _c_void_p, _c_void_p,      # x x_stride conv_state idx
+        _i64,                                       # conv_state rows
         _c_void_p, _c_void_p, _c_void_p, _i64,      # w bias y y_stride
         _i32, _i32, _i32, _i32, _i32,               # n_seqs T C width state_len
         _int, _int, _c_void_p]),
     "gdn_state_commit": (_int, [
-        _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+        _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p,  # pool slot_ids pool_rows snapshots accepted_len
         _i32, _i32, _i32, _i32, _i32, _c_void_p]),
     "gdn_conv_state_commit": (_int, [
-        _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # pool slot_ids hist accepted_len
+        _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p,  # pool slot_ids pool_rows hist accepted_len
         _i32, _i32, _i32, _i32, _int, _c_void_p]),   # n_seqs C S L dtype stream
 }
 
@@ -193,6 +195,11 @@ def per_token(x: torch.Tensor, b: int, t: int, h: int, what: str) -> tuple[torch
         x = x.contiguous()
         st = h
     return x, st
+
+
+def rows_of(t: Optional[torch.Tensor]) -> int:
+    """Row count of a state tensor as the C ABI takes it (0 when absent)."""
+    return 0 if t is None else int(t.shape[0])
 
 
 def as_index(idx: Optional[torch.Tensor], device: torch.device) -> Optional[torch.Tensor]:

@@ -127,7 +127,8 @@ def causal_conv1d_fn(
     lib = _lib.load()
     st = lib.causal_conv1d_fwd(
         _lib.ptr(xt), xs, _lib.ptr(w), _lib.ptr(bb), _lib.ptr(y), c,
-        _lib.ptr(state_in), _lib.ptr(in_idx), _lib.ptr(state_out), _lib.ptr(out_idx),
+        _lib.ptr(state_in), _lib.ptr(in_idx), _lib.rows_of(state_in),
+        _lib.ptr(state_out), _lib.ptr(out_idx), _lib.rows_of(state_out),
         _lib.ptr(cu), n_seqs, b * t if cu is not None else t,
         c, w.shape[1], s_len, _act(activation), _lib.GDN_DTYPE[dt], _lib.stream_of(y))
     _lib.check(st, "causal_conv1d_fwd")
@@ -172,7 +173,7 @@ def causal_conv1d_update(
     y = torch.empty((b, t, c), dtype=dt, device=dev)
     lib = _lib.load()
     st = lib.causal_conv1d_update(
-        _lib.ptr(xt), xs, _lib.ptr(conv_state), _lib.ptr(idx), _lib.ptr(w), _lib.ptr(bb),
+        _lib.ptr(xt), xs, _lib.ptr(conv_state), _lib.ptr(idx), _lib.rows_of(conv_state), _lib.ptr(w), _lib.ptr(bb),
         _lib.ptr(y), c, b, t, c, w.shape[1], conv_state.shape[2], _act(activation),
         _lib.GDN_DTYPE[dt], _lib.stream_of(y))
     _lib.check(st, "causal_conv1d_update")

@@ -191,7 +191,7 @@ def _chunk(query, key, value, gates, chunk_size, initial_state, output_final_sta
     st = getattr(lib, name)(
         _lib.ptr(qx), _lib.ptr(kx), _lib.ptr(vx), _lib.dtype_code(query, "query"), qs, ks, vs,
         *gate_args,
-        _lib.ptr(h0), _lib.ptr(h0_idx), _lib.ptr(hT), _lib.ptr(hT_idx),
+        _lib.ptr(h0), _lib.ptr(h0_idx), _lib.rows_of(h0), _lib.ptr(hT), _lib.ptr(hT_idx), _lib.rows_of(hT),
         _lib.ptr(o), _lib.dtype_code(o, "o"),
         _lib.ptr(cu), n_seqs, total if cu is not None else t,
         hk, hv, dk, dv, float(scale), int(bool(use_qk_l2norm_in_kernel)),

@@ -176,7 +176,8 @@ def _recurrent(q, k, v, gates, scale, initial_state, output_final_state, cu_seql
     st = getattr(lib, name)(
         _lib.ptr(qx), _lib.ptr(kx), _lib.ptr(vx), _lib.dtype_code(q, "q"), qs, ks, vs,
         *gate_args,
-        _lib.ptr(state_in), _lib.ptr(in_idx), _lib.ptr(state_out), _lib.ptr(out_idx),
+        _lib.ptr(state_in), _lib.ptr(in_idx), _lib.rows_of(state_in),
+        _lib.ptr(state_out), _lib.ptr(out_idx), _lib.rows_of(state_out),
         _lib.ptr(o), _lib.dtype_code(o, "o"), _lib.ptr(snapshots),
         _lib.ptr(cu), n_seqs, total if cu is not None else t,
         hk, hv, dk, dv, float(scale), int(bool(use_qk_l2norm_in_kernel)), _lib.stream_of(q))

@@ -21,7 +21,7 @@ def gdn_state_commit(pool: torch.Tensor, slot_ids: torch.Tensor, snapshots: torc
                      accepted_len: torch.Tensor) -> torch.Tensor:
     """``pool[slot_ids[b]] = snapshots[b, accepted_len[b] - 1]`` on the GPU, in place.
 
-    ``accepted_len[b] <= 0`` or a negative slot leaves that slot untouched;
+    ``accepted_len[b] <= 0`` or a slot outside the pool leaves that slot untouched;
     values above T are clamped to T.  There is no reference implementation:
     engine/runtime/spec_decode.py:81-87 and :99-103 document the missing
     GDN rollback ("requires saving state snapshots").
@@ -38,7 +38,7 @@ def gdn_state_commit(pool: torch.Tensor, slot_ids: torch.Tensor, snapshots: torc
     acc = accepted_len.to(device=dev, dtype=torch.int32).contiguous()
     if idx.numel() != n or acc.numel() != n:
         raise ValueError("slot_ids and accepted_len need one entry per sequence")
-    st = _lib.load().gdn_state_commit(_lib.ptr(pool), _lib.ptr(idx), _lib.ptr(snapshots), _lib.ptr(acc),
+    st = _lib.load().gdn_state_commit(_lib.ptr(pool), _lib.ptr(idx), _lib.rows_of(pool), _lib.ptr(snapshots), _lib.ptr(acc),
                                       n, t, h, k, v, _lib.stream_of(pool))
     _lib.check(st, "gdn_state_commit")
     return pool
@@ -69,7 +69,7 @@ def gdn_conv_state_commit(pool: torch.Tensor, slot_ids: torch.Tensor, hist: torc
     acc = accepted_len.to(device=dev, dtype=torch.int32).contiguous()
     if idx.numel() != n or acc.numel() != n:
         raise ValueError("slot_ids and accepted_len need one entry per sequence")
-    st = _lib.load().gdn_conv_state_commit(_lib.ptr(pool), _lib.ptr(idx), _lib.ptr(hist), _lib.ptr(acc),
+    st = _lib.load().gdn_conv_state_commit(_lib.ptr(pool), _lib.ptr(idx), _lib.rows_of(pool), _lib.ptr(hist), _lib.ptr(acc),
                                            n, c, s, length, _lib.GDN_DTYPE[pool.dtype], _lib.stream_of(pool))
     _lib.check(st, "gdn_conv_state_commit")
     return pool

@@ -41,13 +41,13 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.gdn_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.gdn_abi_version() == _lib.ABI_VERSION == 4
 
 
 def _rec_call(lib, **over):
     args = dict(q=1, k=1, v=1, qkv_dtype=1, qs=4096, ks=4096, vs=4096, g=1, beta=1, beta_dtype=0,
-                sin=None, sin_idx=None, sout=None, sout_idx=None, o=1, o_dtype=1, snap=None, cu=None,
-                n=2, t=1, hk=32, hv=32, kd=128, vd=128, scale=0.1, l2=1, stream=None)
+                sin=None, sin_idx=None, sin_rows=0, sout=None, sout_idx=None, sout_rows=0, o=1, o_dtype=1,
+                snap=None, cu=None, n=2, t=1, hk=32, hv=32, kd=128, vd=128, scale=0.1, l2=1, stream=None)
     args.update(over)
     return lib.gdn_recurrent_fwd(*args.values())
 
@@ -66,10 +66,20 @@ def test_recurrent_rejects_bad_gqa_and_nulls(lib):
     assert lib.gdn_last_error_string().decode() == ""
 
 
+def test_state_rows_must_cover_the_sequences_without_ids(lib):
+    # one state row per sequence unless ids select rows; ids outside the rows
+    # are handled on the device (no row), so any row count is accepted with ids
+    assert _rec_call(lib, sin=256, sin_rows=1) == 1          # 2 sequences, 1 row, no ids
+    assert "do not cover" in lib.gdn_last_error_string().decode()
+    assert _rec_call(lib, sout=256, sout_rows=-1, sout_idx=256) == 1  # negative row count
+    assert _rec_call(lib, sin=256, sin_rows=2, n=0) == 0
+    assert lib.causal_conv1d_update(16, 64, 256, None, 1, 1, None, 16, 64, 2, 1, 64, 4, 4, 1, 1, None) == 1
+
+
 def test_conv_rejects_bad_shapes(lib):
     def call(**over):
-        args = dict(x=16, xs=64, w=1, b=None, y=16, ys=64, si=None, sii=None, so=None, soi=None, cu=None,
-                    n=1, t=4, c=64, width=4, sl=4, silu=1, dt=1, stream=None)
+        args = dict(x=16, xs=64, w=1, b=None, y=16, ys=64, si=None, sii=None, sir=0, so=None, soi=None, sor=0,
+                    cu=None, n=1, t=4, c=64, width=4, sl=4, silu=1, dt=1, stream=None)
         args.update(over)
         return lib.causal_conv1d_fwd(*args.values())
     assert call(c=12, xs=12, ys=12) == 1          # C % 8
@@ -77,15 +87,17 @@ def test_conv_rejects_bad_shapes(lib):
     assert call(sl=5) == 2
     assert call(x=8) == 1                          # misaligned
     assert call(dt=2) == 2                         # fp16 not built
+    assert call(so=256, sor=0) == 1                # final-state rows do not cover the sequence
 
 
 def test_commit_rejects_bad_sizes(lib):
-    assert lib.gdn_state_commit(1, 1, 1, 1, 2, 0, 32, 128, 128, None) == 1
-    assert lib.gdn_state_commit(None, 1, 1, 1, 2, 4, 32, 128, 128, None) == 1
-    assert lib.gdn_conv_state_commit(1, 1, 1, 1, 2, 8192, 4, 4, 1, None) == 1   # L must exceed S
-    assert lib.gdn_conv_state_commit(None, 1, 1, 1, 2, 8192, 4, 8, 1, None) == 1
-    assert lib.gdn_conv_state_commit(1, 1, 1, 1, 2, 8192, 4, 8, 3, None) == 2   # dtype
-    assert lib.gdn_conv_state_commit(None, None, None, None, 0, 8192, 4, 8, 1, None) == 0  # nothing to do
+    assert lib.gdn_state_commit(1, 1, 4, 1, 1, 2, 0, 32, 128, 128, None) == 1
+    assert lib.gdn_state_commit(None, 1, 4, 1, 1, 2, 4, 32, 128, 128, None) == 1
+    assert lib.gdn_state_commit(1, 1, -1, 1, 1, 2, 4, 32, 128, 128, None) == 1  # negative pool_rows
+    assert lib.gdn_conv_state_commit(1, 1, 4, 1, 1, 2, 8192, 4, 4, 1, None) == 1   # L must exceed S
+    assert lib.gdn_conv_state_commit(None, 1, 4, 1, 1, 2, 8192, 4, 8, 1, None) == 1
+    assert lib.gdn_conv_state_commit(1, 1, 4, 1, 1, 2, 8192, 4, 8, 3, None) == 2   # dtype
+    assert lib.gdn_conv_state_commit(None, None, 0, None, None, 0, 8192, 4, 8, 1, None) == 0  # nothing to do
 
 
 def test_chunk_workspace_is_host_arithmetic(lib):
@@ -123,8 +135,9 @@ def test_product_path_never_imports_the_oracle():
 
 def _rec_gated_call(lib, **over):
     args = dict(q=1, k=1, v=1, qkv_dtype=1, qs=4096, ks=4096, vs=4096, a=1, b=1, ab_dtype=1, ab_stride=32,
-                A_log=1, dt_bias=1, sin=None, sin_idx=None, sout=None, sout_idx=None, o=1, o_dtype=1,
-                snap=None, cu=None, n=2, t=1, hk=32, hv=32, kd=128, vd=128, scale=0.1, l2=1, stream=None)
+                A_log=1, dt_bias=1, sin=None, sin_idx=None, sin_rows=0, sout=None, sout_idx=None, sout_rows=0,
+                o=1, o_dtype=1, snap=None, cu=None, n=2, t=1, hk=32, hv=32, kd=128, vd=128, scale=0.1, l2=1,
+                stream=None)
     args.update(over)
     return lib.gdn_recurrent_fwd_gated(*args.values())
 
@@ -138,7 +151,8 @@ def test_gated_entry_points_check_their_gate_arguments(lib):
     assert _rec_gated_call(lib, kd=64, vd=64) == 2
     # chunk variant: same gate checks ahead of its own (A_log, then workspace)
     chunk = dict(q=256, k=256, v=256, qkv_dtype=1, qs=4096, ks=4096, vs=4096, a=1, b=1, ab_dtype=1, ab_stride=32,
-                 A_log=None, dt_bias=1, h0=None, h0_idx=None, hT=None, hT_idx=None, o=1, o_dtype=1,
+                 A_log=None, dt_bias=1, h0=None, h0_idx=None, h0_rows=0, hT=None, hT_idx=None, hT_rows=0,
+                 o=1, o_dtype=1,
                  cu=None, n=1, t=64, hk=16, hv=32, kd=128, vd=128, scale=0.1, l2=1,
                  ws=None, ws_bytes=0, stream=None)
     assert lib.gdn_chunk_fwd_gated(*chunk.values()) == 1

@@ -92,6 +92,49 @@ def test_negative_slot_means_fresh_state_and_no_write():
     assert torch.equal(pool[keep].cpu(), c["pool"][keep])
 
 
+def test_out_of_range_slot_is_no_slot_in_every_pool_kernel():
+    # An id past the pool (or negative) selects no row: zero state in, nothing
+    # written -- in the recurrence, the conv update, the chunk kernel and the
+    # commits -- so a bad id can never address memory outside a pool.
+    from engine.kernels import causal_conv1d_update, chunk_gated_delta_rule, gdn_conv_state_commit, gdn_state_commit
+    c = configs.config1(batch=4, num_slots=8)
+    q, k, v, g, beta = cuda(*(c[x] for x in ("q", "k", "v", "g", "beta")))
+    bad = torch.tensor([5, 8, 0, 1 << 40], device=DEV)   # rows 1 and 3 outside the 8-slot pool
+    ref = torch.tensor([5, -1, 0, -1], device=DEV)
+    gen = torch.Generator().manual_seed(5)
+    cpool0 = torch.randn(8, 64, 4, generator=gen).to(DEV, torch.bfloat16)
+    x = torch.randn(4, 64, 1, generator=gen).to(DEV, torch.bfloat16)
+    w = torch.randn(64, 4, generator=gen).to(DEV, torch.bfloat16)
+    outs = []
+    for ids in (bad, ref):
+        pool = c["pool"].to(DEV)
+        o, _ = fused_recurrent_gated_delta_rule(q, k, v, g, beta, initial_state=pool, ssm_state_indices=ids,
+                                                inplace_final_state=True, use_qk_l2norm_in_kernel=True)
+        cpool = cpool0.clone()
+        y = causal_conv1d_update(x, cpool, w, None, "silu", conv_state_indices=ids)
+        outs.append((o, pool, y, cpool))
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a, b)
+    assert torch.equal(outs[0][3][[1, 2, 3, 4, 6, 7]], cpool0[[1, 2, 3, 4, 6, 7]])
+    t = 70  # the chunk kernel, initial and final states by id
+    qc, kc = (torch.randn(4, t, 16, 128, device=DEV).to(torch.bfloat16) for _ in range(2))
+    vc = torch.randn(4, t, 32, 128, device=DEV).to(torch.bfloat16)
+    gc, bc = -0.1 * torch.rand(4, t, 32, device=DEV), torch.rand(4, t, 32, device=DEV)
+    snaps = torch.randn(4, 2, 32, 128, 128, device=DEV)
+    hist = torch.randn(4, 64, 6, generator=torch.Generator().manual_seed(6)).to(DEV, torch.bfloat16)
+    res = []
+    for ids in (bad, ref):
+        pool = c["pool"].to(DEV)
+        o, _ = chunk_gated_delta_rule(qc, kc, vc, gc, bc, initial_state=pool, ssm_state_indices=ids,
+                                      inplace_final_state=True, use_qk_l2norm_in_kernel=True)
+        gdn_state_commit(pool, ids, snaps, torch.tensor([1, 2, 2, 1]))
+        cp = torch.zeros(8, 64, 4, device=DEV, dtype=torch.bfloat16)
+        gdn_conv_state_commit(cp, ids, hist, torch.tensor([1, 2, 2, 1]))
+        res.append((o, pool, cp))
+    for a, b in zip(res[0], res[1]):
+        assert torch.equal(a, b)
+
+
 def test_fla_mode_returns_new_state_and_keeps_input():
     c = configs.config4(batch=3, t=3, num_slots=3)
     h0 = c["pool"].to(DEV)
