@@ -527,7 +527,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
 }
 
 // ------------------------------------------------------------------ phase B
-constexpr int BUF_DWORD3 = 0x00020000;  // raw (untyped) buffer resource word 3 on CDNA
 
 // sched_group_barrier masks
 constexpr int SG_VALU = 0x2, SG_MFMA = 0x8, SG_VMEM_RD = 0x20, SG_VMEM_WR = 0x40, SG_DS_RD = 0x100;

@@ -32,6 +32,9 @@ inline bool rows_cover(const void *state, const int64_t *idx, int64_t rows, int3
 
 // ---------------------------------------------------------------- device side
 
+constexpr int BUF_DWORD3 = 0x00020000;  // raw (untyped) buffer resource word 3 on CDNA
+constexpr int BUF_NT = 2;               // buffer load/store cache policy: non-temporal
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }

@@ -20,6 +20,7 @@ namespace gdn {
 namespace {
 
 typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
 
 constexpr int KD = 128;  // head dim of k (rows of the state)
 constexpr int VD = 128;  // head dim of v (columns of the state)
@@ -44,12 +45,19 @@ struct RecArgs {
   int qkv_dt, o_dt;
 };
 
-template <int VT>
-__global__ __launch_bounds__(2 * VT) void recurrent_kernel(RecArgs a) {
-  constexpr int NT = 2 * VT;
+// Workgroup shape: 32 state columns, 64 threads (one wave, 16 rows per
+// thread, 137 VGPRs, 3 waves per SIMD).  Measured at B=64 on MI355X: 56.0 us;
+// 128 threads (8 rows per thread, 4 waves per SIMD) 58.5 us; 256 threads
+// 62.7 us -- more waves per workgroup cost a cross-wave reduction per token.
+constexpr int REC_VT = 32;
+constexpr int REC_NT = 64;
+
+template <int VT, int NT>
+__global__ __launch_bounds__(NT) void recurrent_kernel(RecArgs a) {
   constexpr int NW = NT / 64;
-  constexpr int TPR = VT / 4;   // threads per state row
-  constexpr int RPT = 16;       // rows per thread (8 row groups)
+  constexpr int TPR = VT / 4;     // threads per state row
+  constexpr int NRG = NT / TPR;   // row groups
+  constexpr int RPT = KD / NRG;   // rows per thread
   constexpr int NSPLIT = VD / VT;
 
   __shared__ float qs_l[KD];
@@ -78,13 +86,22 @@ __global__ __launch_bounds__(2 * VT) void recurrent_kernel(RecArgs a) {
   const int64_t out_row = a.state_out ? pool_row(a.out_idx, n, a.out_rows) : -1;
 
   // The state is touched exactly once per launch: non-temporal loads and
-  // stores keep it from displacing reusable lines in the caches.
+  // stores keep it from displacing reusable lines in the caches.  One
+  // (sequence, head) state is one 64 KiB buffer range; a thread's rows
+  // rg + 8r sit 4 KiB apart, an offset carried in a scalar register, so the
+  // 16 accesses share one vector offset.
+  const int voff = (rg * VD + col0) * 4;
+  constexpr int ROW8 = NRG * VD * 4;  // bytes between a thread's rows
+  auto state_rsrc = [&](const float *pool, int64_t row) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(pool) + (row * a.Hv + h) * (int64_t)(KD * VD), 0,
+                                             KD * VD * 4, BUF_DWORD3);
+  };
   f32x4 s[RPT];
   if (in_row >= 0) {
-    const float *base = a.state_in + (in_row * a.Hv + h) * (int64_t)(KD * VD) + col0;
+    const auto rs = state_rsrc(a.state_in, in_row);
 #pragma unroll
     for (int r = 0; r < RPT; ++r)
-      s[r] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(base + (rg + 8 * r) * VD));
+      s[r] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, r * ROW8, BUF_NT));
   } else {
 #pragma unroll
     for (int r = 0; r < RPT; ++r) s[r] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -123,7 +140,7 @@ __global__ __launch_bounds__(2 * VT) void recurrent_kernel(RecArgs a) {
     float pk[4] = {0.f, 0.f, 0.f, 0.f}, pq[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int r = 0; r < RPT; ++r) {
-      const float kk = ks_l[rg + 8 * r], qq = qs_l[rg + 8 * r];
+      const float kk = ks_l[rg + NRG * r], qq = qs_l[rg + NRG * r];
       pk[0] += kk * s[r].x; pk[1] += kk * s[r].y; pk[2] += kk * s[r].z; pk[3] += kk * s[r].w;
       pq[0] += qq * s[r].x; pq[1] += qq * s[r].y; pq[2] += qq * s[r].z; pq[3] += qq * s[r].w;
     }
@@ -166,7 +183,7 @@ __global__ __launch_bounds__(2 * VT) void recurrent_kernel(RecArgs a) {
     }
 #pragma unroll
     for (int r = 0; r < RPT; ++r) {
-      const float kk = ks_l[rg + 8 * r];
+      const float kk = ks_l[rg + NRG * r];
       s[r].x = eg * s[r].x + kk * d[0];
       s[r].y = eg * s[r].y + kk * d[1];
       s[r].z = eg * s[r].z + kk * d[2];
@@ -177,20 +194,23 @@ __global__ __launch_bounds__(2 * VT) void recurrent_kernel(RecArgs a) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) store_elem(a.o, ooff + c, a.o_dt, out[c]);
     }
+    // Snapshots take plain global stores: stores through a buffer range
+    // rebuilt per token in this loop were compiled with a per-token term in
+    // the vector offset and landed outside the range (dropped).
     if (a.snap) {
       float *sb = a.snap + (((int64_t)n * a.T + t) * a.Hv + h) * (int64_t)(KD * VD) + col0;
 #pragma unroll
       for (int r = 0; r < RPT; ++r)
-        __builtin_nontemporal_store(s[r], reinterpret_cast<f32x4 *>(sb + (rg + 8 * r) * VD));
+        __builtin_nontemporal_store(s[r], reinterpret_cast<f32x4 *>(sb + (rg + NRG * r) * VD));
     }
     __syncthreads();
   }
 
   if (out_row >= 0) {
-    float *base = a.state_out + (out_row * a.Hv + h) * (int64_t)(KD * VD) + col0;
+    const auto rs = state_rsrc(a.state_out, out_row);
 #pragma unroll
     for (int r = 0; r < RPT; ++r)
-      __builtin_nontemporal_store(s[r], reinterpret_cast<f32x4 *>(base + (rg + 8 * r) * VD));
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, s[r]), rs, voff, r * ROW8, BUF_NT);
   }
 }
 
@@ -227,14 +247,14 @@ int recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
                 static_cast<long long>(state_in_rows), static_cast<long long>(state_out_rows), n_seqs);
   if (q_stride_t < Hk * K || k_stride_t < Hk * K || v_stride_t < Hv * V)
     return fail(GDN_ERR_INVALID_ARGUMENT, "%s: token stride smaller than a row", name);
-  const int64_t n_blocks = static_cast<int64_t>(n_seqs) * Hv * (VD / 32);
+  const int64_t n_blocks = static_cast<int64_t>(n_seqs) * Hv * (VD / REC_VT);
   if (n_blocks > 0x7fffffff) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: grid too large", name);
 
   RecArgs a{q, k, v, q_stride_t, k_stride_t, v_stride_t, gate, state_in, state_in_idx, state_in_rows,
             state_out, state_out_idx, state_out_rows, o, snapshots, cu_seqlens, n_seqs, T, Hk, Hv,
             cu_seqlens ? static_cast<int64_t>(T) : static_cast<int64_t>(n_seqs) * T,
             scale, l2norm_qk, qkv_dtype, o_dtype};
-  hipLaunchKernelGGL(recurrent_kernel<32>, dim3(static_cast<unsigned>(n_blocks)), dim3(64), 0,
+  hipLaunchKernelGGL((recurrent_kernel<REC_VT, REC_NT>), dim3(static_cast<unsigned>(n_blocks)), dim3(REC_NT), 0,
                      static_cast<hipStream_t>(stream), a);
   return check_launch(name);
 }
