@@ -44,7 +44,7 @@ MFMA_BF16_PEAK = 2.5e15     # dense flop/s
 DECODE_BYTES = 270_024_960
 # HBM bytes per decode launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE, each scaled by
 # the same counter on a plain 128 MiB copy (profiles/gdn_decode_b64_hbm_traffic_pmc.md)
-DECODE_TRAFFIC_MEASURED = 274_608_128
+DECODE_TRAFFIC_MEASURED = 274_600_550
 # dense-equivalent flops per (chunk, head): 2C^2(3K+2V) + 6CKV + (2/3)C^3, C=64, K=V=128
 PREFILL_FLOP_PER_CHUNK_HEAD = 11_709_099
 
@@ -61,6 +61,8 @@ def parse():
     ap.add_argument("--no-layer-glue", action="store_true",
                     help="skip the fused vs torch layer-glue timing (gates, q/k repeat, gated norm)")
     ap.add_argument("--pools", type=int, default=4, help="rotating decode state pools")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="time only the configuration 2 prefill (for counter profiles; prints no headline value)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 128 MiB device copy (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
@@ -296,6 +298,9 @@ def main():
     if args.copy_probe:
         copy_probe(torch)
         return
+    if args.prefill_only:  # the prefill kernels alone (for counter profiles); no headline value
+        print(json.dumps({"prefill": bench_prefill(torch)}), flush=True)
+        return
     d = bench_decode(torch, args.steps, args.warmup, args.pools)
     wall = d["eager_wall"]
     value = d["tokens"] * d["steps"] / wall
@@ -319,7 +324,7 @@ def main():
         "graph_tok_per_s": (d["tokens"] * d["steps"] / d["graph_wall"]) if d["graph_wall"] else None,
         "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK, "traffic": DECODE_TRAFFIC_MEASURED,
-                     "kernel": "gdn::recurrent_kernel<32>", "kernel_us": d["kernel_s"] * 1e6,
+                     "kernel": "gdn::recurrent_kernel<32, 64>", "kernel_us": d["kernel_s"] * 1e6,
                      "bytes_per_launch": DECODE_BYTES},
     }
     if not args.no_prefill:
