@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 4
+#define GDN_ABI_VERSION 5
 
 typedef enum {
   GDN_OK = 0,
@@ -237,6 +237,35 @@ int causal_conv1d_update(const void *x, int64_t x_stride_t, void *conv_state,
                          void *y, int64_t y_stride_t, int32_t n_seqs, int32_t T,
                          int32_t C, int32_t width, int32_t state_len,
                          int silu, int dtype, void *stream);
+
+/*
+ * Decode-step input projections of the GDN layer with the causal-conv update
+ * fused into the epilogue:
+ *   p       = x W_qkv^T  (rounded to bf16, as the nn.Linear output)
+ *   y_qkv   = act(conv taps . (window[1..3], p) + bias)   per channel
+ *   window  <- (window[1..3], p)                          in conv_pool[slot]
+ *   z = x W_z^T,  b = x W_b^T,  a = x W_a^T               (bf16)
+ *
+ * Replaces, for one decode token per row, the four nn.Linear projections
+ * of HF's GDN layer (transformers modeling_qwen3_5_moe.py:424-427, called at
+ * :443-450) and the causal_conv1d_update that follows (:452-461), on the
+ * reference's conv slot pool (engine/runtime/kv_cache.py:142-146).
+ *
+ *   x       [M, K] bf16, row stride x_stride (elements, >= K, multiple of 8)
+ *   w_*     [n_*, K] bf16 nn.Linear weights, rows contiguous (16-byte aligned)
+ *   conv_w  [n_qkv, 4] bf16 depthwise taps;  conv_bias [n_qkv] bf16 or NULL
+ *   conv_pool [pool_rows, n_qkv, 4] bf16 windows (oldest first), rows by
+ *           slot_idx (NULL: row m); ids outside [0, pool_rows): zero window,
+ *           nothing written
+ *   y_qkv [M, n_qkv], z [M, n_z], b [M, n_b], a [M, n_a] bf16, contiguous
+ *   K in {1024, 2048, 3072, 4096}; n_qkv, n_z multiples of 64;
+ *   n_b, n_a multiples of 4, at most 32.  silu: apply SiLU after the conv.
+ */
+int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w_qkv, const void *w_z,
+                       const void *w_b, const void *w_a, int32_t M, int32_t K, int32_t n_qkv,
+                       int32_t n_z, int32_t n_b, int32_t n_a, const void *conv_w, const void *conv_bias,
+                       void *conv_pool, const int64_t *slot_idx, int64_t pool_rows, void *y_qkv, void *z,
+                       void *b, void *a, int silu, void *stream);
 
 /*
  * Speculative-verify commit: pool[slot_ids[b]] = snapshots[b, accepted_len[b]-1].

@@ -1,0 +1,327 @@
+// Decode-time input projections of the GDN layer with the causal-conv
+// update in the epilogue.
+//
+// HF's decode step (transformers modeling_qwen3_5_moe.py:443-461) runs four
+// skinny GEMMs over the same hidden rows -- in_proj_qkv [2*Hk*K + Hv*V, D],
+// in_proj_z [Hv*V, D], in_proj_b / in_proj_a [Hv, D] -- and then
+// causal_conv1d_update over the qkv output.  At decode the batch M is small
+// (<= 64 rows per workgroup here), so the four GEMMs together are one stream
+// of D x (2*Hk*K + 2*Hv*V + 2*Hv) bf16 weights (50.6 MB for the 2048-wide
+// Qwen3.5-MoE layer) past a few KiB of activations: bound by HBM, not by the
+// matrix cores.  This kernel reads each weight row once, keeps the product
+// in registers and applies the conv update (window shift, depthwise taps,
+// bias, SiLU) to the qkv columns before anything is written, so the qkv
+// projection never round-trips through memory.
+//
+// Work split: one workgroup per 64 output columns of one matrix (b and a
+// share one block: column groups 0, 1 take b's first 32 columns, 2, 3 a's)
+// and per 64 hidden rows.  Its 16 waves are 4 column groups of 16 columns x
+// 4 quarters of K: a lone wave per 16 columns cannot keep enough weight
+// loads in flight (measured: 193 workgroups of 4 waves stream the 50.6 MB at
+// 3.0 TB/s, of 16 waves at 4.9 TB/s).  A wave issues all its weight loads
+// (16 columns x K/4 as MFMA A operands: lane (r, g) reads row r, 16 bytes
+// at k = 32 s + 8 g) at the start and multiplies each as it arrives with the
+// hidden rows of its quarter, which the workgroup copies into LDS by LDS DMA
+// (contiguous 1 KiB reads, row-major in LDS with a chunk swizzle): the first
+// half of every quarter (all 64 rows, 128 KiB) before the weights are
+// requested, the second half into the same buffer once the first is
+// consumed, its copy overlapping the tail of the weight stream.  (Loads
+// retire in order: rows requested after the weights wait for all of them.)
+// The four quarters' partial sums meet in LDS;
+// wave (column group, quarter q) adds them in quarter order for row tile q
+// and runs the epilogue on it.  Lane (c, g) of a row tile's accumulator
+// holds out[16 t + c][16 w + 4 g .. + 3]: four consecutive channels of one
+// row, also the unit of the conv pool ([rows, C, 4] bf16: 32 bytes).
+#include "gdn_common.h"
+
+namespace gdn {
+namespace {
+
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+
+constexpr int IP_CG = 4;                 // column groups of 16
+constexpr int IP_KQ = 4;                 // quarters of K
+constexpr int IP_WAVES = IP_CG * IP_KQ;  // 16
+constexpr int IP_COLS = 16 * IP_CG;      // output columns per workgroup
+constexpr int IP_ROWS = 64;              // hidden rows per workgroup (4 row tiles)
+constexpr int IP_OOB = 0x40000000;       // buffer offset past every conv pool: loads read 0, nothing stored
+
+struct InProjArgs {
+  const uint16_t *x;  // [M, K] bf16, row stride xs elements
+  int64_t xs;
+  const uint16_t *w[4];  // qkv, z, b, a: [n[i], K] bf16, rows contiguous
+  int n[4];
+  int blocks_qkv, blocks_z;  // column blocks of qkv and z; then one block for b, a (<= 32 columns each)
+  int M, K;
+  const uint16_t *cw, *cb;  // conv taps [n[0], 4] bf16, bias [n[0]] bf16 or null
+  uint16_t *pool;           // conv windows [rows, n[0], 4] bf16, updated in place
+  const int64_t *idx;
+  int64_t rows;
+  uint16_t *y[4];  // conv(qkv) [M, n[0]], z [M, n[1]], b [M, n[2]], a [M, n[3]]
+  int silu;
+};
+
+__device__ __forceinline__ f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                 c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float silu_f(float v) { return v / (1.f + expf(-v)); }
+
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+}
+
+// This wave's weights, KS k-steps of its quarter: lane (r, g) of k-step s
+// holds W[col + r][k0 + 32 s + 8 g .. + 8].  Rows past the matrix read as zero.
+template <int KS>
+__device__ __forceinline__ void load_w(u32x4_t (&wr)[KS], __amdgpu_buffer_rsrc_t rw, int k0, int K, int lane) {
+  const int voff = ((lane & 15) * K + 8 * (lane >> 4)) * 2;
+#pragma unroll
+  for (int s = 0; s < KS; ++s) wr[s] = __builtin_amdgcn_raw_buffer_load_b128(rw, voff, (k0 + 32 * s) * 2, 0);
+}
+
+// Half h of every quarter's hidden rows into LDS by DMA.  Per quarter q the
+// half is CH = 2 KS chunks of 8 elements per row, at k = q K/4 + 256 h ...
+// (K/8 per half); LDS holds it row-major, 64 rows of CH chunks, chunk p of
+// row r at position p ^ (r % CH) (so that the 16 rows an MFMA operand read
+// touches fall in 16 different bank groups).  One DMA instruction fills 64
+// consecutive positions, i.e. 64 / CH whole rows, each lane fetching the
+// chunk its position holds: contiguous global reads, 1 KiB per instruction.
+// Wave w copies instructions w, w + 16, ...  Rows past M read as zero.
+template <int KS>
+__device__ __forceinline__ void dma_x(u32x4_t *xl, __amdgpu_buffer_rsrc_t rx, int64_t xs, int K, int h, int wave,
+                                      int lane) {
+  constexpr int CH = 2 * KS, RPI = 64 / CH;  // chunks per row, rows per instruction
+#pragma unroll
+  for (int i = 0; i < IP_KQ * CH / IP_WAVES; ++i) {
+    const int j = wave + IP_WAVES * i;  // quarter j / CH, rows RPI (j % CH) ..
+    const int q = j / CH;
+    const int r = RPI * (j % CH) + lane / CH, pos = lane % CH;
+    const int voff = static_cast<int>((r * xs + 8 * (pos ^ (r % CH))) * 2);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, xl + j * 64, 16, voff, (q * (K / IP_KQ) + h * (K / 8)) * 2, 0, 0);
+  }
+}
+
+// Half h of this wave's quarter against its staged rows (all four row tiles):
+// B operand of row tile t, k-step s at lane (c, g) = row 16 t + c, chunk 4 s + g.
+template <int KS, int HALF>
+__device__ __forceinline__ void half_mfma(f32x4_t (&acc)[4], const u32x4_t (&wr)[KS], const u32x4_t *xq, int lane) {
+  constexpr int H = KS / 2, CH = 2 * KS;
+  const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int s = 0; s < H; ++s)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int r = 16 * t + c;
+      acc[t] = mfma16(wr[HALF * H + s], xq[r * CH + ((4 * s + g) ^ (r % CH))], acc[t]);
+    }
+}
+
+// s_waitcnt operand: vmcnt <= n, lgkmcnt and expcnt unconstrained
+constexpr int ip_vmcnt(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
+// KS = K / 128 k-steps per quarter (K = 1024, 2048).
+template <int KS>
+__global__ __launch_bounds__(64 * IP_WAVES) void in_proj_decode_kernel(InProjArgs a) {
+  __shared__ u32x4_t xl[IP_KQ * 4 * (KS / 2) * 64];  // 64 rows of half of K: 128 KiB at K = 2048
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cg = wave & (IP_CG - 1), kq = wave / IP_CG;
+  const int m0 = blockIdx.y * IP_ROWS;
+  const int mb = min(IP_ROWS, a.M - m0);
+
+  // this wave's matrix and first column
+  int mat, col;
+  const int bid = blockIdx.x;
+  if (bid < a.blocks_qkv) {
+    mat = 0;
+    col = bid * IP_COLS + 16 * cg;
+  } else if (bid < a.blocks_qkv + a.blocks_z) {
+    mat = 1;
+    col = (bid - a.blocks_qkv) * IP_COLS + 16 * cg;
+  } else {
+    mat = 2 + (cg >> 1);
+    col = 16 * (cg & 1);
+  }
+  mat = __builtin_amdgcn_readfirstlane(mat);
+  col = __builtin_amdgcn_readfirstlane(col);
+  // (selects, not a.w[mat]: an indexed kernel-argument array is not known to be uniform)
+  const uint16_t *wmat = mat == 0 ? a.w[0] : mat == 1 ? a.w[1] : mat == 2 ? a.w[2] : a.w[3];
+  const int nmat = mat == 0 ? a.n[0] : mat == 1 ? a.n[1] : mat == 2 ? a.n[2] : a.n[3];
+  const int live = __builtin_amdgcn_readfirstlane(max(0, min(16, nmat - col)));  // columns of this wave in its matrix
+  const auto rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(wmat) + static_cast<int64_t>(col) * a.K, 0,
+                                                    live * a.K * 2, BUF_DWORD3);
+  const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.x) + static_cast<int64_t>(m0) * a.xs, 0,
+                                                    static_cast<int>(((mb - 1) * a.xs + a.K) * 2), BUF_DWORD3);
+  const int c = lane & 15, g = lane >> 4;
+  const int n = col + 4 * g;
+  const int me = m0 + 16 * kq + c;  // the row this lane finishes
+  const bool conv = mat == 0;
+  const auto rp = __builtin_amdgcn_make_buffer_rsrc(a.pool, 0, conv ? static_cast<int>(a.rows * a.n[0] * 8) : 0,
+                                                    BUF_DWORD3);
+  const auto rc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.cw), 0, conv ? a.n[0] * 8 : 0,
+                                                    BUF_DWORD3);
+  const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.cb), 0, conv && a.cb ? a.n[0] * 2 : 0,
+                                                    BUF_DWORD3);
+
+  // Issue order: the epilogue's slot id, taps and bias; rows 0-31 (DMA);
+  // all weights; then the conv window, whose address needs the id (the
+  // oldest load, so waiting for it waits for nothing else).
+  // (through a buffer so that a missing id array reads 0 instead of branching on a load)
+  const auto ri = __builtin_amdgcn_make_buffer_rsrc(const_cast<int64_t *>(a.idx), 0, a.idx ? a.M * 8 : 0, BUF_DWORD3);
+  const uint64_t id_raw = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(ri, min(me, a.M - 1) * 8, 0, 0));
+  const u32x4_t w01 = __builtin_amdgcn_raw_buffer_load_b128(rc, n * 8, 0, 0);
+  const u32x4_t w23 = __builtin_amdgcn_raw_buffer_load_b128(rc, n * 8, 16, 0);
+  const uint64_t bias4 = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(rb, n * 2, 0, 0));
+  __builtin_amdgcn_sched_barrier(0);
+  dma_x<KS>(xl, rx, a.xs, a.K, 0, wave, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4_t wr[KS];
+  load_w<KS>(wr, rw, kq * (a.K / IP_KQ), a.K, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  const int64_t id = a.idx ? static_cast<int64_t>(id_raw) : me;  // pool_row's rule
+  const int woff = conv && me < a.M && id >= 0 && id < a.rows ? static_cast<int>((id * a.n[0] + n) * 8) : IP_OOB;
+  u32x4_t win[2];
+  win[0] = __builtin_amdgcn_raw_buffer_load_b128(rp, woff, 0, 0);
+  win[1] = __builtin_amdgcn_raw_buffer_load_b128(rp, woff, 16, 0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  f32x4_t acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const u32x4_t *xq = xl + kq * (64 * 2 * KS);
+  __builtin_amdgcn_s_waitcnt(ip_vmcnt(KS + 2));  // this wave's copies landed (weights, window may still fly)
+  __syncthreads();
+  half_mfma<KS, 0>(acc, wr, xq, lane);
+  __syncthreads();  // the first halves are consumed: the second into the same buffer
+  dma_x<KS>(xl, rx, a.xs, a.K, 1, wave, lane);
+  __builtin_amdgcn_s_waitcnt(ip_vmcnt(0));
+  __syncthreads();
+  half_mfma<KS, 1>(acc, wr, xq, lane);
+
+  // quarter partials through LDS (the rows' buffer, once every wave is done with it)
+  __syncthreads();
+  f32x4_t *red = reinterpret_cast<f32x4_t *>(xl);  // [quarter][column group][row tile][lane]: 64 KiB
+#pragma unroll
+  for (int t = 0; t < 4; ++t) red[((kq * IP_CG + cg) * 4 + t) * 64 + lane] = acc[t];
+  __syncthreads();
+  f32x4_t o = red[((0 * IP_CG + cg) * 4 + kq) * 64 + lane];
+#pragma unroll
+  for (int q = 1; q < IP_KQ; ++q) o += red[((q * IP_CG + cg) * 4 + kq) * 64 + lane];
+
+  // ---- epilogue of row tile kq: lane (c, g) holds row me, columns n .. n + 3
+  if (4 * g >= live || me >= a.M) return;  // (live is a multiple of 4)
+  if (conv) {
+    // the conv update kernel's arithmetic: fp32, bias first, taps oldest first
+    float y[4];
+    uint32_t nw[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const u32x4_t &tv = e < 2 ? w01 : w23;
+      const uint32_t tlo = tv[2 * (e & 1)], thi = tv[2 * (e & 1) + 1];
+      const u32x4_t &v = win[e >> 1];
+      const uint32_t lo = v[2 * (e & 1)], hi = v[2 * (e & 1) + 1];
+      const uint16_t xb = f32_to_bf16_bits(o[e]);
+      float acc_c = bf16_bits_to_f32(static_cast<uint16_t>(bias4 >> (16 * e)));
+      acc_c += bf16_bits_to_f32(tlo & 0xffffu) * bf16_bits_to_f32(lo >> 16);
+      acc_c += bf16_bits_to_f32(tlo >> 16) * bf16_bits_to_f32(hi & 0xffffu);
+      acc_c += bf16_bits_to_f32(thi & 0xffffu) * bf16_bits_to_f32(hi >> 16);
+      acc_c += bf16_bits_to_f32(thi >> 16) * bf16_bits_to_f32(xb);
+      y[e] = a.silu ? silu_f(acc_c) : acc_c;
+      nw[2 * e] = (lo >> 16) | (hi << 16);                            // s1 | s2
+      nw[2 * e + 1] = (hi >> 16) | (static_cast<uint32_t>(xb) << 16);  // s3 | x
+    }
+    if (woff != IP_OOB) {
+      u32x4_t *st = reinterpret_cast<u32x4_t *>(reinterpret_cast<char *>(a.pool) + woff);
+      st[0] = u32x4_t{nw[0], nw[1], nw[2], nw[3]};
+      st[1] = u32x4_t{nw[4], nw[5], nw[6], nw[7]};
+    }
+    uint2 *yp = reinterpret_cast<uint2 *>(a.y[0] + static_cast<int64_t>(me) * a.n[0] + n);
+    *yp = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+  } else {
+    uint16_t *ymat = mat == 1 ? a.y[1] : mat == 2 ? a.y[2] : a.y[3];
+    uint2 *yp = reinterpret_cast<uint2 *>(ymat + static_cast<int64_t>(me) * nmat + n);
+    *yp = make_uint2(pack2(o[0], o[1]), pack2(o[2], o[3]));
+  }
+}
+
+}  // namespace
+}  // namespace gdn
+
+extern "C" int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w_qkv, const void *w_z,
+                                  const void *w_b, const void *w_a, int32_t M, int32_t K, int32_t n_qkv,
+                                  int32_t n_z, int32_t n_b, int32_t n_a, const void *conv_w, const void *conv_bias,
+                                  void *conv_pool, const int64_t *slot_idx, int64_t pool_rows, void *y_qkv, void *z,
+                                  void *b, void *a, int silu, void *stream) {
+  using namespace gdn;
+  if (!x || !w_qkv || !w_z || !conv_w || !conv_pool || !y_qkv || !z || ((n_b > 0) && (!w_b || !b)) ||
+      ((n_a > 0) && (!w_a || !a)))
+    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_in_proj_decode: null pointer argument");
+  if (M < 0 || n_qkv <= 0 || n_qkv % IP_COLS || n_z < 0 || n_z % IP_COLS || n_b < 0 || n_a < 0 || n_b % 4 ||
+      n_a % 4 || n_b > 32 || n_a > 32)
+    return fail(GDN_ERR_UNSUPPORTED,
+                "gdn_in_proj_decode: need n_qkv and n_z multiples of %d, n_b and n_a multiples of 4 up to 32 "
+                "(got M=%d n=%d/%d/%d/%d)",
+                IP_COLS, M, n_qkv, n_z, n_b, n_a);
+  if (K != 1024 && K != 2048)
+    return fail(GDN_ERR_UNSUPPORTED, "gdn_in_proj_decode: K=%d (built for 1024 and 2048)", K);
+  if (x_stride < K || x_stride % 8)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_in_proj_decode: x row stride %lld must be >= K and a multiple of 8",
+                static_cast<long long>(x_stride));
+  // buffer offsets are 32-bit: one weight tile row block and one 64-row slice of x
+  if (static_cast<int64_t>(16) * K * 2 > INT32_MAX || (static_cast<int64_t>(IP_ROWS - 1) * x_stride + K) * 2 > INT32_MAX)
+    return fail(GDN_ERR_UNSUPPORTED, "gdn_in_proj_decode: K=%d / x stride %lld too large", K,
+                static_cast<long long>(x_stride));
+  auto al = [](const void *p, uintptr_t n) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % n == 0; };
+  if (!al(x, 16) || !al(w_qkv, 16) || !al(w_z, 16) || !al(w_b, 16) || !al(w_a, 16) || !al(conv_w, 16) ||
+      !al(conv_pool, 16) || !al(y_qkv, 8) || !al(z, 8) || !al(b, 8) || !al(a, 8) || !al(conv_bias, 2))
+    return fail(GDN_ERR_INVALID_ARGUMENT,
+                "gdn_in_proj_decode: x, weights, conv taps and pool must be 16-byte aligned, outputs 8-byte aligned");
+  if (pool_rows * n_qkv * 8 >= IP_OOB)
+    return fail(GDN_ERR_UNSUPPORTED, "gdn_in_proj_decode: conv pool of %lld rows x %d channels exceeds 1 GiB",
+                static_cast<long long>(pool_rows), n_qkv);
+  if (!rows_cover(conv_pool, slot_idx, pool_rows, M))
+    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_in_proj_decode: %lld pool rows do not cover %d rows",
+                static_cast<long long>(pool_rows), M);
+  if (M == 0) return ok();
+  if ((M + IP_ROWS - 1) / IP_ROWS > 65535)
+    return fail(GDN_ERR_UNSUPPORTED, "gdn_in_proj_decode: M=%d too large", M);
+  InProjArgs args{};
+  args.x = static_cast<const uint16_t *>(x);
+  args.xs = x_stride;
+  args.w[0] = static_cast<const uint16_t *>(w_qkv);
+  args.w[1] = static_cast<const uint16_t *>(w_z);
+  args.w[2] = static_cast<const uint16_t *>(w_b);
+  args.w[3] = static_cast<const uint16_t *>(w_a);
+  args.n[0] = n_qkv;
+  args.n[1] = n_z;
+  args.n[2] = n_b;
+  args.n[3] = n_a;
+  args.blocks_qkv = n_qkv / IP_COLS;
+  args.blocks_z = n_z / IP_COLS;
+  args.M = M;
+  args.K = K;
+  args.cw = static_cast<const uint16_t *>(conv_w);
+  args.cb = static_cast<const uint16_t *>(conv_bias);
+  args.pool = static_cast<uint16_t *>(conv_pool);
+  args.idx = slot_idx;
+  args.rows = pool_rows;
+  args.y[0] = static_cast<uint16_t *>(y_qkv);
+  args.y[1] = static_cast<uint16_t *>(z);
+  args.y[2] = static_cast<uint16_t *>(b);
+  args.y[3] = static_cast<uint16_t *>(a);
+  args.silu = silu;
+  const dim3 grid(static_cast<unsigned>(args.blocks_qkv + args.blocks_z + (n_b + n_a > 0 ? 1 : 0)),
+                  static_cast<unsigned>((M + IP_ROWS - 1) / IP_ROWS));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (K) {
+    case 1024: hipLaunchKernelGGL(in_proj_decode_kernel<8>, grid, dim3(64 * IP_WAVES), 0, s, args); break;
+    case 2048: hipLaunchKernelGGL(in_proj_decode_kernel<16>, grid, dim3(64 * IP_WAVES), 0, s, args); break;
+    default: return fail(GDN_ERR_UNSUPPORTED, "gdn_in_proj_decode: K=%d unsupported", K);
+  }
+  return check_launch("gdn_in_proj_decode");
+}

@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libgdn_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 GDN_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
@@ -82,6 +82,14 @@ SIGNATURES = {
         _c_void_p, _int,                            # weight w_dtype
         _c_void_p, _int, _i64,                      # y y_dtype y_stride
         _i64, _i32, _i32, _f32, _c_void_p]),        # n_tokens H D eps stream
+    "gdn_in_proj_decode": (_int, [
+        _c_void_p, _i64,                            # x x_stride
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, # w_qkv w_z w_b w_a
+        _i32, _i32, _i32, _i32, _i32, _i32,         # M K n_qkv n_z n_b n_a
+        _c_void_p, _c_void_p,                       # conv_w conv_bias
+        _c_void_p, _c_void_p, _i64,                 # conv_pool slot_idx pool_rows
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, # y_qkv z b a
+        _int, _c_void_p]),                          # silu stream
     "causal_conv1d_fwd": (_int, [
         _c_void_p, _i64, _c_void_p, _c_void_p,      # x x_stride w bias
         _c_void_p, _i64,                            # y y_stride

@@ -13,10 +13,13 @@ hybrid layers) computes, around the core kernel, in separate torch ops:
 
 :func:`gated_delta_net_forward` is that forward with the gates computed in
 the kernel prologues (``*_from_projections``), q/k passed at their 16 heads
-(native GQA), and the norm as one HIP pass (:func:`rms_norm_gated`).  The
-projections stay torch matmuls (hipBLASLt) and the conv runs the HIP
-``causal_conv1d`` kernels; the cache calls are HF's own, in HF's order, so
-the layer works with the transformers cache unchanged.  With an engine
+(native GQA), and the norm as one HIP pass (:func:`rms_norm_gated`).  A
+one-token decode step runs the four input projections and the conv update
+as one HIP kernel (:func:`engine.kernels.in_proj.gdn_in_proj_decode`);
+otherwise the projections are torch matmuls (hipBLASLt) and the conv runs
+the HIP ``causal_conv1d`` kernels on their output in place.  The cache calls
+are HF's own, in HF's order, so the layer works with the transformers cache
+unchanged.  With an engine
 slot-pool cache (``cache_params.gdn_slot_pools``, see
 :mod:`engine.runtime.slot_pools`) the kernels address the pools by slot id
 instead.  :func:`install_gdn_layer_patch` swaps it in for the HF layer
@@ -36,6 +39,7 @@ from . import _lib
 from .causal_conv1d import causal_conv1d_fn, causal_conv1d_update
 from .delta_rule import chunk_gated_delta_rule_from_projections
 from .fused_recurrent import fused_recurrent_gated_delta_rule_from_projections
+from .in_proj import fused_in_proj_supported, gdn_in_proj_decode
 
 log = logging.getLogger(__name__)
 
@@ -77,6 +81,35 @@ def rms_norm_gated(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: 
     return y.view(x.shape)
 
 
+def _fused_decode_fits(self, hidden_states: torch.Tensor, conv_state: torch.Tensor) -> bool:
+    """Whether this one-token step can take :func:`gdn_in_proj_decode`: bf16
+    bias-free projections of a supported shape and a bf16 [rows, C, 4] window
+    pool."""
+    lins = (self.in_proj_qkv, self.in_proj_z, self.in_proj_b, self.in_proj_a)
+    if hidden_states.dtype != torch.bfloat16 or hidden_states.shape[1] != 1:
+        return False
+    if any(l.bias is not None or l.weight.dtype != torch.bfloat16 for l in lins):
+        return False
+    if self.conv1d.weight.dtype != torch.bfloat16 or self.activation not in ("silu", "swish", None):
+        return False
+    n = [l.weight.shape[0] for l in lins]
+    if not fused_in_proj_supported(hidden_states.shape[-1], *n, self.conv1d.weight.shape[-1]):
+        return False
+    return (conv_state.dtype == torch.bfloat16 and conv_state.dim() == 3 and conv_state.is_contiguous()
+            and tuple(conv_state.shape[1:]) == (n[0], 4))
+
+
+def _fused_decode(self, hidden_states: torch.Tensor, conv_state: torch.Tensor,
+                  slots: Optional[torch.Tensor]) -> tuple[torch.Tensor, ...]:
+    """(mixed_qkv after the conv [B, 1, C], z [B, 1, Hv*V], b, a [B, 1, Hv])
+    of a one-token step, conv windows advanced in place."""
+    batch_size = hidden_states.shape[0]
+    y, z, b, a = gdn_in_proj_decode(hidden_states.reshape(batch_size, -1), self.in_proj_qkv.weight,
+                                    self.in_proj_z.weight, self.in_proj_b.weight, self.in_proj_a.weight,
+                                    self.conv1d.weight, self.conv1d.bias, conv_state, slots, self.activation)
+    return tuple(t.view(batch_size, 1, -1) for t in (y, z, b, a))
+
+
 def gated_delta_net_forward(self, hidden_states: torch.Tensor, cache_params=None,
                             attention_mask: Optional[torch.Tensor] = None, **kwargs) -> torch.Tensor:
     """Forward of HF's GDN layer (``self`` is a ``*GatedDeltaNet`` module of
@@ -91,25 +124,28 @@ def gated_delta_net_forward(self, hidden_states: torch.Tensor, cache_params=None
     batch_size, seq_len, _ = hidden_states.shape
     use_precomputed_states = cache_params is not None and cache_params.has_previous_state(self.layer_idx)
 
-    mixed_qkv = self.in_proj_qkv(hidden_states).transpose(1, 2)
-    z = self.in_proj_z(hidden_states)
-    b = self.in_proj_b(hidden_states)
-    a = self.in_proj_a(hidden_states)
-    conv_w = self.conv1d.weight.squeeze(1)
-
     layer = cache_params.layers[self.layer_idx] if cache_params is not None else None
-    if use_precomputed_states and seq_len == 1 and not layer.record_past:
-        mixed_qkv = causal_conv1d_update(mixed_qkv, layer.conv_states[0], conv_w, self.conv1d.bias,
-                                         self.activation)
+    decode_step = use_precomputed_states and seq_len == 1 and not layer.record_past
+    if decode_step and layer.conv_states[0].shape[0] == batch_size and _fused_decode_fits(
+            self, hidden_states, layer.conv_states[0]):
+        mixed_qkv, z, b, a = _fused_decode(self, hidden_states, layer.conv_states[0], None)
     else:
-        if cache_params is not None:
-            mixed_qkv = cache_params.update_conv_state(mixed_qkv, self.layer_idx,
-                                                       conv_kernel_size=self.conv_kernel_size)
-        mixed_qkv = causal_conv1d_fn(mixed_qkv, conv_w, self.conv1d.bias, activation=self.activation)
-        if cache_params is not None:
-            mixed_qkv = mixed_qkv[:, :, -seq_len:]
-
-    mixed_qkv = mixed_qkv.transpose(1, 2)
+        mixed_qkv = self.in_proj_qkv(hidden_states).transpose(1, 2)
+        z = self.in_proj_z(hidden_states)
+        b = self.in_proj_b(hidden_states)
+        a = self.in_proj_a(hidden_states)
+        conv_w = self.conv1d.weight.squeeze(1)
+        if decode_step:
+            mixed_qkv = causal_conv1d_update(mixed_qkv, layer.conv_states[0], conv_w, self.conv1d.bias,
+                                             self.activation)
+        else:
+            if cache_params is not None:
+                mixed_qkv = cache_params.update_conv_state(mixed_qkv, self.layer_idx,
+                                                           conv_kernel_size=self.conv_kernel_size)
+            mixed_qkv = causal_conv1d_fn(mixed_qkv, conv_w, self.conv1d.bias, activation=self.activation)
+            if cache_params is not None:
+                mixed_qkv = mixed_qkv[:, :, -seq_len:]
+        mixed_qkv = mixed_qkv.transpose(1, 2)
     query, key, value = torch.split(mixed_qkv, [self.key_dim, self.key_dim, self.value_dim], dim=-1)
     query = query.reshape(batch_size, seq_len, -1, self.head_k_dim)  # 16 heads: no repeat_interleave
     key = key.reshape(batch_size, seq_len, -1, self.head_k_dim)
@@ -161,21 +197,24 @@ def _forward_on_pools(self, hidden_states: torch.Tensor, pools, attention_mask: 
     if verify and seq_len != verify:
         raise ValueError(f"verify step bound for {verify} tokens, forward has {seq_len}")
 
-    mixed_qkv = self.in_proj_qkv(hidden_states).transpose(1, 2)  # [B, conv_dim, L]
-    z = self.in_proj_z(hidden_states)
-    b = self.in_proj_b(hidden_states)
-    a = self.in_proj_a(hidden_states)
-    conv_w = self.conv1d.weight.squeeze(1)
-    if pools.decode and seq_len == 1:
-        mixed_qkv = causal_conv1d_update(mixed_qkv, conv_pool, conv_w, self.conv1d.bias, self.activation,
-                                         conv_state_indices=slots)
+    if pools.decode and seq_len == 1 and _fused_decode_fits(self, hidden_states, conv_pool):
+        mixed_qkv, z, b, a = _fused_decode(self, hidden_states, conv_pool, slots)
     else:
-        if verify:
-            pools.record_conv(self.layer_idx, mixed_qkv)
-        mixed_qkv = causal_conv1d_fn(mixed_qkv, conv_w, self.conv1d.bias, activation=self.activation,
-                                     conv_states=conv_pool, cache_indices=slots, has_initial_state=pools.has_state())
-
-    mixed_qkv = mixed_qkv.transpose(1, 2)
+        mixed_qkv = self.in_proj_qkv(hidden_states).transpose(1, 2)  # [B, conv_dim, L]
+        z = self.in_proj_z(hidden_states)
+        b = self.in_proj_b(hidden_states)
+        a = self.in_proj_a(hidden_states)
+        conv_w = self.conv1d.weight.squeeze(1)
+        if pools.decode and seq_len == 1:
+            mixed_qkv = causal_conv1d_update(mixed_qkv, conv_pool, conv_w, self.conv1d.bias, self.activation,
+                                             conv_state_indices=slots)
+        else:
+            if verify:
+                pools.record_conv(self.layer_idx, mixed_qkv)
+            mixed_qkv = causal_conv1d_fn(mixed_qkv, conv_w, self.conv1d.bias, activation=self.activation,
+                                         conv_states=conv_pool, cache_indices=slots,
+                                         has_initial_state=pools.has_state())
+        mixed_qkv = mixed_qkv.transpose(1, 2)
     query, key, value = torch.split(mixed_qkv, [self.key_dim, self.key_dim, self.value_dim], dim=-1)
     query = query.reshape(batch_size, seq_len, -1, self.head_k_dim)
     key = key.reshape(batch_size, seq_len, -1, self.head_k_dim)

@@ -30,7 +30,7 @@ def test_header_lists_the_entry_points():
     assert header_functions() == sorted([
         "causal_conv1d_fwd", "causal_conv1d_update", "gdn_abi_version", "gdn_chunk_fwd",
         "gdn_chunk_fwd_gated", "gdn_chunk_workspace_bytes", "gdn_last_error_string", "gdn_recurrent_fwd",
-        "gdn_recurrent_fwd_gated", "gdn_rmsnorm_gated_fwd", "gdn_state_commit", "gdn_conv_state_commit"])
+        "gdn_recurrent_fwd_gated", "gdn_rmsnorm_gated_fwd", "gdn_state_commit", "gdn_conv_state_commit", "gdn_in_proj_decode"])
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -41,7 +41,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.gdn_abi_version() == _lib.ABI_VERSION == 4
+    assert lib.gdn_abi_version() == _lib.ABI_VERSION == 5
 
 
 def _rec_call(lib, **over):
@@ -172,3 +172,25 @@ def test_rmsnorm_gated_rejects_bad_arguments(lib):
     assert call(x=8) == 1                                  # misaligned rows
     assert call(eps=-1.0) == 1
     assert call(n=0) == 0                                  # nothing to do
+
+
+def _inproj_call(lib, **over):
+    args = dict(x=16, xs=2048, wq=16, wz=16, wb=16, wa=16, m=4, k=2048, nq=8192, nz=4096, nb=32, na=32,
+                cw=16, cb=None, pool=16, idx=None, rows=4, y=16, z=16, b=16, a=16, silu=1, stream=None)
+    args.update(over)
+    return lib.gdn_in_proj_decode(*args.values())
+
+
+def test_in_proj_decode_rejects_bad_arguments(lib):
+    assert _inproj_call(lib, k=1000, xs=1000) == 2
+    assert "K=1000" in lib.gdn_last_error_string().decode()
+    assert _inproj_call(lib, nq=8190) == 2   # qkv columns not a multiple of 64
+    assert _inproj_call(lib, nb=40) == 2     # b wider than 32
+    assert _inproj_call(lib, na=6) == 2      # a not a multiple of 4
+    assert _inproj_call(lib, xs=1024) == 1   # row stride below K
+    assert _inproj_call(lib, pool=None) == 1
+    assert _inproj_call(lib, wb=None) == 1   # n_b > 0 needs its weight
+    assert _inproj_call(lib, x=24) == 1      # misaligned
+    assert _inproj_call(lib, rows=3) == 1    # the pool does not cover row m without ids
+    assert "pool rows" in lib.gdn_last_error_string().decode()
+    assert _inproj_call(lib, m=0) == 0       # nothing to do, nothing launched

@@ -1,0 +1,208 @@
+"""GPU parity of the fused decode input projections (gdn_in_proj_decode:
+four projections + causal conv update) with the CPU oracle, with the
+unfused GPU path, under graph capture, and inside the GDN layer against
+HF's module.
+
+Tolerances: bf16 outputs |y - y_ref| <= 2e-2 * max(1, |y_ref|) (the north
+star's 2e-2 abs bound, widened to one bf16 ulp for |y| > 1); window taps
+that are copies are compared bit-exactly, the new tap (the bf16-rounded
+projection) to one bf16 ulp plus the fp32 summation error of a 2048-term
+dot product, 2^-16 * sum_i |x_i w_i| (the oracle sums exactly; where the
+sum cancels, fp32 rounding moves the bf16 result by more than one ulp)."""
+import types
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import conv
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not torch.cuda.is_available(), reason="needs an MI355X")]
+
+DEV = "cuda"
+K, NQKV, NZ, NB, NA = 2048, 8192, 4096, 32, 32  # the Qwen3.5-MoE GDN layer
+
+
+def np64(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def bf16_close(y, y_ref):
+    return (np.abs(np64(y) - y_ref) / np.maximum(1.0, np.abs(y_ref))).max() <= 2e-2
+
+
+def weights(gen, k=K, n=(NQKV, NZ, NB, NA), bias=False):
+    ws = [(0.02 * torch.randn(m, k, generator=gen)).to(torch.bfloat16).to(DEV) for m in n]
+    cw = (0.5 * torch.randn(n[0], 4, generator=gen)).to(torch.bfloat16).to(DEV)
+    cb = (0.1 * torch.randn(n[0], generator=gen)).to(torch.bfloat16).to(DEV) if bias else None
+    return ws, cw, cb
+
+
+def tap_close(got, ref, x, w):
+    """New window tap vs its reference: one bf16 ulp + fp32 sum error."""
+    scale = np.abs(np64(x)) @ np.abs(np64(w)).T
+    return (np.abs(got - ref) <= 2.0 ** -7 * np.abs(ref) + 2.0 ** -16 * scale).all()
+
+
+def run_fused(x, ws, cw, cb, pool, slots):
+    from engine.kernels.in_proj import gdn_in_proj_decode
+    return gdn_in_proj_decode(x, *ws, cw, cb, pool, slots)
+
+
+@pytest.mark.parametrize("m,bias", [(64, False), (5, True), (1, False), (100, False)])
+def test_matches_oracle_at_model_shape(m, bias):
+    print(f"in_proj_decode oracle case M={m} bias={bias}", flush=True)
+    gen = torch.Generator().manual_seed(71 + m)
+    ws, cw, cb = weights(gen, bias=bias)
+    rows = 128
+    pool = torch.randn(rows, NQKV, 4, generator=gen).to(torch.bfloat16).to(DEV)
+    slots = torch.randperm(rows, generator=gen)[:m]
+    if m >= 5:
+        slots[3] = -1  # a padding row
+    x = torch.randn(m, K, generator=gen).to(torch.bfloat16).to(DEV)
+    pool0 = pool.clone()
+    y, z, b, a = run_fused(x, ws, cw, cb, pool, slots.to(DEV))
+
+    s = slots.numpy()
+    hist = np.zeros((m, NQKV, 4))
+    live = s >= 0
+    hist[live] = np64(pool0)[s[live]]
+    y_ref, z_ref, b_ref, a_ref, st_ref = conv.in_proj_decode(
+        np64(x), *(np64(w) for w in ws), np64(cw), hist, None if cb is None else np64(cb))
+    assert bf16_close(y, y_ref)
+    for got, ref in ((z, z_ref), (b, b_ref), (a, a_ref)):
+        assert bf16_close(got, ref)
+    new = np64(pool)
+    assert np.array_equal(new[s[live]][:, :, :3], st_ref[live][:, :, :3])
+    assert tap_close(new[s[live]][:, :, 3], st_ref[live][:, :, 3], x[torch.from_numpy(live).to(DEV)], ws[0])
+    untouched = np.setdiff1d(np.arange(rows), s[live])
+    assert torch.equal(pool[untouched], pool0[untouched])
+
+
+def test_matches_the_unfused_gpu_path():
+    """Four hipBLASLt projections (torch F.linear) then the conv update kernel."""
+    import torch.nn.functional as F
+    from engine.kernels import causal_conv1d_update
+    gen = torch.Generator().manual_seed(81)
+    ws, cw, cb = weights(gen)
+    pool = torch.randn(96, NQKV, 4, generator=gen).to(torch.bfloat16).to(DEV)
+    slots = torch.randperm(96, generator=gen)[:64].to(DEV)
+    x = torch.randn(64, K, generator=gen).to(torch.bfloat16).to(DEV)
+    pool_ref = pool.clone()
+    y, z, b, a = run_fused(x, ws, cw, cb, pool, slots)
+    qkv, z2, b2, a2 = (F.linear(x, w) for w in ws)
+    y2 = causal_conv1d_update(qkv[:, :, None], pool_ref, cw, None, "silu", conv_state_indices=slots)[:, :, 0]
+    for got, ref in ((y, y2), (z, z2), (b, b2), (a, a2)):
+        assert bf16_close(got, np64(ref))
+    assert torch.equal(pool[:, :, :3], pool_ref[:, :, :3])
+    sl = slots.cpu()
+    assert tap_close(np64(pool[sl, :, 3]), np64(pool_ref[sl, :, 3]), x, ws[0])
+    others = np.setdiff1d(np.arange(96), sl.numpy())
+    assert torch.equal(pool[others], pool_ref[others])
+
+
+def test_rows_without_ids_use_row_m_and_small_shapes():
+    """NULL ids (HF's per-batch cache [B, C, 4]) and small shapes: K = 1024
+    (one round per quarter), b / a narrower than a wave's 16 columns."""
+    gen = torch.Generator().manual_seed(82)
+    n = (1024, 512, 4, 8)
+    ws, cw, cb = weights(gen, k=1024, n=n)
+    pool = torch.randn(3, n[0], 4, generator=gen).to(torch.bfloat16).to(DEV)
+    x = torch.randn(3, 1024, generator=gen).to(torch.bfloat16).to(DEV)
+    pool0 = pool.clone()
+    y, z, b, a = run_fused(x, ws, cw, cb, pool, None)
+    y_ref, z_ref, b_ref, a_ref, st_ref = conv.in_proj_decode(np64(x), *(np64(w) for w in ws), np64(cw), np64(pool0))
+    assert b.shape == (3, 4) and a.shape == (3, 8)
+    for got, ref in ((y, y_ref), (z, z_ref), (b, b_ref), (a, a_ref)):
+        assert bf16_close(got, ref)
+    assert np.array_equal(np64(pool)[:, :, :3], st_ref[:, :, :3])
+
+
+def test_graph_replays_match_eager():
+    gen = torch.Generator().manual_seed(83)
+    ws, cw, cb = weights(gen)
+    pool = torch.randn(80, NQKV, 4, generator=gen).to(torch.bfloat16).to(DEV)
+    slots = torch.randperm(80, generator=gen)[:48].to(DEV)
+    static_x = torch.zeros(48, K, dtype=torch.bfloat16, device=DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    p0 = pool.clone()
+    with torch.cuda.stream(side):
+        run_fused(static_x, ws, cw, cb, pool, slots)  # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    pool.copy_(p0)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = run_fused(static_x, ws, cw, cb, pool, slots)
+    pool.copy_(p0)
+    for step in range(3):
+        x = torch.randn(48, K, generator=gen).to(torch.bfloat16).to(DEV)
+        before = pool.clone()
+        eager = run_fused(x, ws, cw, cb, pool, slots)
+        after = pool.clone()
+        pool.copy_(before)
+        torch.cuda.synchronize()
+        static_x.copy_(x)
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, ref in zip(outs, eager):
+            assert torch.equal(got, ref), step
+        assert torch.equal(pool, after), step
+
+
+def test_layer_decode_takes_the_fused_kernel_and_matches_hf(monkeypatch):
+    """A 1024-wide GDN layer (the fused kernel's smallest K): prefill through
+    the slot pools, then decode steps, against HF's module per sequence."""
+    from transformers.cache_utils import DynamicCache
+    from transformers.models.qwen3_5_moe import modeling_qwen3_5_moe as hf
+    from transformers.models.qwen3_5_moe.configuration_qwen3_5_moe import Qwen3_5MoeTextConfig
+    from engine.kernels import gated_delta_net_forward, gdn_layer
+    from engine.runtime import GDNSlotPools
+    from oracle import gdn
+
+    cfg = Qwen3_5MoeTextConfig(hidden_size=1024, num_hidden_layers=1, layer_types=["linear_attention"],
+                               linear_num_key_heads=2, linear_num_value_heads=4, linear_key_head_dim=128,
+                               linear_value_head_dim=128, linear_conv_kernel_dim=4, rms_norm_eps=1e-6)
+    torch.manual_seed(84)
+    ref = hf.Qwen3_5MoeGatedDeltaNet(cfg, layer_idx=0).eval()
+    with torch.no_grad():
+        for p in ref.parameters():
+            p.copy_(p.to(torch.bfloat16).float())
+        ref.A_log.copy_(torch.log(torch.empty(4).uniform_(0.5, 4.0)).to(torch.bfloat16).float())
+    layer = hf.Qwen3_5MoeGatedDeltaNet(cfg, layer_idx=0).eval()
+    layer.load_state_dict(ref.state_dict())
+    layer = layer.to(DEV, torch.bfloat16)
+
+    calls = []
+    real = gdn_layer.gdn_in_proj_decode
+    monkeypatch.setattr(gdn_layer, "gdn_in_proj_decode", lambda *a, **k: calls.append(1) or real(*a, **k))
+
+    pools = GDNSlotPools.allocate([0], 6, conv_dim=2 * 2 * 128 + 4 * 128, num_v_heads=4, device=torch.device(DEV))
+    cache = types.SimpleNamespace(gdn_slot_pools=pools)
+    gen = torch.Generator().manual_seed(85)
+    slots, lens = [4, 1, 2], [40, 7, 70]
+    hf_caches = [DynamicCache(config=cfg) for _ in slots]
+
+    def close(y, y_ref):
+        return np.abs(np64(y) - np64(y_ref)).max() <= 3e-2 * np.abs(np64(y_ref)).max()
+
+    for s, n, c in zip(slots, lens, hf_caches):
+        x = torch.randn(1, n, 1024, generator=gen).to(torch.bfloat16).float()
+        pools.bind(torch.tensor([s]), is_prefill=True)
+        with torch.no_grad():
+            y = gated_delta_net_forward(layer, x.to(DEV, torch.bfloat16), cache_params=cache)
+            assert close(y, ref(x, cache_params=c))
+    assert not calls
+    for _ in range(3):
+        x = torch.randn(3, 1, 1024, generator=gen).to(torch.bfloat16).float()
+        pools.bind(torch.tensor(slots), is_prefill=False)
+        with torch.no_grad():
+            y = gated_delta_net_forward(layer, x.to(DEV, torch.bfloat16), cache_params=cache)
+            for r, c in enumerate(hf_caches):
+                assert close(y[r:r + 1], ref(x[r:r + 1], cache_params=c)), r
+    assert len(calls) == 3
+    conv_pool, rec_pool = pools.layer(0)
+    for s, c in zip(slots, hf_caches):
+        assert gdn.state_rel_err(np64(rec_pool[s])[None], np64(c.layers[0].recurrent_states[0])) < 1e-2
+        assert np.abs(np64(conv_pool[s])[None] - np64(c.layers[0].conv_states[0])).max() < 2e-2

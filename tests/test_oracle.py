@@ -290,3 +290,66 @@ def test_gates_closed_forms():
     a = np.linspace(-5, 5, 11)
     g_line = gdn.gdn_gates(a, np.zeros_like(a), np.zeros(1), np.zeros(1))[0]
     assert np.all(np.diff(g_line) < 0) and np.all(g_line < 0)   # decay strengthens with a
+
+
+# ------------------------------------------------------ decode in-projection
+
+def test_round_bf16_matches_torch():
+    import torch
+    x = np.random.default_rng(61).standard_normal(4096) * 10.0 ** np.random.default_rng(62).integers(-6, 6, 4096)
+    ref = torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16).double().numpy()
+    assert np.array_equal(conv.round_bf16(x.astype(np.float32)), ref)
+
+
+def test_in_proj_decode_matches_hf_layer_on_cpu():
+    """The decode input side of HF's own module (its four projections in
+    bf16 and its torch causal_conv1d_update) on bf16 weights and inputs."""
+    import torch
+    from transformers.models.qwen3_5_moe import modeling_qwen3_5_moe as hf
+    from transformers.models.qwen3_5_moe.configuration_qwen3_5_moe import Qwen3_5MoeTextConfig
+    cfg = Qwen3_5MoeTextConfig(hidden_size=64, num_hidden_layers=1, layer_types=["linear_attention"],
+                               linear_num_key_heads=2, linear_num_value_heads=4, linear_key_head_dim=16,
+                               linear_value_head_dim=16, linear_conv_kernel_dim=4)
+    torch.manual_seed(63)
+    layer = hf.Qwen3_5MoeGatedDeltaNet(cfg, layer_idx=0).eval().to(torch.bfloat16)
+    x = torch.randn(3, 64).to(torch.bfloat16)
+    c = layer.conv1d.weight.shape[0]
+    st = torch.randn(3, c, 4).to(torch.bfloat16)
+    cw = layer.conv1d.weight.squeeze(1)
+    with torch.no_grad():
+        qkv = layer.in_proj_qkv(x)
+        hf_st = st.clone()
+        y_hf = hf.causal_conv1d_update(qkv[:, :, None], hf_st, cw, None, "silu")[:, :, 0]
+        z_hf, b_hf, a_hf = layer.in_proj_z(x), layer.in_proj_b(x), layer.in_proj_a(x)
+    f = lambda t: t.detach().double().numpy()
+    y, z, b, a, new_st = conv.in_proj_decode(f(x), f(layer.in_proj_qkv.weight), f(layer.in_proj_z.weight),
+                                             f(layer.in_proj_b.weight), f(layer.in_proj_a.weight), f(cw), f(st))
+    # HF runs in bf16 (fp32 sums, one rounding per op): allow two bf16 ulps of
+    # the terms' magnitudes, the projection's ulp carried through the last tap
+    ulp = 2.0 ** -7
+    terms = np.abs(f(cw))[None, :, :3] * np.abs(f(st))[:, :, 1:]
+    y_scale = terms.sum(-1) + np.abs(f(cw))[None, :, 3] * np.abs(f(qkv))
+    assert (np.abs(y - f(y_hf)) <= 2 * ulp * y_scale + 1e-6).all()
+    for got, ref in ((z, z_hf), (b, b_hf), (a, a_hf)):
+        assert (np.abs(got - f(ref)) <= ulp * np.abs(f(ref)) + 1e-3).all()
+    # the new window: the three shifted taps exactly, then the bf16 projection
+    assert np.array_equal(new_st[:, :, :3], f(st)[:, :, 1:])
+    assert (np.abs(new_st[:, :, 3] - f(hf_st)[:, :, 3]) <= ulp * np.abs(f(hf_st)[:, :, 3])).all()
+
+
+def test_in_proj_decode_is_the_matmul_then_the_conv_update():
+    """Brute force on tiny shapes: every output entry as an explicit sum."""
+    rng = np.random.default_rng(64)
+    m, k = 2, 8
+    x, wq, wz, wb, wa = (rng.standard_normal(s) for s in ((m, k), (4, k), (3, k), (2, k), (2, k)))
+    cw, st = rng.standard_normal((4, 4)), rng.standard_normal((m, 4, 4))
+    y, z, b, a, new_st = conv.in_proj_decode(x, wq, wz, wb, wa, cw, st, activation=None)
+    for r in range(m):
+        for c in range(4):
+            p = conv.round_bf16(sum(x[r, i] * wq[c, i] for i in range(k)))
+            ref = sum(cw[c, j] * st[r, c, j + 1] for j in range(3)) + cw[c, 3] * p
+            assert abs(y[r, c] - ref) < 1e-12
+            assert list(new_st[r, c]) == [st[r, c, 1], st[r, c, 2], st[r, c, 3], p]
+        assert np.allclose(z[r], [sum(x[r, i] * wz[j, i] for i in range(k)) for j in range(3)], atol=1e-12)
+        assert np.allclose(b[r], [sum(x[r, i] * wb[j, i] for i in range(k)) for j in range(2)], atol=1e-12)
+        assert np.allclose(a[r], [sum(x[r, i] * wa[j, i] for i in range(k)) for j in range(2)], atol=1e-12)
