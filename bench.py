@@ -22,6 +22,12 @@ The JSON line also carries
   layer_glue    the GDN layer glue around the prefill core at configuration 2's
                 shape: HF's torch glue (gates, q/k repeat, RMSNormGated) vs
                 the fused kernels, and the gated-norm kernel's HBM rate;
+  decode_in_proj a decode step's input side at B=64 (row f-4): the four GDN
+                input projections and the conv window update as one kernel
+                (gdn_in_proj_decode) vs hipBLASLt projections + the conv
+                update kernel, both replayed from HIP graphs over 6 weight
+                sets (304 MB, past the Infinity Cache), with the fused
+                kernel's HBM rate;
   cpu_baseline  the CPU oracle (numpy fp32, sequences split over the host's
                 cores) on a bounded sample of the same decode workload.
 """
@@ -60,6 +66,7 @@ def parse():
                     help="skip the prefill timing with q/k repeated to 32 heads")
     ap.add_argument("--no-layer-glue", action="store_true",
                     help="skip the fused vs torch layer-glue timing (gates, q/k repeat, gated norm)")
+    ap.add_argument("--no-in-proj", action="store_true", help="skip the decode input-projection measurement")
     ap.add_argument("--pools", type=int, default=4, help="rotating decode state pools")
     ap.add_argument("--prefill-only", action="store_true",
                     help="time only the configuration 2 prefill (for counter profiles; prints no headline value)")
@@ -285,6 +292,56 @@ def cpu_baseline(budget_s=12.0):
                       f"the numpy fp32 oracle, sequences split over {n} threads; {per * 1e3:.1f} ms/step"}
 
 
+def bench_in_proj(torch, sets=6, reps=4):
+    """Row f-4 at the decode batch (64 rows, hidden 2048, Qwen3.5-MoE GDN
+    shapes): the fused input-projection kernel against the unfused path HF's
+    layer takes (four nn.Linear on hipBLASLt, then causal_conv1d_update on
+    the slot pool).  Each path is captured once per weight set into one
+    HIP graph; the graph is replayed ``reps`` times between two events."""
+    import torch.nn.functional as F
+    from engine.kernels import causal_conv1d_update, gdn_in_proj_decode
+
+    dev = torch.device("cuda", 0)
+    m, k, n = 64, 2048, (8192, 4096, 32, 32)
+    gen = torch.Generator().manual_seed(51)
+    wsets = [[(0.02 * torch.randn(c, k, generator=gen)).to(dev, torch.bfloat16) for c in n] for _ in range(sets)]
+    cw = (0.5 * torch.randn(n[0], 4, generator=gen)).to(dev, torch.bfloat16)
+    pool = torch.randn(128, n[0], 4, generator=gen).to(dev, torch.bfloat16)
+    slots = torch.randperm(128, generator=gen)[:m].to(dev)
+    x = torch.randn(m, k, generator=gen).to(dev, torch.bfloat16)
+
+    def fused(ws):
+        return gdn_in_proj_decode(x, *ws, cw, None, pool, slots)
+
+    def unfused(ws):
+        qkv, z, b, a = (F.linear(x, w) for w in ws)
+        return causal_conv1d_update(qkv[:, :, None], pool, cw, None, "silu", conv_state_indices=slots), z, b, a
+
+    def graph_us(fn):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for ws in wsets:
+                fn(ws)
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for ws in wsets:
+                fn(ws)
+        return _time(torch, g.replay, reps, warmup=2) / sets * 1e6
+
+    t_fused, t_unfused = graph_us(fused), graph_us(unfused)
+    t_eager = _time(torch, lambda: fused(wsets[0]), 50) * 1e6
+    wbytes = sum(c for c in n) * k * 2
+    byts = wbytes + m * k * 2 + m * sum(n) * 2 + 2 * m * n[0] * 8  # weights, x, outputs, windows read + written
+    return {"config": "B=64 rows, hidden 2048 -> qkv 8192 (conv width 4, 128-slot bf16 pool) / z 4096 / b 32 / a 32, bf16",
+            "fused_us": t_fused, "unfused_hipblaslt_us": t_unfused, "speedup": t_unfused / t_fused,
+            "fused_eager_us": t_eager,
+            "roofline": {"bound": "hbm", "achieved": byts / t_fused / 1e3, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                         "frac": byts / (t_fused * 1e-6) / HBM_PEAK, "bytes_per_launch": byts,
+                         "kernel": "gdn::in_proj_decode_kernel<16>"}}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -333,6 +390,8 @@ def main():
             out["prefill_qk_repeated"] = bench_prefill(torch, repeat_qk=True)
         if not args.no_layer_glue:
             out["layer_glue"] = bench_layer_glue(torch)
+    if not args.no_in_proj:
+        out["decode_in_proj"] = bench_in_proj(torch)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)
