@@ -28,6 +28,12 @@ The JSON line also carries
                 update kernel, both replayed from HIP graphs over 6 weight
                 sets (304 MB, past the Infinity Cache), with the fused
                 kernel's HBM rate;
+  layer_decode  one whole GDN layer decode step at B=64 (rows f-2, f-4 and the
+                core together): ``gated_delta_net_forward`` on engine slot
+                pools, four layers with their own weights and 256 MiB state
+                pools replayed from one HIP graph; the same with the unfused
+                input side; and the reference cache's per-step gather + scatter
+                of the same slots, which the pools remove;
   cpu_baseline  the CPU oracle (numpy fp32, sequences split over the host's
                 cores) on a bounded sample of the same decode workload.
 """
@@ -67,6 +73,7 @@ def parse():
     ap.add_argument("--no-layer-glue", action="store_true",
                     help="skip the fused vs torch layer-glue timing (gates, q/k repeat, gated norm)")
     ap.add_argument("--no-in-proj", action="store_true", help="skip the decode input-projection measurement")
+    ap.add_argument("--no-layer-decode", action="store_true", help="skip the whole-layer decode measurement")
     ap.add_argument("--pools", type=int, default=4, help="rotating decode state pools")
     ap.add_argument("--prefill-only", action="store_true",
                     help="time only the configuration 2 prefill (for counter profiles; prints no headline value)")
@@ -342,6 +349,81 @@ def bench_in_proj(torch, sets=6, reps=4):
                          "kernel": "gdn::in_proj_decode_kernel<16>"}}
 
 
+def bench_layer_decode(torch, layers=4, reps=5):
+    """One GDN layer decode step at B=64 with Qwen3.5-MoE layer shapes (hidden
+    2048, 16 k-heads, 32 v-heads of 128, conv width 4; random bf16 weights):
+    HF's ``Qwen3_5MoeGatedDeltaNet`` with ``gated_delta_net_forward`` on
+    engine slot pools (128 slots, 64 bound).  ``layers`` such layers, each
+    with its own weights and pools (256 MiB recurrent pool each, so neither
+    the weights nor the states stay in the 256 MB Infinity Cache), one step
+    of each captured into one HIP graph; the graph is replayed ``reps``
+    times.  Also: the same steps with the unfused input side (hipBLASLt
+    projections + conv update kernel), and the gather + scatter the
+    reference cache runs around every step for the same slots
+    (``index_select`` of both pools before, ``index_copy_`` after,
+    engine/runtime/kv_cache.py:189-208)."""
+    import types
+    from unittest import mock
+    from transformers.models.qwen3_5_moe import modeling_qwen3_5_moe as hf
+    from transformers.models.qwen3_5_moe.configuration_qwen3_5_moe import Qwen3_5MoeTextConfig
+    from engine.kernels import gated_delta_net_forward, gdn_layer
+    from engine.runtime import GDNSlotPools
+
+    dev = torch.device("cuda", 0)
+    cfg = Qwen3_5MoeTextConfig(hidden_size=2048, num_hidden_layers=layers, layer_types=["linear_attention"] * layers,
+                               linear_num_key_heads=16, linear_num_value_heads=32, linear_key_head_dim=128,
+                               linear_value_head_dim=128, linear_conv_kernel_dim=4, rms_norm_eps=1e-6)
+    torch.manual_seed(61)
+    mods = [hf.Qwen3_5MoeGatedDeltaNet(cfg, layer_idx=i).eval().to(dev, torch.bfloat16) for i in range(layers)]
+    pools = GDNSlotPools.allocate(range(layers), 128, conv_dim=8192, num_v_heads=32, device=dev, max_batch=64)
+    gen = torch.Generator().manual_seed(62)
+    torch.cuda.manual_seed(62)
+    for i in range(layers):
+        conv, rec = pools.layer(i)
+        rec.normal_(0.0, 0.1)
+        conv.normal_(0.0, 1.0)
+    slots = torch.randperm(128, generator=gen)[:64]
+    x = torch.randn(64, 1, 2048, generator=gen).to(dev, torch.bfloat16)
+    cache = types.SimpleNamespace(gdn_slot_pools=pools)
+    pools.bind(slots, is_prefill=False)
+    dslots = slots.to(dev)
+
+    def steps():
+        with torch.no_grad():
+            for m in mods:
+                gated_delta_net_forward(m, x, cache_params=cache)
+
+    def gather_scatter():
+        for i in range(layers):
+            conv, rec = pools.layer(i)
+            c, r = conv.index_select(0, dslots), rec.index_select(0, dslots)
+            conv.index_copy_(0, dslots, c)
+            rec.index_copy_(0, dslots, r)
+
+    def graph_us(fn):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        return _time(torch, g.replay, reps, warmup=2) / layers * 1e6
+
+    t_fused = graph_us(steps)
+    with mock.patch.object(gdn_layer, "_fused_decode_fits", lambda *a, **k: False):
+        t_unfused = graph_us(steps)
+    t_gs = graph_us(gather_scatter)
+    return {"config": "one GDN layer decode step, B=64 of 128 slots, hidden 2048, Hk=16 Hv=32 d=128, conv 4, "
+                      "bf16 weights (random), fp32 state pools; 4 layers per graph, own weights and pools",
+            "step_us": t_fused, "tok_per_s": 64 / (t_fused * 1e-6),
+            "step_unfused_input_us": t_unfused,
+            "reference_cache_gather_scatter_us": t_gs,
+            "note": "step = fused input side + recurrence on the pool + gated norm + out_proj (hipBLASLt); "
+                    "the reference runs its gather + scatter in addition to the layer step"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -392,6 +474,8 @@ def main():
             out["layer_glue"] = bench_layer_glue(torch)
     if not args.no_in_proj:
         out["decode_in_proj"] = bench_in_proj(torch)
+    if not args.no_layer_decode:
+        out["layer_decode"] = bench_layer_decode(torch)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

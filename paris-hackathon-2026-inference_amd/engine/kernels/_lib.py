@@ -183,7 +183,8 @@ def token_major(x: torch.Tensor, what: str) -> tuple[torch.Tensor, int]:
     if x.dim() != 4:
         raise ValueError(f"{what}: expected [B, T, H, D], got shape {tuple(x.shape)}")
     b, t, h, d = x.shape
-    st = x.stride(1) if t > 1 else h * d
+    # token b*T + t: with one token per sequence the batch stride is the token stride
+    st = x.stride(1) if t > 1 else (x.stride(0) if b > 1 else h * d)
     ok = (x.stride(3) == 1 and (h == 1 or x.stride(2) == d) and st >= h * d and st % 8 == 0
           and (b == 1 or x.stride(0) == t * st) and x.storage_offset() % 8 == 0)
     if not ok:
@@ -198,11 +199,27 @@ def per_token(x: torch.Tensor, b: int, t: int, h: int, what: str) -> tuple[torch
     contiguous and batches evenly spaced, otherwise a contiguous copy is made."""
     if tuple(x.shape) != (b, t, h):
         raise ValueError(f"{what}: expected shape {(b, t, h)}, got {tuple(x.shape)}")
-    st = x.stride(1) if t > 1 else h
+    st = x.stride(1) if t > 1 else (x.stride(0) if b > 1 else h)
     if not (x.stride(2) == 1 or h == 1) or st < h or (b > 1 and x.stride(0) != t * st):
         x = x.contiguous()
         st = h
     return x, st
+
+
+def f32_vector(t: torch.Tensor) -> torch.Tensor:
+    """``t`` as a contiguous fp32 vector.  A conversion is kept on the tensor
+    itself (the layer's ``A_log``, ``dt_bias`` parameters) and redone when it
+    is modified or replaced, so a layer step launches no conversion kernel
+    (and a captured graph records none) once the parameter was seen."""
+    if t.dtype == torch.float32 and t.is_contiguous():
+        return t.detach().reshape(-1)
+    key = (t.data_ptr(), t._version, t.dtype, t.numel(), t.device)
+    hit = getattr(t, "_gdn_f32", None)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    out = t.detach().to(torch.float32).reshape(-1).contiguous()
+    t._gdn_f32 = (key, out)
+    return out
 
 
 def rows_of(t: Optional[torch.Tensor]) -> int:

@@ -110,8 +110,7 @@ def chunk_gated_delta_rule_from_projections(
     bx, bst = _lib.per_token(b, bsz, t, hv, "b")
     if ast != bst:
         ax, bx, ast = ax.contiguous(), bx.contiguous(), hv
-    alog = A_log.detach().to(torch.float32).reshape(-1).contiguous()
-    dtb = dt_bias.detach().to(torch.float32).reshape(-1).contiguous()
+    alog, dtb = _lib.f32_vector(A_log), _lib.f32_vector(dt_bias)
     if alog.numel() != hv or dtb.numel() != hv:
         raise ValueError(f"A_log / dt_bias must have {hv} entries")
     gates = ("gdn_chunk_fwd_gated", [_lib.ptr(ax), _lib.ptr(bx), _lib.dtype_code(ax, "a"), ast,
