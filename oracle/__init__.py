@@ -11,6 +11,7 @@ Modules
 -------
 gdn   recurrence, chunk-64 algorithm, l2norm, varlen and spec-verify helpers
 conv  causal depthwise conv1d (prefill fn and single-step update)
+proj  the decode step's input projections + conv update
 
 Pinning (how each function is known to be right, independent of itself)
 ------------------------------------------------------------------------
@@ -31,4 +32,7 @@ Pinning (how each function is known to be right, independent of itself)
   ``numpy.convolve`` per channel; update == last column of fn.
 * varlen and spec-verify helpers: defined by composition of the pinned
   functions above (per-sequence loop; snapshot[t] == state after t+1 tokens).
+* ``proj.round_bf16``: torch's own fp32 -> bf16 conversion.
+  ``proj.in_proj_decode``: HF's module on the CPU (its four nn.Linear in
+  bf16 and its causal_conv1d_update) and brute-force sums on tiny shapes.
 """

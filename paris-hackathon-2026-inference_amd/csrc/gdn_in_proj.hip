@@ -41,12 +41,27 @@ typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
-constexpr int IP_CG = 4;                 // column groups of 16
-constexpr int IP_KQ = 4;                 // quarters of K
-constexpr int IP_WAVES = IP_CG * IP_KQ;  // 16
-constexpr int IP_COLS = 16 * IP_CG;      // output columns per workgroup
-constexpr int IP_ROWS = 64;              // hidden rows per workgroup (4 row tiles)
-constexpr int IP_OOB = 0x40000000;       // buffer offset past every conv pool: loads read 0, nothing stored
+constexpr int IP_WAVES = 16;         // waves per workgroup
+constexpr int IP_ROWS = 64;          // hidden rows per workgroup (4 row tiles)
+constexpr int IP_OOB = 0x40000000;   // buffer offset past every conv pool: loads read 0, nothing stored
+
+// Workgroup shape: CG column groups of 16 x KQ parts of K (CG KQ = 16
+// waves); a wave holds KS k-steps (of 32) of weights; the hidden rows reach
+// LDS in NPH phases, each SP = KS / NPH k-steps of every part: per part 64
+// rows of CH = 4 SP chunks of 8 elements (128 KiB at most in all).
+template <int CG_, int KQ_, int KS_, int NPH_>
+struct ProjShape {
+  static constexpr int CG = CG_, KQ = KQ_, KS = KS_, NPH = NPH_;
+  static constexpr int COLS = 16 * CG;
+  static constexpr int SP = KS / NPH, CH = 4 * SP, RPI = 64 / CH;
+  static constexpr int KPART = 32 * KS;
+  static constexpr int DMA_PER_WAVE = KQ * CH / IP_WAVES;
+  static constexpr int LDS_BLOCKS = KQ * 64 * CH;  // 16-byte entries
+  static_assert(CG * KQ == IP_WAVES && KS % NPH == 0 && 64 % CH == 0 && (KQ * CH) % IP_WAVES == 0, "shape");
+  static_assert(LDS_BLOCKS * 16 <= 128 * 1024 && KQ * CG * 4 * 64 <= LDS_BLOCKS, "LDS");
+};
+using InProjShape2048 = ProjShape<4, 4, 16, 2>;  // input projections, K = 2048
+using InProjShape1024 = ProjShape<4, 4, 8, 2>;   // input projections, K = 1024
 
 struct InProjArgs {
   const uint16_t *x;  // [M, K] bf16, row stride xs elements
@@ -74,7 +89,7 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   return static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
 }
 
-// This wave's weights, KS k-steps of its quarter: lane (r, g) of k-step s
+// This wave's weights, KS k-steps of its part: lane (r, g) of k-step s
 // holds W[col + r][k0 + 32 s + 8 g .. + 8].  Rows past the matrix read as zero.
 template <int KS>
 __device__ __forceinline__ void load_w(u32x4_t (&wr)[KS], __amdgpu_buffer_rsrc_t rw, int k0, int K, int lane) {
@@ -83,54 +98,98 @@ __device__ __forceinline__ void load_w(u32x4_t (&wr)[KS], __amdgpu_buffer_rsrc_t
   for (int s = 0; s < KS; ++s) wr[s] = __builtin_amdgcn_raw_buffer_load_b128(rw, voff, (k0 + 32 * s) * 2, 0);
 }
 
-// Half h of every quarter's hidden rows into LDS by DMA.  Per quarter q the
-// half is CH = 2 KS chunks of 8 elements per row, at k = q K/4 + 256 h ...
-// (K/8 per half); LDS holds it row-major, 64 rows of CH chunks, chunk p of
-// row r at position p ^ (r % CH) (so that the 16 rows an MFMA operand read
-// touches fall in 16 different bank groups).  One DMA instruction fills 64
-// consecutive positions, i.e. 64 / CH whole rows, each lane fetching the
-// chunk its position holds: contiguous global reads, 1 KiB per instruction.
-// Wave w copies instructions w, w + 16, ...  Rows past M read as zero.
-template <int KS>
-__device__ __forceinline__ void dma_x(u32x4_t *xl, __amdgpu_buffer_rsrc_t rx, int64_t xs, int K, int h, int wave,
+// Phase h of every part's hidden rows into LDS by DMA: part q's k-steps
+// h SP .. h SP + SP - 1, i.e. CH chunks of 8 elements per row.  LDS holds a
+// part row-major, 64 rows of CH chunks, chunk p of row r at position
+// p ^ (r % CH) (so that the 16 rows an MFMA operand read touches fall in
+// 16 different bank groups).  One DMA instruction fills 64 consecutive
+// positions, i.e. 64 / CH whole rows, each lane fetching the chunk its
+// position holds: contiguous global reads, 1 KiB per instruction.  Wave w
+// copies instructions w, w + 16, ...  Rows past M read as zero.
+template <class S>
+__device__ __forceinline__ void dma_x(u32x4_t *xl, const uint16_t *xbase, int xbytes, int64_t xs, int h, int wave,
                                       int lane) {
-  constexpr int CH = 2 * KS, RPI = 64 / CH;  // chunks per row, rows per instruction
+  const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(xbase), 0, xbytes, BUF_DWORD3);
 #pragma unroll
-  for (int i = 0; i < IP_KQ * CH / IP_WAVES; ++i) {
-    const int j = wave + IP_WAVES * i;  // quarter j / CH, rows RPI (j % CH) ..
-    const int q = j / CH;
-    const int r = RPI * (j % CH) + lane / CH, pos = lane % CH;
-    const int voff = static_cast<int>((r * xs + 8 * (pos ^ (r % CH))) * 2);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, xl + j * 64, 16, voff, (q * (K / IP_KQ) + h * (K / 8)) * 2, 0, 0);
+  for (int i = 0; i < S::DMA_PER_WAVE; ++i) {
+    const int j = wave + IP_WAVES * i;  // part j / CH, rows RPI (j % CH) ..
+    const int q = j / S::CH;
+    const int r = S::RPI * (j % S::CH) + lane / S::CH, pos = lane % S::CH;
+    const int voff = static_cast<int>((r * xs + 8 * (pos ^ (r % S::CH))) * 2);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, xl + j * 64, 16, voff, (q * S::KPART + h * 32 * S::SP) * 2, 0, 0);
   }
 }
 
-// Half h of this wave's quarter against its staged rows (all four row tiles):
+// Phase PH of this wave's part against its staged rows (all four row tiles):
 // B operand of row tile t, k-step s at lane (c, g) = row 16 t + c, chunk 4 s + g.
-template <int KS, int HALF>
-__device__ __forceinline__ void half_mfma(f32x4_t (&acc)[4], const u32x4_t (&wr)[KS], const u32x4_t *xq, int lane) {
-  constexpr int H = KS / 2, CH = 2 * KS;
+template <class S, int PH>
+__device__ __forceinline__ void phase_mfma(f32x4_t (&acc)[4], const u32x4_t (&wr)[S::KS], const u32x4_t *xq,
+                                           int lane) {
   const int c = lane & 15, g = lane >> 4;
 #pragma unroll
-  for (int s = 0; s < H; ++s)
+  for (int s = 0; s < S::SP; ++s)
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int r = 16 * t + c;
-      acc[t] = mfma16(wr[HALF * H + s], xq[r * CH + ((4 * s + g) ^ (r % CH))], acc[t]);
+      acc[t] = mfma16(wr[PH * S::SP + s], xq[r * S::CH + ((4 * s + g) ^ (r % S::CH))], acc[t]);
     }
 }
 
 // s_waitcnt operand: vmcnt <= n, lgkmcnt and expcnt unconstrained
 constexpr int ip_vmcnt(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 
-// KS = K / 128 k-steps per quarter (K = 1024, 2048).
-template <int KS>
+// After phase 0's copies and the weights were issued (and POST more loads
+// after them): the phases, then the parts' partial sums added in LDS in part
+// order.  Returns, for waves of part kq < 4, row tile kq of their column
+// group (rows 16 kq + c, columns 4 g .. 4 g + 3 of the group at lane (c, g)).
+// copy(h) issues phase h's copies (the kernel's dma_x on its LDS buffer).
+template <class S, int POST, class Copy>
+__device__ __forceinline__ f32x4_t proj_phases(u32x4_t *xl, const u32x4_t (&wr)[S::KS], const Copy &copy, int wave,
+                                               int lane) {
+  const int cg = wave % S::CG, kq = wave / S::CG;
+  f32x4_t acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const u32x4_t *xq = xl + kq * (64 * S::CH);
+  __builtin_amdgcn_s_waitcnt(ip_vmcnt(S::KS + POST));  // this wave's copies landed (the weights may still fly)
+  __syncthreads();
+  phase_mfma<S, 0>(acc, wr, xq, lane);
+#pragma unroll
+  for (int h = 1; h < S::NPH; ++h) {
+    __syncthreads();  // the previous phase is consumed: the next into the same buffer
+    copy(h);
+    __builtin_amdgcn_s_waitcnt(ip_vmcnt(0));
+    __syncthreads();
+    if (h == 1) phase_mfma<S, 1>(acc, wr, xq, lane);
+    if constexpr (S::NPH > 2) {
+      if (h == 2) phase_mfma<S, 2>(acc, wr, xq, lane);
+      if (h == 3) phase_mfma<S, 3>(acc, wr, xq, lane);
+    }
+  }
+  // part partials through LDS (the rows' buffer, once every wave is done with it)
+  __syncthreads();
+  f32x4_t *red = reinterpret_cast<f32x4_t *>(xl);  // [part][column group][row tile][lane]
+#pragma unroll
+  for (int t = 0; t < 4; ++t) red[((kq * S::CG + cg) * 4 + t) * 64 + lane] = acc[t];
+  __syncthreads();
+  f32x4_t o = {0.f, 0.f, 0.f, 0.f};
+  if (kq < 4) {
+    o = red[(cg * 4 + kq) * 64 + lane];
+#pragma unroll
+    for (int q = 1; q < S::KQ; ++q) o += red[((q * S::CG + cg) * 4 + kq) * 64 + lane];
+  }
+  return o;
+}
+
+// S: InProjShape2048 or InProjShape1024.
+template <class S>
 __global__ __launch_bounds__(64 * IP_WAVES) void in_proj_decode_kernel(InProjArgs a) {
-  __shared__ u32x4_t xl[IP_KQ * 4 * (KS / 2) * 64];  // 64 rows of half of K: 128 KiB at K = 2048
+  __shared__ u32x4_t xl[S::LDS_BLOCKS];  // one phase of the hidden rows: 128 KiB at K = 2048
+  constexpr int KS = S::KS;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int cg = wave & (IP_CG - 1), kq = wave / IP_CG;
+  const int cg = wave % S::CG, kq = wave / S::CG;
   const int m0 = blockIdx.y * IP_ROWS;
   const int mb = min(IP_ROWS, a.M - m0);
 
@@ -139,10 +198,10 @@ __global__ __launch_bounds__(64 * IP_WAVES) void in_proj_decode_kernel(InProjArg
   const int bid = blockIdx.x;
   if (bid < a.blocks_qkv) {
     mat = 0;
-    col = bid * IP_COLS + 16 * cg;
+    col = bid * S::COLS + 16 * cg;
   } else if (bid < a.blocks_qkv + a.blocks_z) {
     mat = 1;
-    col = (bid - a.blocks_qkv) * IP_COLS + 16 * cg;
+    col = (bid - a.blocks_qkv) * S::COLS + 16 * cg;
   } else {
     mat = 2 + (cg >> 1);
     col = 16 * (cg & 1);
@@ -155,8 +214,8 @@ __global__ __launch_bounds__(64 * IP_WAVES) void in_proj_decode_kernel(InProjArg
   const int live = __builtin_amdgcn_readfirstlane(max(0, min(16, nmat - col)));  // columns of this wave in its matrix
   const auto rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(wmat) + static_cast<int64_t>(col) * a.K, 0,
                                                     live * a.K * 2, BUF_DWORD3);
-  const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.x) + static_cast<int64_t>(m0) * a.xs, 0,
-                                                    static_cast<int>(((mb - 1) * a.xs + a.K) * 2), BUF_DWORD3);
+  const uint16_t *xbase = a.x + static_cast<int64_t>(m0) * a.xs;
+  const int xbytes = static_cast<int>(((mb - 1) * a.xs + a.K) * 2);
   const int c = lane & 15, g = lane >> 4;
   const int n = col + 4 * g;
   const int me = m0 + 16 * kq + c;  // the row this lane finishes
@@ -178,10 +237,10 @@ __global__ __launch_bounds__(64 * IP_WAVES) void in_proj_decode_kernel(InProjArg
   const u32x4_t w23 = __builtin_amdgcn_raw_buffer_load_b128(rc, n * 8, 16, 0);
   const uint64_t bias4 = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(rb, n * 2, 0, 0));
   __builtin_amdgcn_sched_barrier(0);
-  dma_x<KS>(xl, rx, a.xs, a.K, 0, wave, lane);
+  dma_x<S>(xl, xbase, xbytes, a.xs, 0, wave, lane);
   __builtin_amdgcn_sched_barrier(0);
   u32x4_t wr[KS];
-  load_w<KS>(wr, rw, kq * (a.K / IP_KQ), a.K, lane);
+  load_w<KS>(wr, rw, kq * S::KPART, a.K, lane);
   __builtin_amdgcn_sched_barrier(0);
   const int64_t id = a.idx ? static_cast<int64_t>(id_raw) : me;  // pool_row's rule
   const int woff = conv && me < a.M && id >= 0 && id < a.rows ? static_cast<int>((id * a.n[0] + n) * 8) : IP_OOB;
@@ -190,28 +249,8 @@ __global__ __launch_bounds__(64 * IP_WAVES) void in_proj_decode_kernel(InProjArg
   win[1] = __builtin_amdgcn_raw_buffer_load_b128(rp, woff, 16, 0);
   __builtin_amdgcn_sched_barrier(0);
 
-  f32x4_t acc[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const u32x4_t *xq = xl + kq * (64 * 2 * KS);
-  __builtin_amdgcn_s_waitcnt(ip_vmcnt(KS + 2));  // this wave's copies landed (weights, window may still fly)
-  __syncthreads();
-  half_mfma<KS, 0>(acc, wr, xq, lane);
-  __syncthreads();  // the first halves are consumed: the second into the same buffer
-  dma_x<KS>(xl, rx, a.xs, a.K, 1, wave, lane);
-  __builtin_amdgcn_s_waitcnt(ip_vmcnt(0));
-  __syncthreads();
-  half_mfma<KS, 1>(acc, wr, xq, lane);
-
-  // quarter partials through LDS (the rows' buffer, once every wave is done with it)
-  __syncthreads();
-  f32x4_t *red = reinterpret_cast<f32x4_t *>(xl);  // [quarter][column group][row tile][lane]: 64 KiB
-#pragma unroll
-  for (int t = 0; t < 4; ++t) red[((kq * IP_CG + cg) * 4 + t) * 64 + lane] = acc[t];
-  __syncthreads();
-  f32x4_t o = red[((0 * IP_CG + cg) * 4 + kq) * 64 + lane];
-#pragma unroll
-  for (int q = 1; q < IP_KQ; ++q) o += red[((q * IP_CG + cg) * 4 + kq) * 64 + lane];
+  const f32x4_t o = proj_phases<S, 2>(
+      xl, wr, [&](int h) { dma_x<S>(xl, xbase, xbytes, a.xs, h, wave, lane); }, wave, lane);
 
   // ---- epilogue of row tile kq: lane (c, g) holds row me, columns n .. n + 3
   if (4 * g >= live || me >= a.M) return;  // (live is a multiple of 4)
@@ -261,12 +300,12 @@ extern "C" int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w
   if (!x || !w_qkv || !w_z || !conv_w || !conv_pool || !y_qkv || !z || ((n_b > 0) && (!w_b || !b)) ||
       ((n_a > 0) && (!w_a || !a)))
     return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_in_proj_decode: null pointer argument");
-  if (M < 0 || n_qkv <= 0 || n_qkv % IP_COLS || n_z < 0 || n_z % IP_COLS || n_b < 0 || n_a < 0 || n_b % 4 ||
+  if (M < 0 || n_qkv <= 0 || n_qkv % InProjShape2048::COLS || n_z < 0 || n_z % InProjShape2048::COLS || n_b < 0 || n_a < 0 || n_b % 4 ||
       n_a % 4 || n_b > 32 || n_a > 32)
     return fail(GDN_ERR_UNSUPPORTED,
                 "gdn_in_proj_decode: need n_qkv and n_z multiples of %d, n_b and n_a multiples of 4 up to 32 "
                 "(got M=%d n=%d/%d/%d/%d)",
-                IP_COLS, M, n_qkv, n_z, n_b, n_a);
+                InProjShape2048::COLS, M, n_qkv, n_z, n_b, n_a);
   if (K != 1024 && K != 2048)
     return fail(GDN_ERR_UNSUPPORTED, "gdn_in_proj_decode: K=%d (built for 1024 and 2048)", K);
   if (x_stride < K || x_stride % 8)
@@ -301,8 +340,8 @@ extern "C" int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w
   args.n[1] = n_z;
   args.n[2] = n_b;
   args.n[3] = n_a;
-  args.blocks_qkv = n_qkv / IP_COLS;
-  args.blocks_z = n_z / IP_COLS;
+  args.blocks_qkv = n_qkv / InProjShape2048::COLS;
+  args.blocks_z = n_z / InProjShape2048::COLS;
   args.M = M;
   args.K = K;
   args.cw = static_cast<const uint16_t *>(conv_w);
@@ -319,8 +358,8 @@ extern "C" int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w
                   static_cast<unsigned>((M + IP_ROWS - 1) / IP_ROWS));
   const hipStream_t s = static_cast<hipStream_t>(stream);
   switch (K) {
-    case 1024: hipLaunchKernelGGL(in_proj_decode_kernel<8>, grid, dim3(64 * IP_WAVES), 0, s, args); break;
-    case 2048: hipLaunchKernelGGL(in_proj_decode_kernel<16>, grid, dim3(64 * IP_WAVES), 0, s, args); break;
+    case 1024: hipLaunchKernelGGL(in_proj_decode_kernel<InProjShape1024>, grid, dim3(64 * IP_WAVES), 0, s, args); break;
+    case 2048: hipLaunchKernelGGL(in_proj_decode_kernel<InProjShape2048>, grid, dim3(64 * IP_WAVES), 0, s, args); break;
     default: return fail(GDN_ERR_UNSUPPORTED, "gdn_in_proj_decode: K=%d unsupported", K);
   }
   return check_launch("gdn_in_proj_decode");

@@ -7,9 +7,10 @@ HF's GDN decode step (transformers modeling_qwen3_5_moe.py:443-461) runs
 does all of it in one HIP kernel (``gdn_in_proj_decode`` in
 include/gdn_capi.h): each weight row is read once from HBM, and the qkv
 projection goes through the conv window update in registers, so it is never
-written out before the conv.  Prefill keeps the library GEMMs (hipBLASLt via
-``torch.nn.functional.linear``): there the projections are compute-bound
-and the conv kernels read their output in place.
+written out before the conv.  Prefill and ``out_proj`` keep the
+library GEMMs (hipBLASLt via ``torch.nn.functional.linear``): there the
+projections are compute-bound and the conv kernels read their output in
+place.
 """
 from __future__ import annotations
 
@@ -84,8 +85,9 @@ def gdn_in_proj_decode(hidden: torch.Tensor, w_qkv: torch.Tensor, w_z: torch.Ten
     outs = [torch.empty((m, n), dtype=torch.bfloat16, device=dev) for n in (n_qkv, n_z, n_b, n_a)]
     lib = _lib.load()
     st = lib.gdn_in_proj_decode(
-        _lib.ptr(x), x.stride(0), *(_lib.ptr(w) for w in ws), m, k, n_qkv, n_z, n_b, n_a,
+        _lib.ptr(x), x.stride(0) if m > 1 else k, *(_lib.ptr(w) for w in ws), m, k, n_qkv, n_z, n_b, n_a,
         _lib.ptr(cw), _lib.ptr(cb), _lib.ptr(conv_state), _lib.ptr(idx), _lib.rows_of(conv_state),
         *(_lib.ptr(o) for o in outs), silu, _lib.stream_of(x))
     _lib.check(st, "gdn_in_proj_decode")
     return tuple(outs)
+

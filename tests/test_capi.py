@@ -194,3 +194,4 @@ def test_in_proj_decode_rejects_bad_arguments(lib):
     assert _inproj_call(lib, rows=3) == 1    # the pool does not cover row m without ids
     assert "pool rows" in lib.gdn_last_error_string().decode()
     assert _inproj_call(lib, m=0) == 0       # nothing to do, nothing launched
+

@@ -1,7 +1,7 @@
 """GPU parity of the fused decode input projections (gdn_in_proj_decode:
 four projections + causal conv update) with the CPU oracle, with the
 unfused GPU path, under graph capture, and inside the GDN layer against
-HF's module.
+HF's module (a small layer and one at the model's shapes).
 
 Tolerances: bf16 outputs |y - y_ref| <= 2e-2 * max(1, |y_ref|) (the north
 star's 2e-2 abs bound, widened to one bf16 ulp for |y| > 1); window taps
@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import conv
+from oracle import proj
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not torch.cuda.is_available(), reason="needs an MI355X")]
@@ -68,7 +68,7 @@ def test_matches_oracle_at_model_shape(m, bias):
     hist = np.zeros((m, NQKV, 4))
     live = s >= 0
     hist[live] = np64(pool0)[s[live]]
-    y_ref, z_ref, b_ref, a_ref, st_ref = conv.in_proj_decode(
+    y_ref, z_ref, b_ref, a_ref, st_ref = proj.in_proj_decode(
         np64(x), *(np64(w) for w in ws), np64(cw), hist, None if cb is None else np64(cb))
     assert bf16_close(y, y_ref)
     for got, ref in ((z, z_ref), (b, b_ref), (a, a_ref)):
@@ -112,7 +112,7 @@ def test_rows_without_ids_use_row_m_and_small_shapes():
     x = torch.randn(3, 1024, generator=gen).to(torch.bfloat16).to(DEV)
     pool0 = pool.clone()
     y, z, b, a = run_fused(x, ws, cw, cb, pool, None)
-    y_ref, z_ref, b_ref, a_ref, st_ref = conv.in_proj_decode(np64(x), *(np64(w) for w in ws), np64(cw), np64(pool0))
+    y_ref, z_ref, b_ref, a_ref, st_ref = proj.in_proj_decode(np64(x), *(np64(w) for w in ws), np64(cw), np64(pool0))
     assert b.shape == (3, 4) and a.shape == (3, 8)
     for got, ref in ((y, y_ref), (z, z_ref), (b, b_ref), (a, a_ref)):
         assert bf16_close(got, ref)
@@ -206,3 +206,53 @@ def test_layer_decode_takes_the_fused_kernel_and_matches_hf(monkeypatch):
     for s, c in zip(slots, hf_caches):
         assert gdn.state_rel_err(np64(rec_pool[s])[None], np64(c.layers[0].recurrent_states[0])) < 1e-2
         assert np.abs(np64(conv_pool[s])[None] - np64(c.layers[0].conv_states[0])).max() < 2e-2
+
+
+def test_layer_decode_at_model_shapes_takes_the_fused_kernel(monkeypatch):
+    """The Qwen3.5-MoE GDN layer (hidden 2048, 16 k-heads, 32 v-heads):
+    two sequences prefilled into slots, then batched decode steps that take
+    the fused input side, against HF's module per sequence."""
+    from transformers.cache_utils import DynamicCache
+    from transformers.models.qwen3_5_moe import modeling_qwen3_5_moe as hf
+    from transformers.models.qwen3_5_moe.configuration_qwen3_5_moe import Qwen3_5MoeTextConfig
+    from engine.kernels import gated_delta_net_forward, gdn_layer
+    from engine.runtime import GDNSlotPools
+
+    cfg = Qwen3_5MoeTextConfig(hidden_size=2048, num_hidden_layers=1, layer_types=["linear_attention"],
+                               linear_num_key_heads=16, linear_num_value_heads=32, linear_key_head_dim=128,
+                               linear_value_head_dim=128, linear_conv_kernel_dim=4, rms_norm_eps=1e-6)
+    torch.manual_seed(96)
+    ref = hf.Qwen3_5MoeGatedDeltaNet(cfg, layer_idx=0).eval()
+    with torch.no_grad():
+        for p in ref.parameters():
+            p.copy_(p.to(torch.bfloat16).float())
+    layer = hf.Qwen3_5MoeGatedDeltaNet(cfg, layer_idx=0).eval()
+    layer.load_state_dict(ref.state_dict())
+    layer = layer.to(DEV, torch.bfloat16)
+    calls = []
+    real = gdn_layer.gdn_in_proj_decode
+    monkeypatch.setattr(gdn_layer, "gdn_in_proj_decode", lambda *a, **k: calls.append(1) or real(*a, **k))
+
+    pools = GDNSlotPools.allocate([0], 4, conv_dim=2 * 16 * 128 + 32 * 128, num_v_heads=32, device=torch.device(DEV))
+    cache = types.SimpleNamespace(gdn_slot_pools=pools)
+    gen = torch.Generator().manual_seed(97)
+    slots, lens = [2, 0], [20, 9]
+    hf_caches = [DynamicCache(config=cfg) for _ in slots]
+
+    def close(y, y_ref):
+        return np.abs(np64(y) - np64(y_ref)).max() <= 3e-2 * np.abs(np64(y_ref)).max()
+
+    for s, n, c in zip(slots, lens, hf_caches):
+        x = torch.randn(1, n, 2048, generator=gen).to(torch.bfloat16).float()
+        pools.bind(torch.tensor([s]), is_prefill=True)
+        with torch.no_grad():
+            assert close(gated_delta_net_forward(layer, x.to(DEV, torch.bfloat16), cache_params=cache),
+                         ref(x, cache_params=c))
+    for step in range(2):
+        x = torch.randn(2, 1, 2048, generator=gen).to(torch.bfloat16).float()
+        pools.bind(torch.tensor(slots), is_prefill=False)
+        with torch.no_grad():
+            y = gated_delta_net_forward(layer, x.to(DEV, torch.bfloat16), cache_params=cache)
+            for r, c in enumerate(hf_caches):
+                assert close(y[r:r + 1], ref(x[r:r + 1], cache_params=c)), (step, r)
+    assert len(calls) == 2

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 from conftest import golden_case
-from oracle import conv, gdn
+from oracle import conv, gdn, proj
 
 RNG = np.random.default_rng(1234)
 
@@ -298,7 +298,7 @@ def test_round_bf16_matches_torch():
     import torch
     x = np.random.default_rng(61).standard_normal(4096) * 10.0 ** np.random.default_rng(62).integers(-6, 6, 4096)
     ref = torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16).double().numpy()
-    assert np.array_equal(conv.round_bf16(x.astype(np.float32)), ref)
+    assert np.array_equal(proj.round_bf16(x.astype(np.float32)), ref)
 
 
 def test_in_proj_decode_matches_hf_layer_on_cpu():
@@ -322,7 +322,7 @@ def test_in_proj_decode_matches_hf_layer_on_cpu():
         y_hf = hf.causal_conv1d_update(qkv[:, :, None], hf_st, cw, None, "silu")[:, :, 0]
         z_hf, b_hf, a_hf = layer.in_proj_z(x), layer.in_proj_b(x), layer.in_proj_a(x)
     f = lambda t: t.detach().double().numpy()
-    y, z, b, a, new_st = conv.in_proj_decode(f(x), f(layer.in_proj_qkv.weight), f(layer.in_proj_z.weight),
+    y, z, b, a, new_st = proj.in_proj_decode(f(x), f(layer.in_proj_qkv.weight), f(layer.in_proj_z.weight),
                                              f(layer.in_proj_b.weight), f(layer.in_proj_a.weight), f(cw), f(st))
     # HF runs in bf16 (fp32 sums, one rounding per op): allow two bf16 ulps of
     # the terms' magnitudes, the projection's ulp carried through the last tap
@@ -343,13 +343,14 @@ def test_in_proj_decode_is_the_matmul_then_the_conv_update():
     m, k = 2, 8
     x, wq, wz, wb, wa = (rng.standard_normal(s) for s in ((m, k), (4, k), (3, k), (2, k), (2, k)))
     cw, st = rng.standard_normal((4, 4)), rng.standard_normal((m, 4, 4))
-    y, z, b, a, new_st = conv.in_proj_decode(x, wq, wz, wb, wa, cw, st, activation=None)
+    y, z, b, a, new_st = proj.in_proj_decode(x, wq, wz, wb, wa, cw, st, activation=None)
     for r in range(m):
         for c in range(4):
-            p = conv.round_bf16(sum(x[r, i] * wq[c, i] for i in range(k)))
+            p = proj.round_bf16(sum(x[r, i] * wq[c, i] for i in range(k)))
             ref = sum(cw[c, j] * st[r, c, j + 1] for j in range(3)) + cw[c, 3] * p
             assert abs(y[r, c] - ref) < 1e-12
             assert list(new_st[r, c]) == [st[r, c, 1], st[r, c, 2], st[r, c, 3], p]
         assert np.allclose(z[r], [sum(x[r, i] * wz[j, i] for i in range(k)) for j in range(3)], atol=1e-12)
         assert np.allclose(b[r], [sum(x[r, i] * wb[j, i] for i in range(k)) for j in range(2)], atol=1e-12)
         assert np.allclose(a[r], [sum(x[r, i] * wa[j, i] for i in range(k)) for j in range(2)], atol=1e-12)
+
