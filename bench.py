@@ -9,7 +9,8 @@ are resident in HBM before timing.  Steps rotate over 4 disjoint 256 MiB
 state pools (1 GiB), so no step's state can be served by the 256 MB
 Infinity Cache from an earlier step.  ``value`` is the rate of plain
 (eager) launches on the stream, host launch path included; the rate of the
-same steps replayed from HIP graphs (one per pool) is reported beside it.
+same steps replayed from a HIP graph (one step on each pool) is reported
+beside it.
 
 The JSON line also carries
   roofline      decode kernel: algorithmic bytes per launch / mean kernel time
@@ -134,8 +135,7 @@ def bench_decode(torch, steps, warmup, n_pools):
     torch.cuda.synchronize()
     eager_wall = time.perf_counter() - t0
 
-    # graph replay: one graph per pool
-    graphs = []
+    # graph replay: one graph holding one step on each pool, replayed steps / n_pools times
     try:
         side = torch.cuda.Stream()
         side.wait_stream(stream)
@@ -144,19 +144,19 @@ def bench_decode(torch, steps, warmup, n_pools):
                 step(i)
         stream.wait_stream(side)
         torch.cuda.synchronize()
-        for i in range(n_pools):
-            gph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(gph):
+        gph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gph):
+            for i in range(n_pools):
                 step(i)
-            graphs.append(gph)
-        for i in range(warmup):
-            graphs[i % n_pools].replay()
+        for _ in range(max(1, warmup // n_pools)):
+            gph.replay()
         torch.cuda.synchronize()
+        reps = max(1, steps // n_pools)
         t0 = time.perf_counter()
-        for i in range(steps):
-            graphs[i % n_pools].replay()
+        for _ in range(reps):
+            gph.replay()
         torch.cuda.synchronize()
-        graph_wall = time.perf_counter() - t0
+        graph_wall = (time.perf_counter() - t0) * steps / (reps * n_pools)
     except RuntimeError as e:  # capture unavailable: fall back to the eager figure
         print(f"bench.py: graph capture failed ({e}); reporting eager launches", file=sys.stderr)
         graph_wall = None
