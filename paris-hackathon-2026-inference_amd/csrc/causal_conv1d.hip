@@ -23,15 +23,18 @@ constexpr int TILE_T = 32;     // tokens per workgroup tile
 
 template <typename T> struct Vec8;
 template <> struct Vec8<uint16_t> {
-  static __device__ __forceinline__ void load(const uint16_t *p, float *o) {
-    const uint4 u = *reinterpret_cast<const uint4 *>(p);
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+  struct Raw { uint4 u; };
+  static constexpr int PF = 8;  // tokens loaded ahead per batch
+  static __device__ __forceinline__ Raw load_raw(const uint16_t *p) { return Raw{*reinterpret_cast<const uint4 *>(p)}; }
+  static __device__ __forceinline__ void cvt(const Raw &r, float *o) {
+    const uint32_t w[4] = {r.u.x, r.u.y, r.u.z, r.u.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       o[2 * i] = bf16_bits_to_f32(w[i] & 0xffffu);
       o[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
     }
   }
+  static __device__ __forceinline__ void load(const uint16_t *p, float *o) { cvt(load_raw(p), o); }
   static __device__ __forceinline__ void store(uint16_t *p, const float *x) {
     uint32_t w[4];
 #pragma unroll
@@ -42,10 +45,15 @@ template <> struct Vec8<uint16_t> {
   }
 };
 template <> struct Vec8<float> {
-  static __device__ __forceinline__ void load(const float *p, float *o) {
-    const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
-    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  struct Raw { float4 a, b; };
+  static constexpr int PF = 4;
+  static __device__ __forceinline__ Raw load_raw(const float *p) {
+    return Raw{reinterpret_cast<const float4 *>(p)[0], reinterpret_cast<const float4 *>(p)[1]};
   }
+  static __device__ __forceinline__ void cvt(const Raw &r, float *o) {
+    o[0] = r.a.x; o[1] = r.a.y; o[2] = r.a.z; o[3] = r.a.w; o[4] = r.b.x; o[5] = r.b.y; o[6] = r.b.z; o[7] = r.b.w;
+  }
+  static __device__ __forceinline__ void load(const float *p, float *o) { cvt(load_raw(p), o); }
   static __device__ __forceinline__ void store(float *p, const float *x) {
     reinterpret_cast<float4 *>(p)[0] = make_float4(x[0], x[1], x[2], x[3]);
     reinterpret_cast<float4 *>(p)[1] = make_float4(x[4], x[5], x[6], x[7]);
@@ -60,6 +68,9 @@ template <> __device__ __forceinline__ void st1<uint16_t>(uint16_t *p, float x) 
 template <> __device__ __forceinline__ void st1<float>(float *p, float x) { *p = x; }
 
 __device__ __forceinline__ float silu(float x) { return x / (1.f + expf(-x)); }
+// SiLU with the hardware exp2 and reciprocal (a few ulp; the prefill kernel's
+// per-token arithmetic is otherwise dominated by the IEEE exp and division)
+__device__ __forceinline__ float silu_fast(float x) { return x * __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
 struct ConvArgs {
   const void *x;
@@ -92,7 +103,7 @@ __device__ __forceinline__ int64_t in_row_of(const ConvArgs &a, int n) {
   return a.st_in ? pool_row(a.in_idx, n, a.in_rows) : -1;
 }
 
-template <typename T, int SL>
+template <typename T, int SL, bool SILU>
 __global__ __launch_bounds__(CONV_NT) void conv_fwd_kernel(ConvArgs a) {
   const int c0 = (blockIdx.x * CONV_NT + threadIdx.x) * CPT;
   if (c0 >= a.C) return;
@@ -120,13 +131,16 @@ __global__ __launch_bounds__(CONV_NT) void conv_fwd_kernel(ConvArgs a) {
   }
   if (tbeg < s_beg || tbeg >= s_end) return;  // tokens outside every sequence
 
+  // taps aligned to the newest input: wt[k] multiplies x_{t - 3 + k}; a
+  // narrower kernel's missing oldest taps are zero (same sums, same order)
   float wt[4][CPT];
   {
     const T *wp = static_cast<const T *>(a.w);
+    const int lead = 4 - a.width;
 #pragma unroll
     for (int i = 0; i < CPT; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) wt[j][i] = j < a.width ? ld1<T>(wp + (int64_t)(c0 + i) * a.width + j) : 0.f;
+      for (int k = 0; k < 4; ++k) wt[k][i] = k >= lead ? ld1<T>(wp + (int64_t)(c0 + i) * a.width + (k - lead)) : 0.f;
   }
   float bias[CPT];
 #pragma unroll
@@ -148,48 +162,93 @@ __global__ __launch_bounds__(CONV_NT) void conv_fwd_kernel(ConvArgs a) {
     }
   }
 
-  for (int64_t t = tbeg; t < tend; ++t) {
-    if (t == s_end) {  // the next sequence starts inside this tile
-      ++n;
-      if (a.cu) {
-        while (n < a.n_seqs && a.cu[n + 1] <= t) ++n;  // skip empty sequences
-        if (n >= a.n_seqs) break;
-      }
-      {
-        int len;
-        seq_range(a.cu, n, a.T, a.total, &s_beg, &len);
-        s_end = s_beg + len;
-      }
-      if (t < s_beg || t >= s_end) break;
-      const int64_t hrow = in_row_of(a, n);
-#pragma unroll
-      for (int j = 0; j < WIN; ++j)
-#pragma unroll
-        for (int i = 0; i < CPT; ++i) win[j][i] = history_at<T, SL>(a, hrow, c0 + i, WIN - j);
-    }
+  // Tokens in batches of PF: a batch's inputs are requested one batch ahead
+  // (two batches in registers), so each thread keeps up to 2 PF loads in
+  // flight instead of waiting on one load per token.
+  constexpr int PF = Vec8<T>::PF;
+  using Raw = typename Vec8<T>::Raw;
+  const T *xc = static_cast<const T *>(a.x) + c0;
+  T *yc = static_cast<T *>(a.y) + c0;
+  // One token: output from the window and the raw input, then slide the window.
+  auto token = [&](const Raw &raw, int64_t t) {
     float xv[CPT];
-    Vec8<T>::load(static_cast<const T *>(a.x) + t * a.xs + c0, xv);
+    Vec8<T>::cvt(raw, xv);
     float out[CPT];
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       float acc = bias[i];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (j < a.width) {
-          const int back = a.width - 1 - j;  // tap j reads x_{t - back}
-          acc += wt[j][i] * (back == 0 ? xv[i] : win[WIN - back][i]);
-        }
-      }
-      out[i] = a.silu ? silu(acc) : acc;
+      for (int k = 0; k < 4; ++k) acc += wt[k][i] * (k == 3 ? xv[i] : win[k][i]);
+      out[i] = SILU ? silu_fast(acc) : acc;
     }
-    Vec8<T>::store(static_cast<T *>(a.y) + t * a.ys + c0, out);
-
+    Vec8<T>::store(yc + t * a.ys, out);
 #pragma unroll
     for (int j = 0; j < WIN - 1; ++j)
 #pragma unroll
       for (int i = 0; i < CPT; ++i) win[j][i] = win[j + 1][i];
 #pragma unroll
     for (int i = 0; i < CPT; ++i) win[WIN - 1][i] = xv[i];
+  };
+
+  if (tend - tbeg == TILE_T && tend <= s_end) {
+    // The whole tile lies in one sequence (the common case): fully unrolled,
+    // no per-token bounds or sequence checks.
+    constexpr int NB = TILE_T / PF;
+    Raw r[2][PF];
+#pragma unroll
+    for (int u = 0; u < PF; ++u) r[0][u] = Vec8<T>::load_raw(xc + (tbeg + u) * a.xs);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      if (b + 1 < NB) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) r[(b + 1) & 1][u] = Vec8<T>::load_raw(xc + (tbeg + (b + 1) * PF + u) * a.xs);
+      }
+#pragma unroll
+      for (int u = 0; u < PF; ++u) token(r[b & 1][u], tbeg + b * PF + u);
+    }
+    return;
+  }
+
+  // General tile: a sequence boundary or the end of the input falls inside it.
+  auto fetch = [&](Raw (&r)[PF], int64_t tb) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u)
+      if (tb + u < tend) r[u] = Vec8<T>::load_raw(xc + (tb + u) * a.xs);
+  };
+  Raw r0[PF], r1[PF];
+  bool live = true;
+  // One batch: tokens tb .. tb + PF - 1 from registers cur, the next batch requested into nxt.
+  auto batch = [&](const Raw (&cur)[PF], Raw (&nxt)[PF], int64_t tb) {
+    if (tb + PF < tend) fetch(nxt, tb + PF);
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      const int64_t t = tb + u;
+      if (!live || t >= tend) break;
+      if (t == s_end) {  // the next sequence starts inside this tile
+        ++n;
+        if (a.cu) {
+          while (n < a.n_seqs && a.cu[n + 1] <= t) ++n;  // skip empty sequences
+          if (n >= a.n_seqs) { live = false; break; }
+        }
+        {
+          int len;
+          seq_range(a.cu, n, a.T, a.total, &s_beg, &len);
+          s_end = s_beg + len;
+        }
+        if (t < s_beg || t >= s_end) { live = false; break; }
+        const int64_t hrow = in_row_of(a, n);
+#pragma unroll
+        for (int j = 0; j < WIN; ++j)
+#pragma unroll
+          for (int i = 0; i < CPT; ++i) win[j][i] = history_at<T, SL>(a, hrow, c0 + i, WIN - j);
+      }
+      token(cur[u], t);
+    }
+  };
+  fetch(r0, tbeg);
+  for (int64_t tb = tbeg; live && tb < tend; tb += 2 * PF) {
+    batch(r0, r1, tb);
+    if (live && tb + PF < tend) batch(r1, r0, tb + PF);
   }
 }
 
@@ -268,7 +327,12 @@ template <typename T, int SL>
 int launch_fwd(const ConvArgs &a, hipStream_t s) {
   const unsigned gx = (a.C / CPT + CONV_NT - 1) / CONV_NT;
   const unsigned gy = static_cast<unsigned>((a.total + TILE_T - 1) / TILE_T);
-  if (gy > 0) hipLaunchKernelGGL((conv_fwd_kernel<T, SL>), dim3(gx, gy), dim3(CONV_NT), 0, s, a);
+  if (gy > 0) {
+    if (a.silu)
+      hipLaunchKernelGGL((conv_fwd_kernel<T, SL, true>), dim3(gx, gy), dim3(CONV_NT), 0, s, a);
+    else
+      hipLaunchKernelGGL((conv_fwd_kernel<T, SL, false>), dim3(gx, gy), dim3(CONV_NT), 0, s, a);
+  }
   if (a.st_out)
     hipLaunchKernelGGL((conv_final_state_kernel<T, SL>), dim3((a.C + CONV_NT - 1) / CONV_NT, a.n_seqs),
                        dim3(CONV_NT), 0, s, a);
