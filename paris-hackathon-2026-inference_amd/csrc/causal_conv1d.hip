@@ -19,12 +19,16 @@ namespace {
 
 constexpr int CPT = 8;         // channels per thread
 constexpr int CONV_NT = 256;   // threads per workgroup
-constexpr int TILE_T = 32;     // tokens per workgroup tile
+// Tokens per workgroup tile: 64 once that still gives every CU a
+// workgroup, else 32 (a 64-token tile halves the re-read 3-token halo and
+// keeps more loads in flight per thread; short inputs need the 32-token grid)
+constexpr int TILE_SHORT = 32, TILE_LONG = 64;
+constexpr int CONV_CUS = 256;
 
 template <typename T> struct Vec8;
 template <> struct Vec8<uint16_t> {
   struct Raw { uint4 u; };
-  static constexpr int PF = 8;  // tokens loaded ahead per batch
+  static constexpr int PF = 4;  // tokens loaded ahead per batch
   static __device__ __forceinline__ Raw load_raw(const uint16_t *p) { return Raw{*reinterpret_cast<const uint4 *>(p)}; }
   static __device__ __forceinline__ void cvt(const Raw &r, float *o) {
     const uint32_t w[4] = {r.u.x, r.u.y, r.u.z, r.u.w};
@@ -103,7 +107,7 @@ __device__ __forceinline__ int64_t in_row_of(const ConvArgs &a, int n) {
   return a.st_in ? pool_row(a.in_idx, n, a.in_rows) : -1;
 }
 
-template <typename T, int SL, bool SILU>
+template <typename T, int SL, bool SILU, int TILE_T>
 __global__ __launch_bounds__(CONV_NT) void conv_fwd_kernel(ConvArgs a) {
   const int c0 = (blockIdx.x * CONV_NT + threadIdx.x) * CPT;
   if (c0 >= a.C) return;
@@ -323,15 +327,23 @@ __global__ __launch_bounds__(CONV_NT) void conv_update_kernel(UpdArgs a) {
   }
 }
 
+template <typename T, int SL, int TILE_T>
+void launch_tiles(const ConvArgs &a, unsigned gx, hipStream_t s) {
+  const unsigned gy = static_cast<unsigned>((a.total + TILE_T - 1) / TILE_T);
+  if (a.silu)
+    hipLaunchKernelGGL((conv_fwd_kernel<T, SL, true, TILE_T>), dim3(gx, gy), dim3(CONV_NT), 0, s, a);
+  else
+    hipLaunchKernelGGL((conv_fwd_kernel<T, SL, false, TILE_T>), dim3(gx, gy), dim3(CONV_NT), 0, s, a);
+}
+
 template <typename T, int SL>
 int launch_fwd(const ConvArgs &a, hipStream_t s) {
   const unsigned gx = (a.C / CPT + CONV_NT - 1) / CONV_NT;
-  const unsigned gy = static_cast<unsigned>((a.total + TILE_T - 1) / TILE_T);
-  if (gy > 0) {
-    if (a.silu)
-      hipLaunchKernelGGL((conv_fwd_kernel<T, SL, true>), dim3(gx, gy), dim3(CONV_NT), 0, s, a);
+  if (a.total > 0) {
+    if (gx * ((a.total + TILE_LONG - 1) / TILE_LONG) >= CONV_CUS)
+      launch_tiles<T, SL, TILE_LONG>(a, gx, s);
     else
-      hipLaunchKernelGGL((conv_fwd_kernel<T, SL, false>), dim3(gx, gy), dim3(CONV_NT), 0, s, a);
+      launch_tiles<T, SL, TILE_SHORT>(a, gx, s);
   }
   if (a.st_out)
     hipLaunchKernelGGL((conv_final_state_kernel<T, SL>), dim3((a.C + CONV_NT - 1) / CONV_NT, a.n_seqs),
