@@ -20,7 +20,7 @@ import torch
 
 from . import _lib
 
-SUPPORTED_K = (1024, 2048, 3072, 4096)
+SUPPORTED_K = (1024, 2048)  # hidden sizes the kernel is instantiated for
 
 
 def _weight(w: torch.Tensor, k: int, what: str) -> torch.Tensor:

@@ -195,3 +195,15 @@ def test_in_proj_decode_rejects_bad_arguments(lib):
     assert "pool rows" in lib.gdn_last_error_string().decode()
     assert _inproj_call(lib, m=0) == 0       # nothing to do, nothing launched
 
+
+
+def test_in_proj_python_gate_matches_the_built_hidden_sizes(lib):
+    """The layer takes the fused decode input side only for hidden sizes the
+    kernel is instantiated for; every other size is refused by the C side."""
+    from engine.kernels.in_proj import SUPPORTED_K, fused_in_proj_supported
+    for k in (1024, 2048, 3072, 4096):
+        gated = fused_in_proj_supported(k, 8192, 4096, 32, 32, 4)
+        assert gated == (k in SUPPORTED_K)
+        if not gated:
+            assert _inproj_call(lib, k=k, xs=k) == 2
+    assert not fused_in_proj_supported(2048, 8192, 4096, 32, 32, 3)
