@@ -73,6 +73,7 @@ def parse():
                     help="skip the prefill timing with q/k repeated to 32 heads")
     ap.add_argument("--no-layer-glue", action="store_true",
                     help="skip the fused vs torch layer-glue timing (gates, q/k repeat, gated norm)")
+    ap.add_argument("--no-conv", action="store_true", help="skip the prefill conv measurement")
     ap.add_argument("--no-in-proj", action="store_true", help="skip the decode input-projection measurement")
     ap.add_argument("--no-layer-decode", action="store_true", help="skip the whole-layer decode measurement")
     ap.add_argument("--pools", type=int, default=4, help="rotating decode state pools")
@@ -211,6 +212,36 @@ def _time(torch, fn, reps, warmup=3):
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e-3 / reps
+
+
+def bench_conv_prefill(torch, reps=40):
+    """Row a-6's prefill conv (``causal_conv1d_fn`` + SiLU, width 4) over the
+    qkv projection rows as the layer feeds it (token-major [T, 8192] bf16,
+    transformers modeling_qwen3_5_moe.py:443-444, 468-474), for one 4096-token and one 16384-token
+    sequence.  Algorithmic bytes: x read once and y written once, 2 x 2 B per
+    (token, channel); the 3-token halo each tile re-reads hits in L2."""
+    from engine import configs
+    from engine.kernels import causal_conv1d_fn
+
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator().manual_seed(43)
+    c = configs.CONV_DIM
+    w = torch.randn(c, 4, generator=gen).to(dev, torch.bfloat16)
+    out = {"config": f"C={c}, width 4, SiLU, bf16, token-major input (one sequence)"}
+    for t in (4096, 16384):
+        xs = [torch.randn(1, t, c, generator=gen).to(dev, torch.bfloat16) for _ in range(2)]
+        i = [0]
+
+        def run():
+            i[0] ^= 1
+            return causal_conv1d_fn(xs[i[0]].transpose(1, 2), w, None, activation="silu")
+
+        us = _time(torch, run, reps) * 1e6
+        byts = 2 * t * c * 2
+        out[f"T{t}"] = {"us": us, "achieved_GBps": byts / us / 1e3, "peak_GBps": HBM_PEAK / 1e9,
+                        "frac": byts / us / 1e3 / (HBM_PEAK / 1e9), "bytes": byts}
+        del xs
+    return out
 
 
 def bench_layer_glue(torch, reps=20):
@@ -472,6 +503,8 @@ def main():
             out["prefill_qk_repeated"] = bench_prefill(torch, repeat_qk=True)
         if not args.no_layer_glue:
             out["layer_glue"] = bench_layer_glue(torch)
+    if not args.no_conv:
+        out["conv_prefill"] = bench_conv_prefill(torch)
     if not args.no_in_proj:
         out["decode_in_proj"] = bench_in_proj(torch)
     if not args.no_layer_decode:
