@@ -299,9 +299,25 @@ def bench_layer_glue(torch, reps=20):
                               "frac": norm_bytes / t_norm / HBM_PEAK, "bytes": norm_bytes}}
 
 
+def _median_time(fn, min_reps=5, budget_s=3.0):
+    """Median wall time of fn() over >= min_reps runs (and about budget_s), after one warmup run."""
+    fn()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_reps or time.perf_counter() - t_start < budget_s:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
 def cpu_baseline(budget_s=12.0):
-    """CPU oracle (numpy fp32) on a bounded sample of the decode workload, sequences
-    split across the host cores this process may use."""
+    """CPU oracle (numpy fp32) on bounded samples: the decode workload
+    (configuration 1, the headline value) with sequences split across the host
+    cores this process may use, the same on one thread, and the prefill
+    (configuration 2, all 32 heads of the 4096 tokens) with heads split across
+    the cores."""
     import numpy as np
     from engine import configs
     from oracle import gdn
@@ -316,18 +332,35 @@ def cpu_baseline(budget_s=12.0):
         return gdn.recurrent_gated_delta_rule(*(a[sl] for a in args), initial_state=h0[sl], dtype=np.float32)
 
     with cf.ThreadPoolExecutor(n) as ex:
-        list(ex.map(run_part, parts))  # warmup
-        steps, t0 = 0, time.perf_counter()
-        while True:
-            list(ex.map(run_part, parts))
-            steps += 1
-            el = time.perf_counter() - t0
-            if el > budget_s:
-                break
-    per = el / steps
+        per, reps = _median_time(lambda: list(ex.map(run_part, parts)), budget_s=budget_s)
+    per1, reps1 = _median_time(lambda: run_part(slice(0, 64)), budget_s=3.0)
+
+    # prefill: v-heads split into n groups of whole k-head pairs
+    c2 = configs.config2()
+    q, k, v, g, beta = (c2[x].float().numpy() for x in ("q", "k", "v", "g", "beta"))
+    hk, hv = q.shape[2], v.shape[2]
+    grp = hv // hk
+    n2 = min(n, hk)
+    kparts = [slice(i * hk // n2, (i + 1) * hk // n2) for i in range(n2)]
+
+    def run_heads(ks):
+        vs = slice(ks.start * grp, ks.stop * grp)
+        return gdn.chunk_gated_delta_rule(q[:, :, ks], k[:, :, ks], v[:, :, vs], g[:, :, vs], beta[:, :, vs],
+                                          dtype=np.float32)
+
+    with cf.ThreadPoolExecutor(n2) as ex:
+        per2, reps2 = _median_time(lambda: list(ex.map(run_heads, kparts)), min_reps=3, budget_s=3.0)
+    t2 = q.shape[1]
     return {"value": 64 / per, "unit": "tok/s", "cores": n, "kind": "port",
-            "sample": f"{steps} decode steps of configuration 1 (B=64, one layer, 64 gathered slot states) with "
-                      f"the numpy fp32 oracle, sequences split over {n} threads; {per * 1e3:.1f} ms/step"}
+            "sample": f"configuration 1 decode steps (B=64, one layer, 64 gathered slot states) with the numpy "
+                      f"fp32 oracle, sequences split over {n} threads; median of {reps} steps after one warmup, "
+                      f"{per * 1e3:.1f} ms/step",
+            "one_thread": {"value": 64 / per1, "unit": "tok/s", "cores": 1,
+                           "sample": f"the same step on one thread, median of {reps1}: {per1 * 1e3:.1f} ms/step"},
+            "prefill": {"value": t2 / per2, "unit": "tok/s", "cores": n2,
+                        "sample": f"configuration 2 (T={t2}, all {hv} v-heads) through the numpy fp32 chunk oracle, "
+                                  f"k-head groups split over {n2} threads; median of {reps2} runs after one "
+                                  f"warmup, {per2:.2f} s per run"}}
 
 
 def bench_in_proj(torch, sets=6, reps=4):
