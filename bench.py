@@ -74,7 +74,7 @@ def parse():
     ap.add_argument("--no-layer-glue", action="store_true",
                     help="skip the fused vs torch layer-glue timing (gates, q/k repeat, gated norm)")
     ap.add_argument("--no-conv", action="store_true", help="skip the prefill conv measurement")
-    ap.add_argument("--no-in-proj", action="store_true", help="skip the decode input-projection measurement")
+    ap.add_argument("--no-in-proj", action="store_true", help="skip the decode projection measurements")
     ap.add_argument("--no-layer-decode", action="store_true", help="skip the whole-layer decode measurement")
     ap.add_argument("--pools", type=int, default=4, help="rotating decode state pools")
     ap.add_argument("--prefill-only", action="store_true",
@@ -413,6 +413,44 @@ def bench_in_proj(torch, sets=6, reps=4):
                          "kernel": "gdn::in_proj_decode_kernel<16>"}}
 
 
+def bench_out_proj(torch, sets=16, reps=4):
+    """Row f-4's output side at the decode batch: ``out_proj`` (4096 -> 2048,
+    bf16) for 64 rows, the split-K kernel pair against hipBLASLt (torch
+    F.linear), each captured once per weight set into one HIP graph (16 sets:
+    268 MB of weights, past the 256 MB Infinity Cache)."""
+    import torch.nn.functional as F
+    from engine.kernels import gdn_out_proj_decode
+
+    dev = torch.device("cuda", 0)
+    m, k, n = 64, 4096, 2048
+    gen = torch.Generator().manual_seed(53)
+    wsets = [(0.02 * torch.randn(n, k, generator=gen)).to(dev, torch.bfloat16) for _ in range(sets)]
+    x = torch.randn(m, k, generator=gen).to(dev, torch.bfloat16)
+
+    def graph_us(fn):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for w in wsets:
+                fn(w)
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for w in wsets:
+                fn(w)
+        return _time(torch, g.replay, reps, warmup=2) / sets * 1e6
+
+    t_ours = graph_us(lambda w: gdn_out_proj_decode(x, w))
+    t_lt = graph_us(lambda w: F.linear(x, w))
+    byts = n * k * 2 + m * k * 2 + m * n * 2  # weights, x, y
+    return {"config": "B=64 rows, out_proj 4096 -> 2048, bf16",
+            "us": t_ours, "hipblaslt_us": t_lt, "speedup": t_lt / t_ours,
+            "roofline": {"bound": "hbm", "achieved": byts / t_ours / 1e3, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                         "frac": byts / (t_ours * 1e-6) / HBM_PEAK, "bytes_per_call": byts,
+                         "kernels": "gdn::out_proj_partial_kernel + gdn::out_proj_sum_kernel<8> (4 MiB of fp32 "
+                                    "partials written and read besides)"}}
+
+
 def bench_layer_decode(torch, layers=4, reps=5):
     """One GDN layer decode step at B=64 with Qwen3.5-MoE layer shapes (hidden
     2048, 16 k-heads, 32 v-heads of 128, conv width 4; random bf16 weights):
@@ -422,9 +460,9 @@ def bench_layer_decode(torch, layers=4, reps=5):
     the weights nor the states stay in the 256 MB Infinity Cache), one step
     of each captured into one HIP graph; the graph is replayed ``reps``
     times.  Also: the same steps with the unfused input side (hipBLASLt
-    projections + conv update kernel), and the gather + scatter the
-    reference cache runs around every step for the same slots
-    (``index_select`` of both pools before, ``index_copy_`` after,
+    projections + conv update kernel), with out_proj on hipBLASLt, and the
+    gather + scatter the reference cache runs around every step for the same
+    slots (``index_select`` of both pools before, ``index_copy_`` after,
     engine/runtime/kv_cache.py:189-208)."""
     import types
     from unittest import mock
@@ -478,13 +516,16 @@ def bench_layer_decode(torch, layers=4, reps=5):
     t_fused = graph_us(steps)
     with mock.patch.object(gdn_layer, "_fused_decode_fits", lambda *a, **k: False):
         t_unfused = graph_us(steps)
+    with mock.patch.object(gdn_layer, "_out_proj_fits", lambda *a, **k: False):
+        t_lt_out = graph_us(steps)
     t_gs = graph_us(gather_scatter)
     return {"config": "one GDN layer decode step, B=64 of 128 slots, hidden 2048, Hk=16 Hv=32 d=128, conv 4, "
                       "bf16 weights (random), fp32 state pools; 4 layers per graph, own weights and pools",
             "step_us": t_fused, "tok_per_s": 64 / (t_fused * 1e-6),
             "step_unfused_input_us": t_unfused,
+            "step_hipblaslt_out_proj_us": t_lt_out,
             "reference_cache_gather_scatter_us": t_gs,
-            "note": "step = fused input side + recurrence on the pool + gated norm + out_proj (hipBLASLt); "
+            "note": "step = fused input side + recurrence on the pool + gated norm + split-K out_proj; "
                     "the reference runs its gather + scatter in addition to the layer step"}
 
 
@@ -540,6 +581,7 @@ def main():
         out["conv_prefill"] = bench_conv_prefill(torch)
     if not args.no_in_proj:
         out["decode_in_proj"] = bench_in_proj(torch)
+        out["decode_out_proj"] = bench_out_proj(torch)
     if not args.no_layer_decode:
         out["layer_decode"] = bench_layer_decode(torch)
     if not args.no_cpu:

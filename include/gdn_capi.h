@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 5
+#define GDN_ABI_VERSION 6
 
 typedef enum {
   GDN_OK = 0,
@@ -258,7 +258,7 @@ int causal_conv1d_update(const void *x, int64_t x_stride_t, void *conv_state,
  *           slot_idx (NULL: row m); ids outside [0, pool_rows): zero window,
  *           nothing written
  *   y_qkv [M, n_qkv], z [M, n_z], b [M, n_b], a [M, n_a] bf16, contiguous
- *   K in {1024, 2048, 3072, 4096}; n_qkv, n_z multiples of 64;
+ *   K in {1024, 2048}; n_qkv, n_z multiples of 64;
  *   n_b, n_a multiples of 4, at most 32.  silu: apply SiLU after the conv.
  */
 int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w_qkv, const void *w_z,
@@ -266,6 +266,26 @@ int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w_qkv, const
                        int32_t n_z, int32_t n_b, int32_t n_a, const void *conv_w, const void *conv_bias,
                        void *conv_pool, const int64_t *slot_idx, int64_t pool_rows, void *y_qkv, void *z,
                        void *b, void *a, int silu, void *stream);
+
+/*
+ * Decode-step output projection of the GDN layer:  y = x W^T  (bf16, fp32
+ * sums), with K split over workgroups (512 of K each); a second kernel adds
+ * the fp32 partial sums in split order, so results do not depend on
+ * scheduling.
+ *
+ * Replaces, for small M (decode rows), the out_proj nn.Linear of HF's GDN
+ * layer (transformers modeling_qwen3_5_moe.py:428, called at :540).
+ *
+ *   x  [M, K] bf16, row stride x_stride (elements, >= K, multiple of 8), 16-byte aligned
+ *   w  [N, K] bf16 nn.Linear weight, rows contiguous, 16-byte aligned
+ *   y  [M, N] bf16, row stride y_stride (>= N, multiple of 4), 8-byte aligned
+ *   N a multiple of 64; K a multiple of 512, at most 8192
+ *   workspace: gdn_out_proj_workspace_bytes(M, K, N) bytes (the partial
+ *     sums), 16-byte aligned, used until the second kernel has run
+ */
+size_t gdn_out_proj_workspace_bytes(int32_t M, int32_t K, int32_t N);
+int gdn_out_proj_decode(const void *x, int64_t x_stride, const void *w, int32_t M, int32_t K, int32_t N,
+                        void *y, int64_t y_stride, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
  * Speculative-verify commit: pool[slot_ids[b]] = snapshots[b, accepted_len[b]-1].

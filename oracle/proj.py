@@ -3,7 +3,8 @@ infrastructure only.
 
 The decode step's input side (four bias-free ``nn.Linear`` and the conv
 window update, transformers 5.15.0 modeling_qwen3_5_moe.py:424-427,
-443-461), on bf16-valued inputs in float64.
+443-461) and its output projection (:420, applied at :540), on bf16-valued
+inputs in float64.
 """
 from __future__ import annotations
 
@@ -44,3 +45,9 @@ def in_proj_decode(x, w_qkv, w_z, w_b, w_a, conv_weight, conv_state, conv_bias=N
                                         activation=activation, dtype=dtype)
     return y[:, :, 0], z, b, a, new_state
 
+
+def out_proj(x, w, dtype=np.float64):
+    """The layer's ``out_proj`` over decode rows: a bias-free ``nn.Linear``
+    (transformers 5.15.0 modeling_qwen3_5_moe.py:420, applied at :540),
+    x [M, K] @ w [N, K]^T, unrounded (the module stores it in bf16)."""
+    return np.asarray(x, dtype) @ np.asarray(w, dtype).T

@@ -32,6 +32,14 @@
 // and runs the epilogue on it.  Lane (c, g) of a row tile's accumulator
 // holds out[16 t + c][16 w + 4 g .. + 3]: four consecutive channels of one
 // row, also the unit of the conv pool ([rows, C, 4] bf16: 32 bytes).
+//
+// The same scheme serves out_proj at decode ([Hv*V -> D], modeling_qwen3_5_moe.py:540:
+// 16.8 MB of weights for 64 rows): there the 2048 output columns give only
+// 32 blocks of 64, so K is split over workgroups as well (512 of K each, 256
+// workgroups), each writing its fp32 partial block to a workspace; a second
+// small kernel adds the partials in split order and writes bf16.  (Letting
+// the last workgroup of a column block add them needs agent-scope fences,
+// whose L2 writeback and invalidate per workgroup measured 111 us.)
 #include "gdn_common.h"
 
 namespace gdn {
@@ -62,6 +70,10 @@ struct ProjShape {
 };
 using InProjShape2048 = ProjShape<4, 4, 16, 2>;  // input projections, K = 2048
 using InProjShape1024 = ProjShape<4, 4, 8, 2>;   // input projections, K = 1024
+using OutProjShape = ProjShape<4, 4, 4, 1>;      // out_proj: 64 columns x 512 of K per workgroup
+constexpr int OP_KSPAN = 4 * OutProjShape::KPART;  // K per workgroup (512)
+constexpr int OP_MAX_SPLIT = 16;                  // workgroups per column block (K <= 8192)
+constexpr int OP_RED_NT = 256;                    // threads per workgroup of the partials' sum
 
 struct InProjArgs {
   const uint16_t *x;  // [M, K] bf16, row stride xs elements
@@ -288,8 +300,139 @@ __global__ __launch_bounds__(64 * IP_WAVES) void in_proj_decode_kernel(InProjArg
   }
 }
 
+struct OutProjArgs {
+  const uint16_t *x;  // [M, K] bf16, row stride xs elements
+  int64_t xs;
+  const uint16_t *w;  // [N, K] bf16, rows contiguous
+  int M, K, N;
+  int split, ncb;     // workgroups per column block (K / 512), column blocks (N / 64)
+  float *part;        // [split][row blocks][64][N] fp32 partial sums
+  uint16_t *y;        // [M, N] bf16, row stride ys elements
+  int64_t ys;
+};
+
+// Partial block (64 rows x 64 columns, 512 of K) of workgroup (column block
+// cb, split sp, row block blockIdx.y).  A column block's split workgroups
+// are bid = cb + ncb sp.
+__global__ __launch_bounds__(64 * IP_WAVES) void out_proj_partial_kernel(OutProjArgs a) {
+  using S = OutProjShape;
+  __shared__ u32x4_t xl[S::LDS_BLOCKS];  // the rows' 512 columns of K: 64 KiB
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cg = wave % S::CG, kq = wave / S::CG;
+  const int cb = blockIdx.x % a.ncb, sp = blockIdx.x / a.ncb;
+  const int mblk = blockIdx.y, nmb = gridDim.y;
+  const int m0 = mblk * IP_ROWS;
+  const int mb = min(IP_ROWS, a.M - m0);
+  const int col = cb * S::COLS + 16 * cg;
+  const int k0 = sp * OP_KSPAN;
+  const auto rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.w) + static_cast<int64_t>(col) * a.K, 0,
+                                                    16 * a.K * 2, BUF_DWORD3);
+  const uint16_t *xbase = a.x + static_cast<int64_t>(m0) * a.xs + k0;
+  const int xbytes = static_cast<int>(((mb - 1) * a.xs + (a.K - k0)) * 2);  // rows past M read as zero
+
+  dma_x<S>(xl, xbase, xbytes, a.xs, 0, wave, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4_t wr[S::KS];
+  load_w<S::KS>(wr, rw, k0 + kq * S::KPART, a.K, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  const f32x4_t o = proj_phases<S, 0>(xl, wr, [](int) {}, wave, lane);
+
+  // lane (c, g) of wave (cg, kq): row 16 kq + c, columns col + 4 g .. + 3
+  const int c = lane & 15, g = lane >> 4;
+  const int64_t prow = static_cast<int64_t>(sp * nmb + mblk) * IP_ROWS + 16 * kq + c;
+  *reinterpret_cast<f32x4_t *>(a.part + prow * a.N + col + 4 * g) = o;
+}
+
+// y[m][4 i .. 4 i + 3] = bf16(sum over splits, in split order): one thread
+// per 4 outputs.  SPLIT > 0: that many splits, all loads issued before the
+// adds; SPLIT = 0: a.split of them, one at a time.
+template <int SPLIT>
+__global__ __launch_bounds__(OP_RED_NT) void out_proj_sum_kernel(OutProjArgs a) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * OP_RED_NT + threadIdx.x;
+  const int n4 = a.N / 4;
+  if (i >= static_cast<int64_t>(a.M) * n4) return;
+  const int m = static_cast<int>(i / n4), n = 4 * static_cast<int>(i % n4);
+  const int64_t pstride = static_cast<int64_t>((a.M + IP_ROWS - 1) / IP_ROWS) * IP_ROWS * a.N;
+  const float *p = a.part + static_cast<int64_t>(m) * a.N + n;
+  f32x4_t t;
+  if constexpr (SPLIT > 0) {
+    f32x4_t v[SPLIT];
+#pragma unroll
+    for (int q = 0; q < SPLIT; ++q) v[q] = *reinterpret_cast<const f32x4_t *>(p + q * pstride);
+    t = v[0];
+#pragma unroll
+    for (int q = 1; q < SPLIT; ++q) t += v[q];
+  } else {
+    t = *reinterpret_cast<const f32x4_t *>(p);
+    for (int q = 1; q < a.split; ++q) t += *reinterpret_cast<const f32x4_t *>(p + q * pstride);
+  }
+  *reinterpret_cast<uint2 *>(a.y + static_cast<int64_t>(m) * a.ys + n) = make_uint2(pack2(t[0], t[1]), pack2(t[2], t[3]));
+}
+
 }  // namespace
 }  // namespace gdn
+
+extern "C" size_t gdn_out_proj_workspace_bytes(int32_t M, int32_t K, int32_t N) {
+  using namespace gdn;
+  if (M <= 0 || K <= 0 || N <= 0) return 0;
+  const int64_t nmb = (M + IP_ROWS - 1) / IP_ROWS;
+  const int64_t split = (K + OP_KSPAN - 1) / OP_KSPAN;
+  return static_cast<size_t>(split * nmb * IP_ROWS * N * 4);
+}
+
+extern "C" int gdn_out_proj_decode(const void *x, int64_t x_stride, const void *w, int32_t M, int32_t K, int32_t N,
+                                   void *y, int64_t y_stride, void *workspace, size_t workspace_bytes, void *stream) {
+  using namespace gdn;
+  if (!x || !w || !y || !workspace) return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_out_proj_decode: null pointer argument");
+  if (M < 0 || N <= 0 || N % OutProjShape::COLS || K <= 0 || K % OP_KSPAN || K / OP_KSPAN > OP_MAX_SPLIT)
+    return fail(GDN_ERR_UNSUPPORTED,
+                "gdn_out_proj_decode: need N a multiple of %d and K a multiple of %d up to %d (got M=%d K=%d N=%d)",
+                OutProjShape::COLS, OP_KSPAN, OP_KSPAN * OP_MAX_SPLIT, M, K, N);
+  if (x_stride < K || x_stride % 8 || y_stride < N || y_stride % 4)
+    return fail(GDN_ERR_INVALID_ARGUMENT,
+                "gdn_out_proj_decode: row strides x %lld (>= K, multiple of 8), y %lld (>= N, multiple of 4)",
+                static_cast<long long>(x_stride), static_cast<long long>(y_stride));
+  // buffer offsets are 32-bit: one 64-row slice of x and one 16-row block of w
+  if ((static_cast<int64_t>(IP_ROWS - 1) * x_stride + K) * 2 > INT32_MAX)
+    return fail(GDN_ERR_UNSUPPORTED, "gdn_out_proj_decode: x stride %lld too large", static_cast<long long>(x_stride));
+  auto al = [](const void *p, uintptr_t n) { return reinterpret_cast<uintptr_t>(p) % n == 0; };
+  if (!al(x, 16) || !al(w, 16) || !al(y, 8) || !al(workspace, 16))
+    return fail(GDN_ERR_INVALID_ARGUMENT,
+                "gdn_out_proj_decode: x, w and the workspace must be 16-byte aligned, y 8-byte");
+  if (M == 0) return ok();
+  if ((M + IP_ROWS - 1) / IP_ROWS > 65535) return fail(GDN_ERR_UNSUPPORTED, "gdn_out_proj_decode: M=%d too large", M);
+  const size_t need = gdn_out_proj_workspace_bytes(M, K, N);
+  if (workspace_bytes < need)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_out_proj_decode: workspace of %zu bytes, need %zu", workspace_bytes,
+                need);
+  OutProjArgs args{};
+  args.x = static_cast<const uint16_t *>(x);
+  args.xs = x_stride;
+  args.w = static_cast<const uint16_t *>(w);
+  args.M = M;
+  args.K = K;
+  args.N = N;
+  args.split = K / OP_KSPAN;
+  args.ncb = N / OutProjShape::COLS;
+  args.part = static_cast<float *>(workspace);
+  args.y = static_cast<uint16_t *>(y);
+  args.ys = y_stride;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(args.ncb * args.split), static_cast<unsigned>((M + IP_ROWS - 1) / IP_ROWS));
+  hipLaunchKernelGGL(out_proj_partial_kernel, grid, dim3(64 * IP_WAVES), 0, s, args);
+  const int64_t quads = static_cast<int64_t>(M) * (N / 4);
+  const dim3 rgrid(static_cast<unsigned>((quads + OP_RED_NT - 1) / OP_RED_NT));
+  switch (args.split) {
+    case 1: hipLaunchKernelGGL(out_proj_sum_kernel<1>, rgrid, dim3(OP_RED_NT), 0, s, args); break;
+    case 2: hipLaunchKernelGGL(out_proj_sum_kernel<2>, rgrid, dim3(OP_RED_NT), 0, s, args); break;
+    case 4: hipLaunchKernelGGL(out_proj_sum_kernel<4>, rgrid, dim3(OP_RED_NT), 0, s, args); break;
+    case 8: hipLaunchKernelGGL(out_proj_sum_kernel<8>, rgrid, dim3(OP_RED_NT), 0, s, args); break;
+    default: hipLaunchKernelGGL(out_proj_sum_kernel<0>, rgrid, dim3(OP_RED_NT), 0, s, args); break;
+  }
+  return check_launch("gdn_out_proj_decode");
+}
 
 extern "C" int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w_qkv, const void *w_z,
                                   const void *w_b, const void *w_a, int32_t M, int32_t K, int32_t n_qkv,

@@ -17,6 +17,8 @@ third-party packages (fla, causal-conv1d) via HF:
 - ``rms_norm_gated``                    the GDN output norm in one pass
 - ``gdn_in_proj_decode``                a decode step's four input projections
   and the conv update in one kernel (in_proj.py)
+- ``gdn_out_proj_decode``               a decode step's output projection,
+  K split over workgroups (in_proj.py)
 - ``gated_delta_net_forward``, ``install_gdn_layer_patch``  HF's GDN layer
   forward on these kernels (native GQA, fused gates and norm)
 
@@ -33,7 +35,7 @@ from .delta_rule import (chunk_gated_delta_rule, chunk_gated_delta_rule_from_pro
 from .fused_recurrent import (fused_recurrent_gated_delta_rule, fused_recurrent_gated_delta_rule_from_projections,
                               recurrent_gated_delta_rule)
 from .gdn_layer import gated_delta_net_forward, install_gdn_layer_patch, rms_norm_gated
-from .in_proj import gdn_in_proj_decode
+from .in_proj import gdn_in_proj_decode, gdn_out_proj_decode
 from .state_pool import LinearAttentionSlotPool, gdn_conv_state_commit, gdn_state_commit
 
 __all__ = [
@@ -50,6 +52,7 @@ __all__ = [
     "fused_recurrent_gated_delta_rule_from_projections",
     "rms_norm_gated",
     "gdn_in_proj_decode",
+    "gdn_out_proj_decode",
     "gated_delta_net_forward",
     "install_gdn_layer_patch",
 ]

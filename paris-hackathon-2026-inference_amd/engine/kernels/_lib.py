@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libgdn_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 GDN_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
@@ -90,6 +90,12 @@ SIGNATURES = {
         _c_void_p, _c_void_p, _i64,                 # conv_pool slot_idx pool_rows
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, # y_qkv z b a
         _int, _c_void_p]),                          # silu stream
+    "gdn_out_proj_workspace_bytes": (_size, [_i32, _i32, _i32]),  # M K N
+    "gdn_out_proj_decode": (_int, [
+        _c_void_p, _i64, _c_void_p,                 # x x_stride w
+        _i32, _i32, _i32,                           # M K N
+        _c_void_p, _i64,                            # y y_stride
+        _c_void_p, _size, _c_void_p]),              # workspace bytes stream
     "causal_conv1d_fwd": (_int, [
         _c_void_p, _i64, _c_void_p, _c_void_p,      # x x_stride w bias
         _c_void_p, _i64,                            # y y_stride

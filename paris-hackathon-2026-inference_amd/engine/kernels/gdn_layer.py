@@ -39,7 +39,7 @@ from . import _lib
 from .causal_conv1d import causal_conv1d_fn, causal_conv1d_update
 from .delta_rule import chunk_gated_delta_rule_from_projections
 from .fused_recurrent import fused_recurrent_gated_delta_rule_from_projections
-from .in_proj import fused_in_proj_supported, gdn_in_proj_decode
+from .in_proj import OUT_PROJ_MAX_M, fused_in_proj_supported, fused_out_proj_supported, gdn_in_proj_decode, gdn_out_proj_decode
 
 log = logging.getLogger(__name__)
 
@@ -110,6 +110,23 @@ def _fused_decode(self, hidden_states: torch.Tensor, conv_state: torch.Tensor,
     return tuple(t.view(batch_size, 1, -1) for t in (y, z, b, a))
 
 
+def _out_proj_fits(self, out: torch.Tensor) -> bool:
+    """Whether ``out_proj`` over these rows can take :func:`gdn_out_proj_decode`:
+    one token per row, at most OUT_PROJ_MAX_M rows, a plain bias-free bf16
+    ``nn.Linear`` of a supported shape."""
+    lin = self.out_proj
+    return (type(lin) is torch.nn.Linear and out.shape[1] == 1 and out.shape[0] <= OUT_PROJ_MAX_M
+            and out.dtype == torch.bfloat16 and lin.bias is None and lin.weight.dtype == torch.bfloat16
+            and fused_out_proj_supported(lin.weight.shape[1], lin.weight.shape[0]))
+
+
+def _out_proj(self, out: torch.Tensor) -> torch.Tensor:
+    """``self.out_proj(out)`` for ``out`` [B, L, Hv*V]; decode rows through the kernel."""
+    if _out_proj_fits(self, out):
+        return gdn_out_proj_decode(out, self.out_proj.weight)
+    return self.out_proj(out)
+
+
 def gated_delta_net_forward(self, hidden_states: torch.Tensor, cache_params=None,
                             attention_mask: Optional[torch.Tensor] = None, **kwargs) -> torch.Tensor:
     """Forward of HF's GDN layer (``self`` is a ``*GatedDeltaNet`` module of
@@ -172,7 +189,7 @@ def gated_delta_net_forward(self, hidden_states: torch.Tensor, cache_params=None
 
     z = z.reshape(batch_size, seq_len, -1, self.head_v_dim)
     out = rms_norm_gated(core, z, self.norm.weight, self.norm.variance_epsilon)
-    return self.out_proj(out.reshape(batch_size, seq_len, -1))
+    return _out_proj(self, out.reshape(batch_size, seq_len, -1))
 
 
 # decode steps longer than this (a continued prefill) take the chunk kernels
@@ -232,7 +249,7 @@ def _forward_on_pools(self, hidden_states: torch.Tensor, pools, attention_mask: 
 
     z = z.reshape(batch_size, seq_len, -1, self.head_v_dim)
     out = rms_norm_gated(core, z, self.norm.weight, self.norm.variance_epsilon)
-    return self.out_proj(out.reshape(batch_size, seq_len, -1))
+    return _out_proj(self, out.reshape(batch_size, seq_len, -1))
 
 
 _LAYER_CLASSES = (

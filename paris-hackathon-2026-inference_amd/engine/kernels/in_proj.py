@@ -1,4 +1,5 @@
-"""Decode-step input projections of the GDN layer, conv update fused.
+"""Decode-step projections of the GDN layer: the input side (conv update
+fused) and the output projection.
 
 HF's GDN decode step (transformers modeling_qwen3_5_moe.py:443-461) runs
 ``in_proj_qkv``, ``in_proj_z``, ``in_proj_b``, ``in_proj_a`` (four
@@ -7,10 +8,11 @@ HF's GDN decode step (transformers modeling_qwen3_5_moe.py:443-461) runs
 does all of it in one HIP kernel (``gdn_in_proj_decode`` in
 include/gdn_capi.h): each weight row is read once from HBM, and the qkv
 projection goes through the conv window update in registers, so it is never
-written out before the conv.  Prefill and ``out_proj`` keep the
-library GEMMs (hipBLASLt via ``torch.nn.functional.linear``): there the
-projections are compute-bound and the conv kernels read their output in
-place.
+written out before the conv.  :func:`gdn_out_proj_decode` runs ``out_proj``
+(:428, called at :540) for decode rows with K split over 256 workgroups (the
+2048 output columns alone would occupy 32).  Prefill keeps the library GEMMs
+(hipBLASLt via ``torch.nn.functional.linear``): there the projections are
+compute-bound and the conv kernels read their output in place.
 """
 from __future__ import annotations
 
@@ -91,3 +93,39 @@ def gdn_in_proj_decode(hidden: torch.Tensor, w_qkv: torch.Tensor, w_z: torch.Ten
     _lib.check(st, "gdn_in_proj_decode")
     return tuple(outs)
 
+
+OUT_PROJ_MAX_M = 64  # rows up to which the decode out_proj kernel is used (above: hipBLASLt, measured faster at 128)
+
+
+def fused_out_proj_supported(k: int, n: int) -> bool:
+    """Shapes :func:`gdn_out_proj_decode` takes: K a multiple of 512 up to
+    8192 (Hv*V = 4096 for Qwen3.5), N a multiple of 64 (hidden 2048)."""
+    return k % 512 == 0 and 0 < k <= 8192 and n % 64 == 0 and n > 0
+
+
+def gdn_out_proj_decode(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """``x @ weight.T`` for decode rows: x ``[M, K]`` (or ``[M, 1, K]``) bf16,
+    weight the ``nn.Linear`` weight ``[N, K]`` bf16; returns ``[M, N]`` bf16
+    (``[M, 1, N]`` for a 3-d x).  The partial sums over K are added in a
+    fixed order, so the result does not depend on scheduling."""
+    dev = _lib.require_gpu(x, weight)
+    x2 = x.reshape(-1, x.shape[-1]) if x.dim() == 3 else x
+    if x2.dim() != 2 or x2.dtype != torch.bfloat16:
+        raise ValueError(f"x: expected bf16 [M, K] or [M, 1, K], got {tuple(x.shape)} {x.dtype}")
+    if x.dim() == 3 and x.shape[1] != 1:
+        raise ValueError(f"x: one token per row, got {tuple(x.shape)}")
+    m, k = x2.shape
+    if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    w = _weight(weight, k, "weight")
+    n = w.shape[0]
+    if not fused_out_proj_supported(k, n):
+        raise ValueError(f"out_proj of {k} -> {n}: the kernel needs K a multiple of 512 up to 8192 and N of 64")
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    lib = _lib.load()
+    ws_bytes = int(lib.gdn_out_proj_workspace_bytes(m, k, n))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    st = lib.gdn_out_proj_decode(_lib.ptr(x2), x2.stride(0) if m > 1 else k, _lib.ptr(w), m, k, n,
+                                 _lib.ptr(y), n, _lib.ptr(ws), ws.numel(), _lib.stream_of(x2))
+    _lib.check(st, "gdn_out_proj_decode")
+    return y.view(m, 1, n) if x.dim() == 3 else y

@@ -30,7 +30,8 @@ def test_header_lists_the_entry_points():
     assert header_functions() == sorted([
         "causal_conv1d_fwd", "causal_conv1d_update", "gdn_abi_version", "gdn_chunk_fwd",
         "gdn_chunk_fwd_gated", "gdn_chunk_workspace_bytes", "gdn_last_error_string", "gdn_recurrent_fwd",
-        "gdn_recurrent_fwd_gated", "gdn_rmsnorm_gated_fwd", "gdn_state_commit", "gdn_conv_state_commit", "gdn_in_proj_decode"])
+        "gdn_recurrent_fwd_gated", "gdn_rmsnorm_gated_fwd", "gdn_state_commit", "gdn_conv_state_commit", "gdn_in_proj_decode",
+        "gdn_out_proj_decode", "gdn_out_proj_workspace_bytes"])
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -41,7 +42,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.gdn_abi_version() == _lib.ABI_VERSION == 5
+    assert lib.gdn_abi_version() == _lib.ABI_VERSION == 6
 
 
 def _rec_call(lib, **over):
@@ -207,3 +208,40 @@ def test_in_proj_python_gate_matches_the_built_hidden_sizes(lib):
         if not gated:
             assert _inproj_call(lib, k=k, xs=k) == 2
     assert not fused_in_proj_supported(2048, 8192, 4096, 32, 32, 3)
+
+
+def _outproj_call(lib, **over):
+    args = dict(x=256, xs=4096, w=256, m=64, k=4096, n=2048, y=256, ys=2048, ws=256, ws_bytes=1 << 30,
+                stream=None)
+    args.update(over)
+    return lib.gdn_out_proj_decode(*args.values())
+
+
+def test_out_proj_workspace_is_host_arithmetic(lib):
+    # the partial sums: [K/512 splits][row blocks][64 rows][N] fp32
+    assert lib.gdn_out_proj_workspace_bytes(64, 4096, 2048) == 8 * 64 * 2048 * 4
+    assert lib.gdn_out_proj_workspace_bytes(65, 4096, 2048) == 8 * 2 * 64 * 2048 * 4
+    assert lib.gdn_out_proj_workspace_bytes(1, 2048, 64 * 70) == 4 * 64 * 64 * 70 * 4
+    assert lib.gdn_out_proj_workspace_bytes(0, 4096, 2048) == 0
+
+
+def test_out_proj_decode_rejects_bad_arguments(lib):
+    assert _outproj_call(lib, k=4000, xs=4000) == 2        # K not a multiple of 512
+    assert "K=4000" in lib.gdn_last_error_string().decode()
+    assert _outproj_call(lib, k=16384, xs=16384) == 2      # more than 16 splits
+    assert _outproj_call(lib, n=2000, ys=2000) == 2        # N not a multiple of 64
+    assert _outproj_call(lib, xs=2048) == 1                # row stride below K
+    assert _outproj_call(lib, ys=1024) == 1
+    assert _outproj_call(lib, x=24) == 1                   # misaligned
+    assert _outproj_call(lib, ws=24) == 1                  # workspace not 16-byte aligned
+    assert _outproj_call(lib, ws=None) == 1
+    assert _outproj_call(lib, ws_bytes=1 << 20) == 1       # too small for 64 rows
+    assert "workspace" in lib.gdn_last_error_string().decode()
+    assert _outproj_call(lib, m=0) == 0                    # nothing to do, nothing launched
+
+
+def test_out_proj_python_gate():
+    from engine.kernels.in_proj import fused_out_proj_supported
+    assert fused_out_proj_supported(4096, 2048) and fused_out_proj_supported(2048, 1024)
+    assert not fused_out_proj_supported(4000, 2048) and not fused_out_proj_supported(4096, 2000)
+    assert not fused_out_proj_supported(16384, 2048)

@@ -1,7 +1,8 @@
 """GPU parity of the fused decode input projections (gdn_in_proj_decode:
-four projections + causal conv update) with the CPU oracle, with the
-unfused GPU path, under graph capture, and inside the GDN layer against
-HF's module (a small layer and one at the model's shapes).
+four projections + causal conv update) and of the decode output projection
+(gdn_out_proj_decode) with the CPU oracle, with the unfused / hipBLASLt GPU
+path, under graph capture, and inside the GDN layer against HF's module (a
+small layer and one at the model's shapes).
 
 Tolerances: bf16 outputs |y - y_ref| <= 2e-2 * max(1, |y_ref|) (the north
 star's 2e-2 abs bound, widened to one bf16 ulp for |y| > 1); window taps
@@ -174,9 +175,11 @@ def test_layer_decode_takes_the_fused_kernel_and_matches_hf(monkeypatch):
     layer.load_state_dict(ref.state_dict())
     layer = layer.to(DEV, torch.bfloat16)
 
-    calls = []
+    calls, out_calls = [], []
     real = gdn_layer.gdn_in_proj_decode
     monkeypatch.setattr(gdn_layer, "gdn_in_proj_decode", lambda *a, **k: calls.append(1) or real(*a, **k))
+    real_out = gdn_layer.gdn_out_proj_decode
+    monkeypatch.setattr(gdn_layer, "gdn_out_proj_decode", lambda *a, **k: out_calls.append(1) or real_out(*a, **k))
 
     pools = GDNSlotPools.allocate([0], 6, conv_dim=2 * 2 * 128 + 4 * 128, num_v_heads=4, device=torch.device(DEV))
     cache = types.SimpleNamespace(gdn_slot_pools=pools)
@@ -201,7 +204,7 @@ def test_layer_decode_takes_the_fused_kernel_and_matches_hf(monkeypatch):
             y = gated_delta_net_forward(layer, x.to(DEV, torch.bfloat16), cache_params=cache)
             for r, c in enumerate(hf_caches):
                 assert close(y[r:r + 1], ref(x[r:r + 1], cache_params=c)), r
-    assert len(calls) == 3
+    assert len(calls) == 3 and len(out_calls) == 3
     conv_pool, rec_pool = pools.layer(0)
     for s, c in zip(slots, hf_caches):
         assert gdn.state_rel_err(np64(rec_pool[s])[None], np64(c.layers[0].recurrent_states[0])) < 1e-2
@@ -229,9 +232,11 @@ def test_layer_decode_at_model_shapes_takes_the_fused_kernel(monkeypatch):
     layer = hf.Qwen3_5MoeGatedDeltaNet(cfg, layer_idx=0).eval()
     layer.load_state_dict(ref.state_dict())
     layer = layer.to(DEV, torch.bfloat16)
-    calls = []
+    calls, out_calls = [], []
     real = gdn_layer.gdn_in_proj_decode
     monkeypatch.setattr(gdn_layer, "gdn_in_proj_decode", lambda *a, **k: calls.append(1) or real(*a, **k))
+    real_out = gdn_layer.gdn_out_proj_decode
+    monkeypatch.setattr(gdn_layer, "gdn_out_proj_decode", lambda *a, **k: out_calls.append(1) or real_out(*a, **k))
 
     pools = GDNSlotPools.allocate([0], 4, conv_dim=2 * 16 * 128 + 32 * 128, num_v_heads=32, device=torch.device(DEV))
     cache = types.SimpleNamespace(gdn_slot_pools=pools)
@@ -255,4 +260,65 @@ def test_layer_decode_at_model_shapes_takes_the_fused_kernel(monkeypatch):
             y = gated_delta_net_forward(layer, x.to(DEV, torch.bfloat16), cache_params=cache)
             for r, c in enumerate(hf_caches):
                 assert close(y[r:r + 1], ref(x[r:r + 1], cache_params=c)), (step, r)
-    assert len(calls) == 2
+    assert len(calls) == 2 and len(out_calls) == 2
+
+
+def run_out(x, w):
+    from engine.kernels.in_proj import gdn_out_proj_decode
+    return gdn_out_proj_decode(x, w)
+
+
+@pytest.mark.parametrize("m,k,n", [(64, 4096, 2048), (1, 4096, 2048), (5, 4096, 2048), (100, 4096, 2048),
+                                   (256, 4096, 2048), (3, 2048, 1024), (7, 512, 64), (9, 1536, 128)])
+def test_out_proj_matches_oracle(m, k, n):
+    """Against the exact sum: one bf16 ulp plus the fp32 summation error."""
+    print(f"out_proj_decode oracle case M={m} K={k} N={n}", flush=True)
+    gen = torch.Generator().manual_seed(90 + m + n)
+    x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(DEV)
+    w = (0.02 * torch.randn(n, k, generator=gen)).to(torch.bfloat16).to(DEV)
+    y = run_out(x, w)
+    assert y.shape == (m, n) and y.dtype == torch.bfloat16
+    ref = proj.out_proj(np64(x), np64(w))
+    assert bf16_close(y, ref)
+    assert tap_close(np64(y), ref, x, w)
+
+
+def test_out_proj_matches_hipblaslt_and_is_deterministic():
+    """torch F.linear (hipBLASLt) to the bf16 bound; repeated calls, also
+    after calls of other shapes on the same workspace, give the same bits;
+    a strided x view gives the same bits as its contiguous copy."""
+    import torch.nn.functional as F
+    gen = torch.Generator().manual_seed(91)
+    x = torch.randn(64, 4096, generator=gen).to(torch.bfloat16).to(DEV)
+    w = (0.02 * torch.randn(2048, 4096, generator=gen)).to(torch.bfloat16).to(DEV)
+    y = run_out(x, w)
+    assert bf16_close(y, np64(F.linear(x, w)))
+    run_out(x[:5], w)
+    run_out(torch.randn(300, 4096, generator=gen).to(torch.bfloat16).to(DEV), w)
+    assert torch.equal(run_out(x, w), y)
+    wide = torch.zeros(64, 4160, dtype=torch.bfloat16, device=DEV)
+    wide[:, :4096] = x
+    assert torch.equal(run_out(wide[:, :4096], w), y)
+    assert torch.equal(run_out(x[:, None], w)[:, 0], y)
+
+
+def test_out_proj_graph_replays_match_eager():
+    gen = torch.Generator().manual_seed(92)
+    w = (0.02 * torch.randn(2048, 4096, generator=gen)).to(torch.bfloat16).to(DEV)
+    static_x = torch.zeros(48, 4096, dtype=torch.bfloat16, device=DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run_out(static_x, w)  # warm-up (and the workspace) outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = run_out(static_x, w)
+    for step in range(3):
+        x = torch.randn(48, 4096, generator=gen).to(torch.bfloat16).to(DEV)
+        eager = run_out(x, w)
+        torch.cuda.synchronize()
+        static_x.copy_(x)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), step

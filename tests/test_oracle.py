@@ -354,3 +354,34 @@ def test_in_proj_decode_is_the_matmul_then_the_conv_update():
         assert np.allclose(b[r], [sum(x[r, i] * wb[j, i] for i in range(k)) for j in range(2)], atol=1e-12)
         assert np.allclose(a[r], [sum(x[r, i] * wa[j, i] for i in range(k)) for j in range(2)], atol=1e-12)
 
+
+def test_out_proj_matches_hf_module_on_cpu():
+    """HF's out_proj module (bf16 weights, bf16 output) against the exact sum
+    rounded to bf16: equal up to the fp32 summation of the module (one ulp
+    of the rounding plus 2^-16 of the terms' magnitudes)."""
+    import torch
+    from transformers.models.qwen3_5_moe import modeling_qwen3_5_moe as hf
+    from transformers.models.qwen3_5_moe.configuration_qwen3_5_moe import Qwen3_5MoeTextConfig
+    cfg = Qwen3_5MoeTextConfig(hidden_size=64, num_hidden_layers=1, layer_types=["linear_attention"],
+                               linear_num_key_heads=2, linear_num_value_heads=4, linear_key_head_dim=16,
+                               linear_value_head_dim=32, linear_conv_kernel_dim=4)
+    torch.manual_seed(65)
+    layer = hf.Qwen3_5MoeGatedDeltaNet(cfg, layer_idx=0).eval().to(torch.bfloat16)
+    x = torch.randn(5, 1, 128).to(torch.bfloat16)
+    with torch.no_grad():
+        y_hf = layer.out_proj(x)[:, 0]
+    f = lambda t: t.detach().double().numpy()
+    w = f(layer.out_proj.weight)
+    assert w.shape == (64, 128)
+    ref = proj.out_proj(f(x[:, 0]), w)
+    scale = np.abs(f(x[:, 0])) @ np.abs(w).T
+    assert (np.abs(proj.round_bf16(ref) - f(y_hf)) <= 2.0 ** -7 * np.abs(ref) + 2.0 ** -16 * scale).all()
+
+
+def test_out_proj_is_the_explicit_sum():
+    rng = np.random.default_rng(66)
+    x, w = rng.standard_normal((3, 7)), rng.standard_normal((5, 7))
+    y = proj.out_proj(x, w)
+    for r in range(3):
+        for c in range(5):
+            assert abs(y[r, c] - sum(x[r, i] * w[c, i] for i in range(7))) < 1e-12
