@@ -200,6 +200,86 @@ def bench_prefill(torch, reps=20, warmup=3, repeat_qk=False):
                      "frac": flop / per / MFMA_BF16_PEAK, "flop_per_call": flop}}
 
 
+def bench_varlen(torch, reps=10):
+    """Configuration 3: 16 packed sequences (lengths U{128..2048}, seeded) as
+    HF's layer runs them after the input projections: the causal conv + SiLU
+    over the packed [sum L, 8192] projection with cu_seqlens (windows from
+    zero), q|k|v as strided views of its output, then the chunk prefill with
+    cu_seqlens, per-sequence initial states [16, 32, 128, 128] and final
+    states out.  Algorithmic units as configurations 2 and the conv."""
+    from engine import configs
+    from engine.kernels import causal_conv1d_fn, chunk_gated_delta_rule
+
+    c = configs.config3()
+    dev = torch.device("cuda", 0)
+    cu = c["cu_seqlens"].to(dev)
+    x, w, g, beta, h0 = (c[k].to(dev) for k in ("x", "conv_w", "g", "beta", "h0"))
+    lens = (c["cu_seqlens"][1:] - c["cu_seqlens"][:-1]).tolist()
+    total = int(sum(lens))
+    conv_out = [None]
+
+    def conv():
+        conv_out[0] = causal_conv1d_fn(x, w, None, activation="silu", cu_seqlens=cu)
+        return conv_out[0]
+
+    def gdn():
+        q, k, v = configs.split_qkv(conv_out[0])
+        return chunk_gated_delta_rule(q, k, v, g, beta, initial_state=h0, output_final_state=True,
+                                      use_qk_l2norm_in_kernel=True, cu_seqlens=cu)
+
+    conv()
+    t_conv = _time(torch, conv, reps)
+    t_gdn = _time(torch, gdn, reps)
+    t_all = _time(torch, lambda: (conv(), gdn()), reps)
+    flop = PREFILL_FLOP_PER_CHUNK_HEAD * 32 * sum((n + 63) // 64 for n in lens)
+    conv_bytes = total * 8192 * 2 * 2
+    gdn_bytes = total * (16 * 128 * 2 * 2 + 32 * 128 * 2 * 2 + 32 * 4 * 2) + 2 * 16 * 2 * 2 ** 20
+    return {"config": f"configuration 3: 16 sequences, sum L = {total}, conv (8192 channels, SiLU) + chunk "
+                      "prefill with cu_seqlens, h0 in, final states out",
+            "tok_per_s": total / t_all, "us": t_all * 1e6, "conv_us": t_conv * 1e6, "gdn_us": t_gdn * 1e6,
+            "gdn_mfma": {"achieved": flop / t_gdn / 1e12, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+                         "frac": flop / t_gdn / MFMA_BF16_PEAK, "flop": flop},
+            "conv_hbm": {"achieved": conv_bytes / t_conv / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                         "frac": conv_bytes / t_conv / HBM_PEAK, "bytes": conv_bytes},
+            "gdn_bytes": gdn_bytes}
+
+
+def bench_spec_verify(torch, reps=20):
+    """Configuration 4: a speculative verify step of B=32 sequences x T=4
+    tokens on a 64-slot fp32 pool (the recurrence reading each slot's state
+    and writing all four per-token states as snapshots, the pool untouched),
+    then the commit of each sequence's accepted snapshot into its slot.
+    Algorithmic bytes: states read 64 MiB + snapshots written 256 MiB +
+    commit 64 MiB read + 64 MiB written = 469,762,048 B (+ q, k, v, o)."""
+    from engine import configs
+    from engine.kernels import fused_recurrent_gated_delta_rule, gdn_state_commit
+
+    c = configs.config4()
+    dev = torch.device("cuda", 0)
+    q, k, v, g, beta = (c[x].to(dev) for x in ("q", "k", "v", "g", "beta"))
+    pool, slots, acc = c["pool"].to(dev), c["slots"].to(dev), c["accepted"].to(dev)
+    b, t = q.shape[:2]
+    snaps = torch.empty(b, t, 32, 128, 128, device=dev)
+
+    def verify():
+        return fused_recurrent_gated_delta_rule(q, k, v, g, beta, initial_state=pool, ssm_state_indices=slots,
+                                                snapshots=snaps, use_qk_l2norm_in_kernel=True)
+
+    def commit():
+        return gdn_state_commit(pool, slots, snaps, acc)
+
+    verify()
+    t_v, t_c = _time(torch, verify, reps), _time(torch, commit, reps)
+    state = 32 * 128 * 128 * 4
+    v_bytes, c_bytes = b * state + b * t * state, 2 * b * state
+    return {"config": "configuration 4: B=32, T=4 verify on a 64-slot fp32 pool, snapshots [32, 4, 32, 128, 128], "
+                      "accepted lengths U{1..4}, commit",
+            "verify_us": t_v * 1e6, "commit_us": t_c * 1e6, "tok_per_s": b * t / (t_v + t_c),
+            "verify_hbm": {"achieved": v_bytes / t_v / 1e9, "frac": v_bytes / t_v / HBM_PEAK, "bytes": v_bytes},
+            "commit_hbm": {"achieved": c_bytes / t_c / 1e9, "frac": c_bytes / t_c / HBM_PEAK, "bytes": c_bytes},
+            "total_bytes": v_bytes + c_bytes, "peak_GBps": HBM_PEAK / 1e9}
+
+
 def _time(torch, fn, reps, warmup=3):
     for _ in range(warmup):
         fn()
@@ -577,6 +657,8 @@ def main():
             out["prefill_qk_repeated"] = bench_prefill(torch, repeat_qk=True)
         if not args.no_layer_glue:
             out["layer_glue"] = bench_layer_glue(torch)
+        out["varlen"] = bench_varlen(torch)
+    out["spec_verify"] = bench_spec_verify(torch)
     if not args.no_conv:
         out["conv_prefill"] = bench_conv_prefill(torch)
     if not args.no_in_proj:

@@ -27,8 +27,8 @@
 //                       two loader waves stream the operand blocks of the
 //                       chunk after next into a double-buffered LDS stage
 //                       with buffer_load ... lds.
-// Inputs longer than one segment (64 chunks) run prep / scan per segment,
-// the next segment's prep on a side stream.
+// Inputs longer than one segment (512 chunks) run prep / scan per segment,
+// one segment after the other on the caller's stream.
 // Precision (checked against an fp64 restatement at T=4096): the state is fed
 // to MFMA as bf16, U stays fp32 (it initialises the V' accumulator), the state
 // increment K^T V'' uses V'' split into bf16 hi + lo.
@@ -42,7 +42,6 @@
 // by conversion to bf16 alone (in the scan, between waves, through LDS
 // without any reordering).
 #include <algorithm>
-#include <mutex>
 #include <type_traits>
 
 #include "gdn_common.h"
@@ -896,21 +895,22 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_kernel(ChunkArgs a
   }
 }
 
-// Chunks per prep + scan segment.  One segment's operand workspace (about
-// 2.3 MiB per chunk at 32 v-heads, so ~150 MB) stays resident in the 256 MB
-// Infinity Cache between the producer and the consumer.  Longer inputs run as
-// several segments with the next segment's prep on a side stream; a
-// cross-stream hand-off costs ~10 us on MI355X, so segments are kept long
-// enough (a 64-chunk scan takes ~120 us) for that to be small.
-constexpr int SEG_CHUNKS = 64;
+// Chunks per prep + scan segment: one prep launch produces a segment's
+// operands (about 2.3 MiB per chunk at 32 v-heads, 1.2 GB for 512 chunks)
+// and one scan launch consumes them.  Longer inputs run segment after
+// segment on the caller's stream.  (The next segment's prep on a second
+// stream, overlapping the scan, measured slower: the two kernels cannot share
+// a CU -- the scan holds 138 KiB of LDS -- so the prep takes CUs from the
+// scan's chain; 64-chunk overlapped segments took 700 us at T = 16384 and
+// 3.1 ms at T = 65536, one 256-chunk segment 540 us, and serial 512-chunk
+// segments 2.0 ms.)
+constexpr int SEG_CHUNKS = 512;
 
-// Workspace: the chunk table, the state carried between segments, and the
-// scan operands of one segment of SEG_CHUNKS chunks -- twice when there are
-// several segments, so that the next segment's operands are produced while
-// the current one is scanned.
+// Workspace: the chunk table, the state carried between segments (when
+// there are several) and the scan operands of one segment.
 struct WsLayout {
   size_t chunk_start, carry, total;
-  size_t vh[2], kh[2], Ut[2];  // segment k uses buffer k % 2
+  size_t vh, kh, Ut;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -922,20 +922,12 @@ WsLayout ws_layout(int n_seqs, int64_t seg_chunks, int Hv, int Hk, bool multi) {
   off = align256(off + sizeof(int32_t) * (n_seqs + 1));
   l.carry = off;
   if (multi) off = align256(off + sizeof(float) * static_cast<size_t>(n_seqs) * Hv * DK * DV);
-  for (int b = 0; b < 2; ++b) {
-    if (b == 1 && !multi) {
-      l.vh[1] = l.vh[0];
-      l.kh[1] = l.kh[0];
-      l.Ut[1] = l.Ut[0];
-      break;
-    }
-    l.vh[b] = off;
-    off = align256(off + 16ull * seg_chunks * Hv * NB_VH * 64);
-    l.kh[b] = off;
-    off = align256(off + 16ull * seg_chunks * Hk * NB_KH * 64);
-    l.Ut[b] = off;
-    off = align256(off + sizeof(float) * seg_chunks * Hv * DV * CK);
-  }
+  l.vh = off;
+  off = align256(off + 16ull * seg_chunks * Hv * NB_VH * 64);
+  l.kh = off;
+  off = align256(off + 16ull * seg_chunks * Hk * NB_KH * 64);
+  l.Ut = off;
+  off = align256(off + sizeof(float) * seg_chunks * Hv * DV * CK);
   l.total = off;
   return l;
 }
@@ -943,36 +935,6 @@ WsLayout ws_layout(int n_seqs, int64_t seg_chunks, int Hv, int Hk, bool multi) {
 int64_t max_chunks_of(int n_seqs, int64_t total_tokens, bool varlen, int T) {
   if (!varlen) return static_cast<int64_t>(n_seqs) * ((T + CK - 1) / CK);
   return (total_tokens + CK - 1) / CK + n_seqs;
-}
-
-// Per-device side stream for the segment producer (chunk_prep_kernel), plus a
-// ring of events for the hand-offs.  Created on the first multi-segment call
-// on a device (that call must not be under graph capture) and kept until the
-// process ends.  The stream is non-blocking, so it does not synchronise
-// implicitly with the legacy default stream; default priority.
-constexpr int SIDE_EVENTS = 8;
-struct SideStream {
-  hipStream_t stream = nullptr;
-  hipEvent_t ev[SIDE_EVENTS] = {};
-};
-constexpr int MAX_DEVICES = 64;
-SideStream g_side[MAX_DEVICES];
-std::mutex g_side_mu;
-
-int side_stream(SideStream **out) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
-    return fail(GDN_ERR_LAUNCH, "gdn_chunk_fwd: no current device");
-  SideStream &ss = g_side[dev];
-  if (!ss.stream) {
-    if (hipStreamCreateWithFlags(&ss.stream, hipStreamNonBlocking) != hipSuccess)
-      return fail(GDN_ERR_LAUNCH, "gdn_chunk_fwd: hipStreamCreateWithFlags failed");
-    for (int i = 0; i < SIDE_EVENTS; ++i)
-      if (hipEventCreateWithFlags(&ss.ev[i], hipEventDisableTiming) != hipSuccess)
-        return fail(GDN_ERR_LAUNCH, "gdn_chunk_fwd: hipEventCreateWithFlags failed");
-  }
-  *out = &ss;
-  return GDN_OK;
 }
 
 }  // namespace
@@ -1031,18 +993,12 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
   ChunkArgs a{static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
               q_stride_t, k_stride_t, v_stride_t, gate, h0, h0_idx, h0_rows, hT, hT_idx, hT_rows, o, o_dtype,
               cu_seqlens, n_seqs, T, Hk, Hv, total, scale, l2norm_qk, static_cast<int>(nc), 0, 0,
-              reinterpret_cast<int32_t *>(ws + l.chunk_start), nullptr, nullptr, nullptr,
+              reinterpret_cast<int32_t *>(ws + l.chunk_start), reinterpret_cast<u32x4 *>(ws + l.vh),
+              reinterpret_cast<u32x4 *>(ws + l.kh), reinterpret_cast<float *>(ws + l.Ut),
               reinterpret_cast<float *>(ws + l.carry)};
-  auto use_buffer = [&](int64_t segment) {
-    const int b = static_cast<int>(segment & 1);
-    a.vh = reinterpret_cast<u32x4 *>(ws + l.vh[b]);
-    a.kh = reinterpret_cast<u32x4 *>(ws + l.kh[b]);
-    a.Ut = reinterpret_cast<float *>(ws + l.Ut[b]);
-  };
   auto set_segment = [&](int64_t segment) {
     a.seg_begin = static_cast<int>(segment * seg);
     a.seg_end = static_cast<int>(std::min<int64_t>((segment + 1) * seg, nc));
-    use_buffer(segment);
   };
   auto launch_prep = [&](hipStream_t st) {
     hipLaunchKernelGGL(chunk_prep_kernel, dim3(Hv, static_cast<unsigned>(seg)), dim3(256), 0, st, a);
@@ -1058,41 +1014,15 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (cu_seqlens) hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, s, a);
   const int64_t nseg = seg > 0 ? (nc + seg - 1) / seg : 0;
-  if (nseg <= 1) {  // one segment (or none: empty sequences still pass their state through)
+  if (nseg == 0) {  // only empty sequences: they still pass their state through
     set_segment(0);
-    if (seg > 0) launch_prep(s);
     launch_scan(s);
-    return check_launch(name);
   }
-  // Several segments: segment k + 1 is prepared on the side stream while
-  // segment k is scanned on the caller's stream.  prep(k + 1) writes buffer
-  // (k + 1) % 2, which scan(k - 1) read: it waits for that scan.  Every side
-  // stream operation is followed by an event the caller's stream waits on,
-  // so the caller's stream ends after all of this call's work (and a graph
-  // captured on it contains the side branch).
-  std::lock_guard<std::mutex> lock(g_side_mu);
-  SideStream *side = nullptr;
-  if (const int st = side_stream(&side)) return st;
-  hipEvent_t *ev = side->ev;
-  const int R = SIDE_EVENTS / 2;  // ring of prep-done events ev[0..R) and scan-done events ev[R..2R)
-  int rc = hipEventRecord(ev[0], s) != hipSuccess;  // inputs and chunk table ready
-  rc |= hipStreamWaitEvent(side->stream, ev[0], 0) != hipSuccess;
-  set_segment(0);
-  launch_prep(side->stream);
-  rc |= hipEventRecord(ev[0], side->stream) != hipSuccess;
-  for (int64_t kseg = 0; kseg < nseg; ++kseg) {
-    if (kseg + 1 < nseg) {
-      if (kseg >= 1) rc |= hipStreamWaitEvent(side->stream, ev[R + (kseg - 1) % R], 0) != hipSuccess;
-      set_segment(kseg + 1);
-      launch_prep(side->stream);
-      rc |= hipEventRecord(ev[(kseg + 1) % R], side->stream) != hipSuccess;
-    }
-    rc |= hipStreamWaitEvent(s, ev[kseg % R], 0) != hipSuccess;
+  for (int64_t kseg = 0; kseg < nseg; ++kseg) {  // segment k's scan reads the state carried from k - 1
     set_segment(kseg);
+    launch_prep(s);
     launch_scan(s);
-    rc |= hipEventRecord(ev[R + kseg % R], s) != hipSuccess;
   }
-  if (rc) return fail(GDN_ERR_LAUNCH, "%s: stream event hand-off failed", name);
   return check_launch(name);
 }
 
