@@ -528,7 +528,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
 // ------------------------------------------------------------------ phase B
 
 // sched_group_barrier masks
-constexpr int SG_VALU = 0x2, SG_MFMA = 0x8, SG_VMEM_RD = 0x20, SG_VMEM_WR = 0x40, SG_DS_RD = 0x100;
+constexpr int SG_MFMA = 0x8, SG_DS_RD = 0x100;
 #define GDN_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 #define GDN_GROUP(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
 
