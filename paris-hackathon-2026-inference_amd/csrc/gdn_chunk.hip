@@ -27,8 +27,10 @@
 //                       two loader waves stream the operand blocks of the
 //                       chunk after next into a double-buffered LDS stage
 //                       with buffer_load ... lds.
-// Inputs longer than one segment (512 chunks) run prep / scan per segment,
-// one segment after the other on the caller's stream.
+// Inputs longer than one segment (64 chunks) run prep / scan per segment,
+// one segment after the other on the caller's stream; several sequences
+// (varlen or a batch) are scanned by one workgroup per (v-head, 16 state
+// columns) walking all of them (chunk_scan_persist_kernel).
 // Precision (checked against an fp64 restatement at T=4096): the state is fed
 // to MFMA as bf16, U stays fp32 (it initialises the V' accumulator), the state
 // increment K^T V'' uses V'' split into bf16 hi + lo.
@@ -563,6 +565,7 @@ constexpr int RS_LOADER0 = NB_VH + 4;  // loader 0: v-head region + U blocks; lo
 constexpr int RS_LOADER1 = NB_KH;
 constexpr int SCAN_WAVES = 6;
 constexpr int SCAN_COLS = 16;  // state columns per workgroup
+constexpr int SCAN_PERSIST_BLOCKS = 256;  // one scan workgroup per CU (MI355X: 256 CUs)
 
 struct RowOps {     // one chunk's operands of one compute wave
   u32x4 w[4];       // -W rows 16q.., k-steps 0..3
@@ -656,10 +659,10 @@ __device__ __forceinline__ u32x2 pack4(f32x4 x) {
 // registers of an A operand are those of the transposed B operand, so sb,
 // the V' exchange and the Q and A blocks serve unchanged, and lane (g, r)
 // ends with O[16q + r][4g .. 4g + 3], one 8-byte store.
-template <bool TWO_A, class StoreOut>
+template <bool TWO_A, class StoreOut, class AtState>
 __device__ __forceinline__ void scan_rows_chunk(const RowOps &op, RowOps &nx, const u32x4 *nst, bf16x8 (&sb)[4],
                                                 f32x4 (&S)[2], u32x2 (*xv)[2][64][2], u32x4 (*xs)[64], int q,
-                                                int lane, const StoreOut &store_out) {
+                                                int lane, const StoreOut &store_out, const AtState &at_state) {
   // ---- R1
   f32x4 vp = op.u;
 #pragma unroll
@@ -712,6 +715,7 @@ __device__ __forceinline__ void scan_rows_chunk(const RowOps &op, RowOps &nx, co
     GDN_GROUP(SG_DS_RD, 2);
   }
   GDN_SCHED_FENCE();
+  at_state(S);  // (persistent scan: a sequence that ends here hands over to the next one's initial state)
   xs[q][lane] = __builtin_bit_cast(u32x4, pack_hi(S[0], S[1]));
   lds_barrier();
 
@@ -862,10 +866,11 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_kernel(ChunkArgs a
     // (after the last chunk the "next" reads take the idle buffer's stale contents, unused)
     const u32x4 *nst = stage[(c + 1) & 1];
     auto out = [&](const f32x4 &o) { store_out(o, c); };
+    auto keep = [](f32x4 (&)[2]) {};
     if (q >= 2)
-      scan_rows_chunk<true>(op, nx, nst, sb, S, xv, xs, q, lane, out);
+      scan_rows_chunk<true>(op, nx, nst, sb, S, xv, xs, q, lane, out, keep);
     else
-      scan_rows_chunk<false>(op, nx, nst, sb, S, xv, xs, q, lane, out);
+      scan_rows_chunk<false>(op, nx, nst, sb, S, xv, xs, q, lane, out, keep);
   };
 
   RowOps op0, op1;
@@ -895,16 +900,182 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_kernel(ChunkArgs a
   }
 }
 
+// Persistent scan for several sequences (varlen or a dense batch): one
+// workgroup per (v-head, 16 state columns) walks every chunk of the segment
+// in order, sequence after sequence, instead of one workgroup per
+// (sequence, v-head, columns) paying its start and end for a few chunks each.
+// The loader waves stream the segment's chunks as for one sequence; the
+// compute waves track the sequence of each chunk, and where one ends (after
+// its last state update, before the state exchange) they store its final
+// state and continue from the next one's initial state, loaded into
+// registers a sequence ahead.  Used when (v-heads x column tiles) alone fill
+// the CUs.
+template <bool BF16_OUT>
+__global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_persist_kernel(ChunkArgs a) {
+  __shared__ u32x4 stage[2][RS_BLOCKS * 64];  // 122 KiB
+  __shared__ u32x4 xs[4][64];
+  __shared__ u32x2 xv[3][2][64][2];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = wave & 3;
+  const int g4 = lane >> 4;
+  const int ratio = a.Hv / a.Hk;
+  int ct = blockIdx.x / a.Hv;
+  int h = blockIdx.x % a.Hv;
+  if (a.Hk % 8 == 0) {  // the column tiles and v-heads of one k-head on one XCD
+    int g, m;
+    xcd_group_order(blockIdx.x, ratio * (DV / SCAN_COLS), &g, &m);
+    ct = m % (DV / SCAN_COLS);
+    h = g * ratio + m / (DV / SCAN_COLS);
+  }
+  const int hk = h / ratio;
+  const int col = 16 * ct + (lane & 15);
+  const int64_t kv = static_cast<int64_t>(DK) * DV;
+  const int row0 = 32 * q;
+  auto state_at = [&](float *base, int64_t row) { return base + (row * a.Hv + h) * kv + col; };
+  auto load_state = [&](const float *src, f32x4 (&S)[2]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) S[t][e] = src ? src[(row0 + 16 * t + 4 * g4 + e) * DV] : 0.f;
+  };
+  auto store_state = [&](float *dst, const f32x4 (&S)[2]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dst[(row0 + 16 * t + 4 * g4 + e) * DV] = S[t][e];
+  };
+  auto in_row = [&](int n) -> int64_t { return a.h0 ? uniform64(pool_row(a.h0_idx, n, a.h0_rows)) : -1; };
+  auto out_row = [&](int n) -> int64_t { return a.hT ? uniform64(pool_row(a.hT_idx, n, a.hT_rows)) : -1; };
+  auto init_src = [&](int n) -> const float * {
+    const int64_t r = in_row(n);
+    return r >= 0 ? state_at(const_cast<float *>(a.h0), r) : nullptr;
+  };
+
+  const int lo = a.seg_begin, hi = min(a.seg_end, chunk_start_at(a, a.n_seqs));
+  if (wave < 4 && a.seg_begin == 0) {  // empty sequences pass their initial state through
+    for (int m = 0; m < a.n_seqs; ++m) {
+      if (chunk_start_at(a, m) != chunk_start_at(a, m + 1)) continue;
+      const int64_t orow = out_row(m);
+      if (orow < 0) continue;
+      f32x4 Sx[2];
+      load_state(init_src(m), Sx);
+      store_state(state_at(a.hT, orow), Sx);
+    }
+  }
+  if (lo >= hi) return;
+  const int nch = hi - lo;
+  if (wave >= 4) {
+    if (wave == 4)
+      scan_rows_loader<0>(stage, nch, ct, lane, a, 0, h, hk);
+    else
+      scan_rows_loader<1>(stage, nch, ct, lane, a, 0, h, hk);
+    return;
+  }
+
+  // the sequence of chunk lo: the last one starting at or before it (non-empty)
+  int n;
+  {
+    int l = 0, r = a.n_seqs;
+    while (r - l > 1) {
+      const int mid = (l + r) >> 1;
+      if (chunk_start_at(a, mid) <= lo) l = mid; else r = mid;
+    }
+    n = __builtin_amdgcn_readfirstlane(l);
+  }
+  int cs = __builtin_amdgcn_readfirstlane(chunk_start_at(a, n));
+  int ce = __builtin_amdgcn_readfirstlane(chunk_start_at(a, n + 1));
+  int64_t s0;
+  int slen;
+  seq_bounds(a, n, &s0, &slen);
+  s0 = uniform64(s0);
+  slen = __builtin_amdgcn_readfirstlane(slen);
+  // the next non-empty sequence after m (n_seqs: none)
+  auto next_seq = [&](int m) {
+    int k = m + 1;
+    while (k < a.n_seqs && chunk_start_at(a, k) == chunk_start_at(a, k + 1)) ++k;
+    return __builtin_amdgcn_readfirstlane(k);
+  };
+  float *carry = a.carry;
+  f32x4 S[2], Sn[2];
+  load_state(lo == cs ? init_src(n) : state_at(carry, n), S);
+  int nn = ce < hi ? next_seq(n) : a.n_seqs;
+  load_state(nn < a.n_seqs ? init_src(nn) : nullptr, Sn);
+
+  typedef typename std::conditional<BF16_OUT, uint16_t, float>::type OT;
+  const int64_t ostep = static_cast<int64_t>(a.Hv) * DV;
+  const int voff = static_cast<int>(((16 * q + (lane & 15)) * ostep + h * DV + 16 * ct + 4 * g4) * sizeof(OT));
+  bf16x8 sb[4];
+  auto chunk = [&](const RowOps &op, RowOps &nx, int c) {
+    const u32x4 *nst = stage[(c + 1) & 1];
+    const int j = lo + c;  // global chunk, in sequence n
+    const int64_t toff = static_cast<int64_t>(j - cs) * CK;
+    const int rows = static_cast<int>(min<int64_t>(CK, slen - toff));
+    OT *base = static_cast<OT *>(a.o) + (s0 + toff) * ostep;
+    auto out = [base, rows, ostep, voff](const f32x4 &o) {
+      const auto r = __builtin_amdgcn_make_buffer_rsrc(base, 0, static_cast<int>(rows * ostep * sizeof(OT)), BUF_DWORD3);
+      if constexpr (BF16_OUT)
+        __builtin_amdgcn_raw_buffer_store_b64(pack4(o), r, voff, 0, 0);
+      else
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), r, voff, 0, 0);
+    };
+    auto at_state = [&](f32x4 (&St)[2]) {
+      if (j + 1 == ce && j + 1 < hi) {  // sequence n ends here, sequence nn starts with the next chunk
+        const int64_t orow = out_row(n);
+        if (orow >= 0) store_state(state_at(a.hT, orow), St);
+        St[0] = Sn[0];
+        St[1] = Sn[1];
+        n = nn;
+        cs = __builtin_amdgcn_readfirstlane(chunk_start_at(a, n));
+        ce = __builtin_amdgcn_readfirstlane(chunk_start_at(a, n + 1));
+        seq_bounds(a, n, &s0, &slen);
+        s0 = uniform64(s0);
+        slen = __builtin_amdgcn_readfirstlane(slen);
+        nn = ce < hi ? next_seq(n) : a.n_seqs;
+        load_state(nn < a.n_seqs ? init_src(nn) : nullptr, Sn);
+      }
+    };
+    if (q >= 2)
+      scan_rows_chunk<true>(op, nx, nst, sb, S, xv, xs, q, lane, out, at_state);
+    else
+      scan_rows_chunk<false>(op, nx, nst, sb, S, xv, xs, q, lane, out, at_state);
+  };
+
+  RowOps op0, op1;
+  xs[q][lane] = __builtin_bit_cast(u32x4, pack_hi(S[0], S[1]));
+  lds_barrier();  // state exchange; chunk 0 staged
+#pragma unroll
+  for (int s = 0; s < 4; ++s) sb[s] = __builtin_bit_cast(bf16x8, xs[s][lane]);
+  read_rows<0>(op0, stage[0], q, lane);
+  read_rows<1>(op0, stage[0], q, lane);
+  read_rows<2>(op0, stage[0], q, lane);
+  read_rows<3>(op0, stage[0], q, lane);
+  lds_barrier();  // chunk 0 read: its buffer may be refilled
+  for (int c = 0; c < nch; c += 2) {
+    chunk(op0, op1, c);
+    if (c + 1 >= nch) break;
+    chunk(op1, op0, c + 1);
+  }
+  // the last sequence: finished here, or continued by the next segment
+  if (ce <= hi) {
+    const int64_t orow = out_row(n);
+    if (orow >= 0) store_state(state_at(a.hT, orow), S);
+  } else {
+    store_state(state_at(carry, n), S);
+  }
+}
+
 // Chunks per prep + scan segment: one prep launch produces a segment's
-// operands (about 2.3 MiB per chunk at 32 v-heads, 1.2 GB for 512 chunks)
-// and one scan launch consumes them.  Longer inputs run segment after
-// segment on the caller's stream.  (The next segment's prep on a second
-// stream, overlapping the scan, measured slower: the two kernels cannot share
-// a CU -- the scan holds 138 KiB of LDS -- so the prep takes CUs from the
-// scan's chain; 64-chunk overlapped segments took 700 us at T = 16384 and
-// 3.1 ms at T = 65536, one 256-chunk segment 540 us, and serial 512-chunk
-// segments 2.0 ms.)
-constexpr int SEG_CHUNKS = 512;
+// operands (about 2.3 MiB per chunk at 32 v-heads: 146 MiB for 64 chunks,
+// which stay in the 256 MB Infinity Cache until the scan reads them) and one
+// scan launch consumes them; longer inputs run segment after segment on the
+// caller's stream.  Measured (T = 16384 / 65536 / configuration 3): serial
+// 64-chunk segments 478 us / 1.78 ms / 431 us; 96, 128 and 512 chunks, whose
+// operands spill to HBM, 532-560 us / 2.0-2.2 ms / 490-518 us; the next
+// segment's prep on a second stream beside the scan 700 us / 3.1 ms (the two
+// kernels cannot share a CU -- the scan holds 138 KiB of LDS -- so the prep
+// takes CUs from the scan's chain).
+constexpr int SEG_CHUNKS = 64;
 
 // Workspace: the chunk table, the state carried between segments (when
 // there are several) and the scan operands of one segment.
@@ -987,7 +1158,10 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
   if (reinterpret_cast<uintptr_t>(workspace) % 256)
     return fail(GDN_ERR_WORKSPACE, "%s: workspace must be 256-byte aligned", name);
   if (nc > 65535) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: %lld chunks exceed one launch", name, (long long)nc);
-  const int64_t scan_blocks = static_cast<int64_t>(n_seqs) * Hv * (DV / SCAN_COLS);
+  // several sequences: the persistent scan once its (v-head, column tile)
+  // workgroups fill the CUs without spreading the sequences over the grid
+  const bool persist = n_seqs > 1 && static_cast<int64_t>(Hv) * (DV / SCAN_COLS) >= SCAN_PERSIST_BLOCKS;
+  const int64_t scan_blocks = static_cast<int64_t>(persist ? 1 : n_seqs) * Hv * (DV / SCAN_COLS);
   if (scan_blocks > 0x7fffffff) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: grid too large", name);
   char *ws = static_cast<char *>(workspace);
   ChunkArgs a{static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
@@ -1004,6 +1178,15 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
     hipLaunchKernelGGL(chunk_prep_kernel, dim3(Hv, static_cast<unsigned>(seg)), dim3(256), 0, st, a);
   };
   auto launch_scan = [&](hipStream_t st) {
+    if (persist) {
+      if (o_dtype == GDN_DTYPE_BF16)
+        hipLaunchKernelGGL((chunk_scan_persist_kernel<true>), dim3(static_cast<unsigned>(scan_blocks)),
+                           dim3(64 * SCAN_WAVES), 0, st, a);
+      else
+        hipLaunchKernelGGL((chunk_scan_persist_kernel<false>), dim3(static_cast<unsigned>(scan_blocks)),
+                           dim3(64 * SCAN_WAVES), 0, st, a);
+      return;
+    }
     if (o_dtype == GDN_DTYPE_BF16)
       hipLaunchKernelGGL((chunk_scan_kernel<true>), dim3(static_cast<unsigned>(scan_blocks)),
                          dim3(64 * SCAN_WAVES), 0, st, a);

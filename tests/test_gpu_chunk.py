@@ -158,25 +158,26 @@ def test_state_passing_split_on_gpu():
 
 
 def test_segments_equal_split_calls():
-    """Inputs over 512 chunks run as several prep + scan segments, the state
-    carried between them in fp32: the same bits as splitting the input at
-    the segment boundary into two calls threaded through h0 / hT, dense and
-    varlen (the second sequence spans the boundary)."""
-    print("chunk segments: dense T=33000", flush=True)
-    c = configs.config2(seed=21, t=33000)
+    """Inputs over 64 chunks run as several prep + scan segments, the state
+    carried between them in fp32: the same bits as splitting the input at a
+    segment boundary into two calls threaded through h0 / hT, dense and
+    varlen (both sequences span a segment boundary; several sequences take
+    the persistent scan, which walks them in one workgroup)."""
+    print("chunk segments: dense T=9000", flush=True)
+    c = configs.config2(seed=21, t=9000)
     q, k, v, g, beta = (c[x].to(DEV) for x in ("q", "k", "v", "g", "beta"))
     h0 = torch.randn(1, 32, 128, 128, generator=torch.Generator().manual_seed(22)).mul(0.1).to(DEV)
     kw = dict(output_final_state=True, use_qk_l2norm_in_kernel=True)
     o, s = chunk_gated_delta_rule(q, k, v, g, beta, initial_state=h0, **kw)
-    cut = 512 * 64
+    cut = 64 * 64
     o1, s1 = chunk_gated_delta_rule(q[:, :cut], k[:, :cut], v[:, :cut], g[:, :cut], beta[:, :cut],
                                     initial_state=h0, **kw)
     o2, s2 = chunk_gated_delta_rule(q[:, cut:], k[:, cut:], v[:, cut:], g[:, cut:], beta[:, cut:],
                                     initial_state=s1, **kw)
     assert torch.equal(o[:, :cut], o1) and torch.equal(o[:, cut:], o2) and torch.equal(s, s2)
 
-    print("chunk segments: varlen 20000 + 15000", flush=True)
-    lens = [20000, 15000]
+    print("chunk segments: varlen 5000 + 4000", flush=True)
+    lens = [5000, 4000]
     cu = torch.tensor([0, lens[0], sum(lens)], dtype=torch.int32, device=DEV)
     c = configs.config2(seed=23, t=sum(lens))
     q, k, v, g, beta = (c[x].to(DEV) for x in ("q", "k", "v", "g", "beta"))
