@@ -13,10 +13,8 @@
  *     allocates device memory or synchronises the device or the stream:
  *     every kernel is enqueued on `stream` (a hipStream_t passed as void*;
  *     NULL is the null stream), so calls are safe to record into a HIP graph.
- *     The only state kept between calls: a chunk prefill longer than one
- *     segment (64 chunks) runs its producer on a per-device side stream,
- *     created with a ring of events by the first such call on the device
- *     (which must not itself be under graph capture) and kept until exit.
+ *     The library keeps no state between calls and creates no streams or
+ *     events (apart from the thread-local error string).
  *   - The return value is a gdn_status_t.  On failure nothing was launched
  *     and gdn_last_error_string() (thread-local) says why.
  *   - Token-major activations: element (token t, head h, dim d) of q/k/v lives
