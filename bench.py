@@ -164,6 +164,47 @@ def bench_decode(torch, steps, warmup, n_pools):
     return dict(tokens=b, steps=steps, kernel_s=kernel_s, eager_wall=eager_wall, graph_wall=graph_wall)
 
 
+def bench_decode_batches(torch, batches=(1, 4, 16, 64), reps=50):
+    """The decode step of configuration 1 at smaller batches (the first B
+    rows of its inputs and slots; pool of 128 slots, 4 pools rotating so that
+    the touched states come from HBM): time per step from a HIP graph of 20
+    steps (below B = 64 an eager step is bound by the host's launch path,
+    about 20 us, not by the GPU), also eager, and the HBM fraction of the
+    state bytes (2 x B x 2 MiB read + written)."""
+    from engine import configs
+    from engine.kernels import fused_recurrent_gated_delta_rule
+
+    c = configs.config1()
+    dev = torch.device("cuda", 0)
+    q, k, v, g, beta = (c[x].to(dev) for x in ("q", "k", "v", "g", "beta"))
+    slots = c["slots"].to(dev)
+    pools = [c["pool"].to(dev)] + [torch.randn_like(c["pool"]).to(dev).mul_(0.1) for _ in range(3)]
+    out = {}
+    for b in batches:
+        i = [0]
+
+        def step():
+            i[0] += 1
+            return fused_recurrent_gated_delta_rule(q[:b], k[:b], v[:b], g[:b], beta[:b],
+                                                    initial_state=pools[i[0] % 4], ssm_state_indices=slots[:b],
+                                                    inplace_final_state=True, use_qk_l2norm_in_kernel=True)
+
+        t_eager = _time(torch, step, reps)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        gph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gph):
+            for _ in range(20):
+                step()
+        t = _time(torch, gph.replay, max(1, reps // 10)) / 20
+        byts = 2 * b * 32 * 128 * 128 * 4
+        out[f"B{b}"] = {"us": t * 1e6, "tok_per_s": b / t, "frac": byts / t / HBM_PEAK, "eager_us": t_eager * 1e6}
+    return out
+
+
 def bench_prefill(torch, reps=20, warmup=3, repeat_qk=False):
     """Configuration 2.  With repeat_qk, q and k arrive repeated to the 32 v-heads
     (HF's repeat_interleave before the call), the layout the reference's boundary
@@ -651,6 +692,7 @@ def main():
                      "kernel": "gdn::recurrent_kernel<32, 64>", "kernel_us": d["kernel_s"] * 1e6,
                      "bytes_per_launch": DECODE_BYTES},
     }
+    out["decode_batches"] = bench_decode_batches(torch)
     if not args.no_prefill:
         out["prefill"] = bench_prefill(torch)
         if not args.no_prefill_repeated:
