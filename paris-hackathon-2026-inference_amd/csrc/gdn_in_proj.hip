@@ -52,6 +52,7 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 constexpr int IP_WAVES = 16;         // waves per workgroup
 constexpr int IP_ROWS = 64;          // hidden rows per workgroup (4 row tiles)
 constexpr int IP_OOB = 0x40000000;   // buffer offset past every conv pool: loads read 0, nothing stored
+constexpr int IP_GEMV_ROWS = 2;      // up to this many rows: in_proj_gemv_kernel (more spill at K = 2048)
 
 // Workgroup shape: CG column groups of 16 x KQ parts of K (CG KQ = 16
 // waves); a wave holds KS k-steps (of 32) of weights; the hidden rows reach
@@ -300,6 +301,113 @@ __global__ __launch_bounds__(64 * IP_WAVES) void in_proj_decode_kernel(InProjArg
   }
 }
 
+// One or two rows (the smallest decode batches): the projection is a GEMV stream.
+// Workgroup = 16 waves over 64 columns of one matrix (the same column
+// blocks as the MFMA kernel); wave w takes columns 4 w .. 4 w + 3 and reads
+// each of its weight rows as K / 512 contiguous 1 KiB loads (lane l: 16
+// bytes at 16 l of every KiB), all issued at the start; the rows of x sit in
+// registers in the same lane layout.  Each lane sums its products in fp32,
+// a wave reduction gives the dot products, and lane c + 4 m writes (row m,
+// column c), through the same conv epilogue as the MFMA kernel.
+template <int MR, int KB>  // MR rows (1, 2); KB = K / 512
+__global__ __launch_bounds__(64 * IP_WAVES) void in_proj_gemv_kernel(InProjArgs a) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int mat, col;
+  const int bid = blockIdx.x;
+  if (bid < a.blocks_qkv) {
+    mat = 0;
+    col = bid * 64 + 4 * wave;
+  } else if (bid < a.blocks_qkv + a.blocks_z) {
+    mat = 1;
+    col = (bid - a.blocks_qkv) * 64 + 4 * wave;
+  } else {
+    mat = 2 + (wave >> 3);
+    col = 4 * (wave & 7);
+  }
+  mat = __builtin_amdgcn_readfirstlane(mat);
+  col = __builtin_amdgcn_readfirstlane(col);
+  const uint16_t *wmat = mat == 0 ? a.w[0] : mat == 1 ? a.w[1] : mat == 2 ? a.w[2] : a.w[3];
+  const int nmat = mat == 0 ? a.n[0] : mat == 1 ? a.n[1] : mat == 2 ? a.n[2] : a.n[3];
+  if (col >= nmat) return;  // (b / a narrower than 32 columns; nmat is a multiple of 4)
+  const int K = KB * 512;
+  const auto rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(wmat) + static_cast<int64_t>(col) * K, 0,
+                                                    4 * K * 2, BUF_DWORD3);
+  const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.x), 0,
+                                                    static_cast<int>(((a.M - 1) * a.xs + K) * 2), BUF_DWORD3);
+  u32x4_t wv[4][KB], xv[MR][KB];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+      xv[m][i] = __builtin_amdgcn_raw_buffer_load_b128(rx, static_cast<int>((m * a.xs + 512 * i + 8 * lane) * 2), 0, 0);
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+      wv[c][i] = __builtin_amdgcn_raw_buffer_load_b128(rw, (c * K + 512 * i + 8 * lane) * 2, 0, 0);
+  float dot[4][MR];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < KB; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t wp = wv[c][i][e], xp = xv[m][i][e];
+          s += bf16_bits_to_f32(wp & 0xffffu) * bf16_bits_to_f32(xp & 0xffffu);
+          s += bf16_bits_to_f32(wp >> 16) * bf16_bits_to_f32(xp >> 16);
+        }
+      dot[c][m] = wave_sum(s);
+    }
+  // lane c + 4 m finishes (row m, column col + c)
+  const int c = lane & 3, m = lane >> 2;
+  if (m >= MR || m >= a.M) return;
+  float o = 0.f;
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+    for (int mm = 0; mm < MR; ++mm)
+      if (cc == c && mm == m) o = dot[cc][mm];
+  const int n = col + c;
+  if (mat == 0) {
+    const int64_t id = a.idx ? a.idx[m] : m;  // pool_row's rule
+    const bool live = id >= 0 && id < a.rows;
+    uint16_t win[4] = {0, 0, 0, 0};
+    uint16_t *wp = a.pool + (live ? (id * a.n[0] + n) * 4 : 0);
+    if (live)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) win[j] = wp[j];
+    const uint16_t xb = f32_to_bf16_bits(o);
+    float acc_c = a.cb ? bf16_bits_to_f32(a.cb[n]) : 0.f;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) acc_c += bf16_bits_to_f32(a.cw[n * 4 + j]) * bf16_bits_to_f32(win[j + 1]);
+    acc_c += bf16_bits_to_f32(a.cw[n * 4 + 3]) * bf16_bits_to_f32(xb);
+    const float y = a.silu ? silu_f(acc_c) : acc_c;
+    if (live) {
+      wp[0] = win[1];
+      wp[1] = win[2];
+      wp[2] = win[3];
+      wp[3] = xb;
+    }
+    a.y[0][static_cast<int64_t>(m) * a.n[0] + n] = f32_to_bf16_bits(y);
+  } else {
+    uint16_t *ymat = mat == 1 ? a.y[1] : mat == 2 ? a.y[2] : a.y[3];
+    ymat[static_cast<int64_t>(m) * nmat + n] = f32_to_bf16_bits(o);
+  }
+}
+
+template <int MR>
+void launch_gemv(const InProjArgs &args, unsigned gx, int kb, hipStream_t s) {
+  if (kb == 2)
+    hipLaunchKernelGGL((in_proj_gemv_kernel<MR, 2>), dim3(gx), dim3(64 * IP_WAVES), 0, s, args);
+  else
+    hipLaunchKernelGGL((in_proj_gemv_kernel<MR, 4>), dim3(gx), dim3(64 * IP_WAVES), 0, s, args);
+}
+
 struct OutProjArgs {
   const uint16_t *x;  // [M, K] bf16, row stride xs elements
   int64_t xs;
@@ -500,6 +608,13 @@ extern "C" int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w
   const dim3 grid(static_cast<unsigned>(args.blocks_qkv + args.blocks_z + (n_b + n_a > 0 ? 1 : 0)),
                   static_cast<unsigned>((M + IP_ROWS - 1) / IP_ROWS));
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (M <= IP_GEMV_ROWS) {  // a GEMV stream of the weights (one row block)
+    if (M == 1)
+      launch_gemv<1>(args, grid.x, K / 512, s);
+    else
+      launch_gemv<2>(args, grid.x, K / 512, s);
+    return check_launch("gdn_in_proj_decode");
+  }
   switch (K) {
     case 1024: hipLaunchKernelGGL(in_proj_decode_kernel<InProjShape1024>, grid, dim3(64 * IP_WAVES), 0, s, args); break;
     case 2048: hipLaunchKernelGGL(in_proj_decode_kernel<InProjShape2048>, grid, dim3(64 * IP_WAVES), 0, s, args); break;

@@ -81,6 +81,60 @@ def test_matches_oracle_at_model_shape(m, bias):
     assert torch.equal(pool[untouched], pool0[untouched])
 
 
+@pytest.mark.parametrize("m,k,ids", [(1, 2048, True), (2, 2048, True), (2, 2048, False), (1, 1024, False),
+                                     (2, 1024, True)])
+def test_small_batches_gemv_path(m, k, ids):
+    """One or two rows take the GEMV kernel: against the oracle (a padding id
+    for two rows with ids), narrow b / a at K = 1024; its graph replays are
+    bit-identical to eager calls."""
+    print(f"in_proj_decode gemv case M={m} K={k} ids={ids}", flush=True)
+    gen = torch.Generator().manual_seed(101 + m + k)
+    n = (NQKV, NZ, NB, NA) if k == 2048 else (1024, 512, 4, 8)
+    ws, cw, cb = weights(gen, k=k, n=n, bias=ids)
+    rows = 16
+    pool = torch.randn(rows, n[0], 4, generator=gen).to(torch.bfloat16).to(DEV)
+    slots = torch.randperm(rows, generator=gen)[:m] if ids else torch.arange(m)
+    if ids and m == 2:
+        slots[1] = -1
+    x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(DEV)
+    pool0 = pool.clone()
+    y, z, b, a = run_fused(x, ws, cw, cb, pool, slots.to(DEV) if ids else None)
+    s = slots.numpy()
+    live = s >= 0
+    hist = np.zeros((m, n[0], 4))
+    hist[live] = np64(pool0)[s[live]]
+    y_ref, z_ref, b_ref, a_ref, st_ref = proj.in_proj_decode(
+        np64(x), *(np64(w) for w in ws), np64(cw), hist, None if cb is None else np64(cb))
+    for got, ref in ((y, y_ref), (z, z_ref), (b, b_ref), (a, a_ref)):
+        assert bf16_close(got, ref)
+    new = np64(pool)
+    assert np.array_equal(new[s[live]][:, :, :3], st_ref[live][:, :, :3])
+    assert tap_close(new[s[live]][:, :, 3], st_ref[live][:, :, 3], x[torch.from_numpy(live).to(DEV)], ws[0])
+    untouched = np.setdiff1d(np.arange(rows), s[live])
+    assert torch.equal(pool[untouched], pool0[untouched])
+    # graph replay of the same call
+    pool.copy_(pool0)
+    eager = run_fused(x, ws, cw, cb, pool, slots.to(DEV) if ids else None)
+    after = pool.clone()
+    pool.copy_(pool0)
+    sl = slots.to(DEV) if ids else None
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run_fused(x, ws, cw, cb, pool, sl)
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(graph):
+        outs = run_fused(x, ws, cw, cb, pool, sl)
+    pool.copy_(pool0)
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    for got, ref in zip(outs, eager):
+        assert torch.equal(got, ref)
+    assert torch.equal(pool, after)
+
+
 def test_matches_the_unfused_gpu_path():
     """Four hipBLASLt projections (torch F.linear) then the conv update kernel."""
     import torch.nn.functional as F
