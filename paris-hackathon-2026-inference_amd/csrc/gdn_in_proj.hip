@@ -479,6 +479,51 @@ __global__ __launch_bounds__(OP_RED_NT) void out_proj_sum_kernel(OutProjArgs a) 
   *reinterpret_cast<uint2 *>(a.y + static_cast<int64_t>(m) * a.ys + n) = make_uint2(pack2(t[0], t[1]), pack2(t[2], t[3]));
 }
 
+// One row: a GEMV stream in one kernel (no partial sums).  Workgroup = 16
+// waves over 32 columns; wave w takes columns 2 w, 2 w + 1 and streams each
+// weight row as K / 512 contiguous 1 KiB loads (all issued at the start),
+// the row of x in registers in the same lane layout; a wave reduction per
+// column, lanes 0 and 1 store.  KB = K / 512.
+template <int KB>
+__global__ __launch_bounds__(64 * IP_WAVES) void out_proj_gemv_kernel(OutProjArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int col = (blockIdx.x * IP_WAVES + wave) * 2;
+  constexpr int K = KB * 512;
+  const auto rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.w) + static_cast<int64_t>(col) * K, 0,
+                                                    2 * K * 2, BUF_DWORD3);
+  const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.x), 0, K * 2, BUF_DWORD3);
+  u32x4_t xv[KB], wv[2][KB];
+#pragma unroll
+  for (int i = 0; i < KB; ++i) xv[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (512 * i + 8 * lane) * 2, 0, 0);
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+      wv[c][i] = __builtin_amdgcn_raw_buffer_load_b128(rw, (c * K + 512 * i + 8 * lane) * 2, 0, 0);
+  float dot[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t wp = wv[c][i][e], xp = xv[i][e];
+        s += bf16_bits_to_f32(wp & 0xffffu) * bf16_bits_to_f32(xp & 0xffffu);
+        s += bf16_bits_to_f32(wp >> 16) * bf16_bits_to_f32(xp >> 16);
+      }
+    dot[c] = wave_sum(s);
+  }
+  if (lane < 2) a.y[col + lane] = f32_to_bf16_bits(lane == 0 ? dot[0] : dot[1]);
+}
+
+template <int KB>
+void launch_out_gemv(const OutProjArgs &args, hipStream_t s) {
+  hipLaunchKernelGGL((out_proj_gemv_kernel<KB>), dim3(static_cast<unsigned>(args.N / (2 * IP_WAVES))),
+                     dim3(64 * IP_WAVES), 0, s, args);
+}
+
 }  // namespace
 }  // namespace gdn
 
@@ -528,6 +573,15 @@ extern "C" int gdn_out_proj_decode(const void *x, int64_t x_stride, const void *
   args.y = static_cast<uint16_t *>(y);
   args.ys = y_stride;
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (M == 1 && (args.split == 1 || args.split == 2 || args.split == 4 || args.split == 8)) {  // one GEMV kernel
+    switch (args.split) {
+      case 1: launch_out_gemv<1>(args, s); break;
+      case 2: launch_out_gemv<2>(args, s); break;
+      case 4: launch_out_gemv<4>(args, s); break;
+      default: launch_out_gemv<8>(args, s); break;
+    }
+    return check_launch("gdn_out_proj_decode");
+  }
   const dim3 grid(static_cast<unsigned>(args.ncb * args.split), static_cast<unsigned>((M + IP_ROWS - 1) / IP_ROWS));
   hipLaunchKernelGGL(out_proj_partial_kernel, grid, dim3(64 * IP_WAVES), 0, s, args);
   const int64_t quads = static_cast<int64_t>(M) * (N / 4);

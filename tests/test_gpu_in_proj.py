@@ -323,9 +323,12 @@ def run_out(x, w):
 
 
 @pytest.mark.parametrize("m,k,n", [(64, 4096, 2048), (1, 4096, 2048), (5, 4096, 2048), (100, 4096, 2048),
-                                   (256, 4096, 2048), (3, 2048, 1024), (7, 512, 64), (9, 1536, 128)])
+                                   (256, 4096, 2048), (3, 2048, 1024), (7, 512, 64), (9, 1536, 128),
+                                   (1, 2048, 1024), (1, 512, 64), (1, 1536, 128)])
 def test_out_proj_matches_oracle(m, k, n):
-    """Against the exact sum: one bf16 ulp plus the fp32 summation error."""
+    """Against the exact sum: one bf16 ulp plus the fp32 summation error (one
+    row with K / 512 in {1, 2, 4, 8} takes the GEMV kernel, the rest the
+    split-K pair)."""
     print(f"out_proj_decode oracle case M={m} K={k} N={n}", flush=True)
     gen = torch.Generator().manual_seed(90 + m + n)
     x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(DEV)
