@@ -269,7 +269,8 @@ int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w_qkv, const
  * Decode-step output projection of the GDN layer:  y = x W^T  (bf16, fp32
  * sums), with K split over workgroups (512 of K each); a second kernel adds
  * the fp32 partial sums in split order, so results do not depend on
- * scheduling.
+ * scheduling.  One row with K / 512 in {1, 2, 4, 8} runs as a single GEMV
+ * kernel (the workspace is then not touched).
  *
  * Replaces, for small M (decode rows), the out_proj nn.Linear of HF's GDN
  * layer (transformers modeling_qwen3_5_moe.py:428, called at :540).
