@@ -572,7 +572,7 @@ def bench_out_proj(torch, sets=16, reps=4):
                                     "partials written and read besides)"}}
 
 
-def bench_layer_decode(torch, layers=4, reps=5):
+def bench_layer_decode(torch, layers=4, reps=5, batch=64):
     """One GDN layer decode step at B=64 with Qwen3.5-MoE layer shapes (hidden
     2048, 16 k-heads, 32 v-heads of 128, conv width 4; random bf16 weights):
     HF's ``Qwen3_5MoeGatedDeltaNet`` with ``gated_delta_net_forward`` on
@@ -605,8 +605,8 @@ def bench_layer_decode(torch, layers=4, reps=5):
         conv, rec = pools.layer(i)
         rec.normal_(0.0, 0.1)
         conv.normal_(0.0, 1.0)
-    slots = torch.randperm(128, generator=gen)[:64]
-    x = torch.randn(64, 1, 2048, generator=gen).to(dev, torch.bfloat16)
+    slots = torch.randperm(128, generator=gen)[:batch]
+    x = torch.randn(batch, 1, 2048, generator=gen).to(dev, torch.bfloat16)
     cache = types.SimpleNamespace(gdn_slot_pools=pools)
     pools.bind(slots, is_prefill=False)
     dslots = slots.to(dev)
@@ -640,9 +640,9 @@ def bench_layer_decode(torch, layers=4, reps=5):
     with mock.patch.object(gdn_layer, "_out_proj_fits", lambda *a, **k: False):
         t_lt_out = graph_us(steps)
     t_gs = graph_us(gather_scatter)
-    return {"config": "one GDN layer decode step, B=64 of 128 slots, hidden 2048, Hk=16 Hv=32 d=128, conv 4, "
+    return {"config": f"one GDN layer decode step, B={batch} of 128 slots, hidden 2048, Hk=16 Hv=32 d=128, conv 4, "
                       "bf16 weights (random), fp32 state pools; 4 layers per graph, own weights and pools",
-            "step_us": t_fused, "tok_per_s": 64 / (t_fused * 1e-6),
+            "step_us": t_fused, "tok_per_s": batch / (t_fused * 1e-6),
             "step_unfused_input_us": t_unfused,
             "step_hipblaslt_out_proj_us": t_lt_out,
             "reference_cache_gather_scatter_us": t_gs,
@@ -708,6 +708,7 @@ def main():
         out["decode_out_proj"] = bench_out_proj(torch)
     if not args.no_layer_decode:
         out["layer_decode"] = bench_layer_decode(torch)
+        out["layer_decode_b1"] = bench_layer_decode(torch, batch=1)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)
