@@ -241,6 +241,31 @@ def bench_prefill(torch, reps=20, warmup=3, repeat_qk=False):
                      "frac": flop / per / MFMA_BF16_PEAK, "flop_per_call": flop}}
 
 
+def bench_prefill_b16(torch, reps=10):
+    """The reference's own profiled prefill shape (fla's chunk
+    kernel, 1.659 ms per layer on H200): a dense batch of 16 sequences of 1038
+    tokens (17 chunks each), q/k at 16 heads, v at 32, zero h0, final states
+    out; the batch is scanned by the persistent scan."""
+    from engine import configs
+    from engine.kernels import chunk_gated_delta_rule
+
+    dev = torch.device("cuda", 0)
+    b, t = 16, 1038
+    c = configs.config2(seed=47, t=b * t)
+    q, k, v, g, beta = (c[x].to(dev).reshape(b, t, *c[x].shape[2:]) for x in ("q", "k", "v", "g", "beta"))
+
+    def run():
+        return chunk_gated_delta_rule(q, k, v, g, beta, output_final_state=True, use_qk_l2norm_in_kernel=True)
+
+    per = _time(torch, run, reps)
+    flop = PREFILL_FLOP_PER_CHUNK_HEAD * b * ((t + 63) // 64) * 32
+    return {"config": "B=16 x T=1038 (17 chunks each), Hk=16 Hv=32 d=128 bf16, zero h0, final states out",
+            "us": per * 1e6, "tok_per_s": b * t / per,
+            "mfma": {"achieved": flop / per / 1e12, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+                     "frac": flop / per / MFMA_BF16_PEAK, "flop": flop},
+            "reference_h200_us": 1659.0}
+
+
 def bench_varlen(torch, reps=10):
     """Configuration 3: 16 packed sequences (lengths U{128..2048}, seeded) as
     HF's layer runs them after the input projections: the causal conv + SiLU
@@ -700,6 +725,7 @@ def main():
         if not args.no_layer_glue:
             out["layer_glue"] = bench_layer_glue(torch)
         out["varlen"] = bench_varlen(torch)
+        out["prefill_b16_t1038"] = bench_prefill_b16(torch)
     out["spec_verify"] = bench_spec_verify(torch)
     if not args.no_conv:
         out["conv_prefill"] = bench_conv_prefill(torch)
