@@ -242,8 +242,8 @@ def bench_prefill(torch, reps=20, warmup=3, repeat_qk=False):
 
 
 def bench_prefill_b16(torch, reps=10):
-    """The reference's own profiled prefill shape (fla's chunk
-    kernel, 1.659 ms per layer on H200): a dense batch of 16 sequences of 1038
+    """The reference's own profiled prefill shape (its profile of fla's chunk
+    kernel: 1.659 ms per layer on H200): a dense batch of 16 sequences of 1038
     tokens (17 chunks each), q/k at 16 heads, v at 32, zero h0, final states
     out; the batch is scanned by the persistent scan."""
     from engine import configs
