@@ -679,7 +679,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the GDN path "
-              "shards over sequences and heads with no exchange (DESIGN.md)", file=sys.stderr)
+              "shards over sequences and heads with no exchange inside the path", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
