@@ -449,7 +449,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int b = 0; b < 4; ++b) trow[b] = b == p ? drow : z4;
-  // round 1: T[p][p-1] = -T[p][p] L[p][p-1] T[p-1][p-1]
+  // step 1: T[p][p-1] = -T[p][p] L[p][p-1] T[p-1][p-1]
 #pragma unroll
   for (int b = 0; b < 3; ++b)
     if (b == p - 1) {
@@ -458,7 +458,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
       if (b <= 1) txch[b * 64 + lane] = -mm16(drow, x, z4);  // T[1][0], T[2][1]
     }
   __syncthreads();
-  // round 2: T[p][p-2] = -T[p][p] (L[p][p-2] T[p-2][p-2] + L[p][p-1] T[p-1][p-2])
+  // step 2: T[p][p-2] = -T[p][p] (L[p][p-2] T[p-2][p-2] + L[p][p-1] T[p-1][p-2])
 #pragma unroll
   for (int b = 0; b < 2; ++b)
     if (b == p - 2) {
@@ -468,7 +468,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
       if (b == 0) txch[2 * 64 + lane] = -mm16(drow, x, z4);  // T[2][0]
     }
   __syncthreads();
-  if (p == 3) {  // round 3: T[3][0]
+  if (p == 3) {  // step 3: T[3][0]
     f32x4 x = mm16(lf[0], dxch[lane], z4);
     x = mm16(lf[1], txch[lane], x);           // T[1][0]
     x = mm16(lf[2], txch[2 * 64 + lane], x);  // T[2][0]
