@@ -126,7 +126,7 @@ struct ChunkArgs {
   int max_chunks;
   int seg_begin, seg_end;  // global chunk range of this launch (workspace holds SEG chunks)
   // workspace
-  int32_t *chunk_start;  // [n_seqs + 1]
+  int32_t *chunk_start;  // [n_seqs + 2]: chunk starts, then the empty-sequence count
   u32x4 *vh;             // [SEG][Hv][NB_VH][64]   -W, A, scalars
   u32x4 *kh;             // [SEG][Hk][NB_KH][64]   Q, K^T
   float *Ut;             // [SEG][Hv][8 x 4 blocks][64][4]  U, fp32
@@ -155,15 +155,25 @@ __device__ __forceinline__ void xcd_group_order(int bid, int per, int *g, int *m
 }
 
 // ------------------------------------------------------------------ chunk table
+// chunk_start[0 .. n_seqs]: first global chunk of each sequence (and the
+// total); chunk_start[n_seqs + 1]: the number of empty sequences.
 __global__ __launch_bounds__(256) void chunk_table_kernel(ChunkArgs a) {
   __shared__ int32_t part[256];
+  __shared__ int32_t empties;
   int32_t carry = 0;
-  if (threadIdx.x == 0) a.chunk_start[0] = 0;
+  if (threadIdx.x == 0) {
+    a.chunk_start[0] = 0;
+    empties = 0;
+  }
+  __syncthreads();
   for (int base = 0; base < a.n_seqs; base += 256) {
     const int n = base + threadIdx.x;
     int64_t s0;
     int len = 0;
-    if (n < a.n_seqs) seq_bounds(a, n, &s0, &len);
+    if (n < a.n_seqs) {
+      seq_bounds(a, n, &s0, &len);
+      if (len == 0) atomicAdd(&empties, 1);
+    }
     part[threadIdx.x] = (len + CK - 1) / CK;
     __syncthreads();
     for (int off = 1; off < 256; off <<= 1) {  // inclusive scan
@@ -176,6 +186,7 @@ __global__ __launch_bounds__(256) void chunk_table_kernel(ChunkArgs a) {
     carry += part[255];
     __syncthreads();
   }
+  if (threadIdx.x == 0) a.chunk_start[a.n_seqs + 1] = empties;
 }
 
 // ------------------------------------------------------------------ phase A
@@ -953,7 +964,8 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_persist_kernel(Chu
   };
 
   const int lo = a.seg_begin, hi = min(a.seg_end, chunk_start_at(a, a.n_seqs));
-  if (wave < 4 && a.seg_begin == 0) {  // empty sequences pass their initial state through
+  const bool any_empty = a.cu ? a.chunk_start[a.n_seqs + 1] > 0 : a.T == 0;  // (counted by the table kernel)
+  if (wave < 4 && a.seg_begin == 0 && any_empty) {  // empty sequences pass their initial state through
     for (int m = 0; m < a.n_seqs; ++m) {
       if (chunk_start_at(a, m) != chunk_start_at(a, m + 1)) continue;
       const int64_t orow = out_row(m);
@@ -1090,7 +1102,7 @@ WsLayout ws_layout(int n_seqs, int64_t seg_chunks, int Hv, int Hk, bool multi) {
   WsLayout l;
   size_t off = 0;
   l.chunk_start = off;
-  off = align256(off + sizeof(int32_t) * (n_seqs + 1));
+  off = align256(off + sizeof(int32_t) * (n_seqs + 2));
   l.carry = off;
   if (multi) off = align256(off + sizeof(float) * static_cast<size_t>(n_seqs) * Hv * DK * DV);
   l.vh = off;
