@@ -131,7 +131,14 @@ struct ChunkArgs {
   u32x4 *kh;             // [SEG][Hk][NB_KH][64]   Q, K^T
   float *Ut;             // [SEG][Hv][8 x 4 blocks][64][4]  U, fp32
   float *carry;          // [n_seqs][Hv][128][128] state between segments
+  int64_t *seqrec;       // [n_seqs][SEQREC]: per-sequence record for the persistent scan
 };
+
+// Per-sequence record written by chunk_table_kernel for the persistent scan:
+// token start, state rows in / out (-1: none), end chunk, length, and the
+// next non-empty sequence (n_seqs: none).
+constexpr int SEQREC = 6;
+enum { SR_S0 = 0, SR_IN, SR_OUT, SR_CE, SR_LEN, SR_NXT };
 
 __device__ __forceinline__ void seq_bounds(const ChunkArgs &a, int n, int64_t *s0, int *len) {
   seq_range(a.cu, n, a.T, a.total, s0, len);
@@ -187,6 +194,21 @@ __global__ __launch_bounds__(256) void chunk_table_kernel(ChunkArgs a) {
     __syncthreads();
   }
   if (threadIdx.x == 0) a.chunk_start[a.n_seqs + 1] = empties;
+  __syncthreads();  // chunk_start complete (workgroup-visible)
+  for (int n = threadIdx.x; n < a.n_seqs; n += 256) {
+    int64_t s0;
+    int len;
+    seq_bounds(a, n, &s0, &len);
+    int k = n + 1;
+    while (k < a.n_seqs && a.chunk_start[k] == a.chunk_start[k + 1]) ++k;  // skip empty sequences
+    int64_t *r = a.seqrec + static_cast<int64_t>(n) * SEQREC;
+    r[SR_S0] = s0;
+    r[SR_IN] = a.h0 ? pool_row(a.h0_idx, n, a.h0_rows) : -1;
+    r[SR_OUT] = a.hT ? pool_row(a.hT_idx, n, a.hT_rows) : -1;
+    r[SR_CE] = a.chunk_start[n + 1];
+    r[SR_LEN] = len;
+    r[SR_NXT] = k;
+  }
 }
 
 // ------------------------------------------------------------------ phase A
@@ -956,11 +978,21 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_persist_kernel(Chu
 #pragma unroll
       for (int e = 0; e < 4; ++e) dst[(row0 + 16 * t + 4 * g4 + e) * DV] = S[t][e];
   };
-  auto in_row = [&](int n) -> int64_t { return a.h0 ? uniform64(pool_row(a.h0_idx, n, a.h0_rows)) : -1; };
-  auto out_row = [&](int n) -> int64_t { return a.hT ? uniform64(pool_row(a.hT_idx, n, a.hT_rows)) : -1; };
-  auto init_src = [&](int n) -> const float * {
-    const int64_t r = in_row(n);
-    return r >= 0 ? state_at(const_cast<float *>(a.h0), r) : nullptr;
+  auto init_src = [&](int64_t row) -> const float * {
+    return row >= 0 ? state_at(const_cast<float *>(a.h0), row) : nullptr;
+  };
+  // sequence records (chunk_table_kernel, read-only here): uniform, so read
+  // through the constant address space as scalar loads into SGPRs
+  typedef const __attribute__((address_space(4))) int64_t crec_t;
+  crec_t *recp = (crec_t *)(a.seqrec);
+  struct Rec {
+    int64_t s0, in, out;
+    int ce, len, nxt;
+  };
+  auto rec_get = [&](int m) -> Rec {
+    crec_t *r = recp + static_cast<int64_t>(m) * SEQREC;
+    return Rec{r[SR_S0], r[SR_IN], r[SR_OUT], static_cast<int>(r[SR_CE]), static_cast<int>(r[SR_LEN]),
+               static_cast<int>(r[SR_NXT])};
   };
 
   const int lo = a.seg_begin, hi = min(a.seg_end, chunk_start_at(a, a.n_seqs));
@@ -968,11 +1000,11 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_persist_kernel(Chu
   if (wave < 4 && a.seg_begin == 0 && any_empty) {  // empty sequences pass their initial state through
     for (int m = 0; m < a.n_seqs; ++m) {
       if (chunk_start_at(a, m) != chunk_start_at(a, m + 1)) continue;
-      const int64_t orow = out_row(m);
-      if (orow < 0) continue;
+      const Rec r = rec_get(m);
+      if (r.out < 0) continue;
       f32x4 Sx[2];
-      load_state(init_src(m), Sx);
-      store_state(state_at(a.hT, orow), Sx);
+      load_state(init_src(r.in), Sx);
+      store_state(state_at(a.hT, r.out), Sx);
     }
   }
   if (lo >= hi) return;
@@ -995,24 +1027,28 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_persist_kernel(Chu
     }
     n = __builtin_amdgcn_readfirstlane(l);
   }
-  int cs = __builtin_amdgcn_readfirstlane(chunk_start_at(a, n));
-  int ce = __builtin_amdgcn_readfirstlane(chunk_start_at(a, n + 1));
-  int64_t s0;
-  int slen;
-  seq_bounds(a, n, &s0, &slen);
-  s0 = uniform64(s0);
-  slen = __builtin_amdgcn_readfirstlane(slen);
-  // the next non-empty sequence after m (n_seqs: none)
-  auto next_seq = [&](int m) {
-    int k = m + 1;
-    while (k < a.n_seqs && chunk_start_at(a, k) == chunk_start_at(a, k + 1)) ++k;
-    return __builtin_amdgcn_readfirstlane(k);
-  };
+  // Current sequence n, the next one nn (its record and initial state Sn in
+  // registers) and the one after, nnn (its record requested): at a sequence
+  // end what the next sequence needs is already loaded.
   float *carry = a.carry;
   f32x4 S[2], Sn[2];
-  load_state(lo == cs ? init_src(n) : state_at(carry, n), S);
-  int nn = ce < hi ? next_seq(n) : a.n_seqs;
-  load_state(nn < a.n_seqs ? init_src(nn) : nullptr, Sn);
+  const Rec rc = rec_get(n);
+  int cs = __builtin_amdgcn_readfirstlane(chunk_start_at(a, n));
+  int ce = rc.ce, slen = rc.len;
+  int64_t s0 = rc.s0, orow = rc.out;
+  load_state(lo == cs ? init_src(rc.in) : state_at(carry, n), S);
+  int nn = ce < hi ? rc.nxt : a.n_seqs;
+  int nnn = a.n_seqs;
+  Rec rn{0, -1, -1, 0, 0, 0}, r3{0, -1, -1, 0, 0, 0};
+  auto take_next = [&]() {  // rn = nn's record: its initial state, and nnn's record
+    load_state(init_src(rn.in), Sn);
+    nnn = rn.ce < hi ? rn.nxt : a.n_seqs;
+    if (nnn < a.n_seqs) r3 = rec_get(nnn);
+  };
+  if (nn < a.n_seqs) {
+    rn = rec_get(nn);
+    take_next();
+  }
 
   typedef typename std::conditional<BF16_OUT, uint16_t, float>::type OT;
   const int64_t ostep = static_cast<int64_t>(a.Hv) * DV;
@@ -1033,18 +1069,20 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_persist_kernel(Chu
     };
     auto at_state = [&](f32x4 (&St)[2]) {
       if (j + 1 == ce && j + 1 < hi) {  // sequence n ends here, sequence nn starts with the next chunk
-        const int64_t orow = out_row(n);
         if (orow >= 0) store_state(state_at(a.hT, orow), St);
         St[0] = Sn[0];
         St[1] = Sn[1];
         n = nn;
-        cs = __builtin_amdgcn_readfirstlane(chunk_start_at(a, n));
-        ce = __builtin_amdgcn_readfirstlane(chunk_start_at(a, n + 1));
-        seq_bounds(a, n, &s0, &slen);
-        s0 = uniform64(s0);
-        slen = __builtin_amdgcn_readfirstlane(slen);
-        nn = ce < hi ? next_seq(n) : a.n_seqs;
-        load_state(nn < a.n_seqs ? init_src(nn) : nullptr, Sn);
+        cs = ce;
+        ce = rn.ce;
+        s0 = rn.s0;
+        slen = rn.len;
+        orow = rn.out;
+        nn = nnn;
+        if (nn < a.n_seqs) {
+          rn = r3;
+          take_next();
+        }
       }
     };
     if (q >= 2)
@@ -1070,7 +1108,6 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_persist_kernel(Chu
   }
   // the last sequence: finished here, or continued by the next segment
   if (ce <= hi) {
-    const int64_t orow = out_row(n);
     if (orow >= 0) store_state(state_at(a.hT, orow), S);
   } else {
     store_state(state_at(carry, n), S);
@@ -1092,7 +1129,7 @@ constexpr int SEG_CHUNKS = 64;
 // Workspace: the chunk table, the state carried between segments (when
 // there are several) and the scan operands of one segment.
 struct WsLayout {
-  size_t chunk_start, carry, total;
+  size_t chunk_start, seqrec, carry, total;
   size_t vh, kh, Ut;
 };
 
@@ -1103,6 +1140,8 @@ WsLayout ws_layout(int n_seqs, int64_t seg_chunks, int Hv, int Hk, bool multi) {
   size_t off = 0;
   l.chunk_start = off;
   off = align256(off + sizeof(int32_t) * (n_seqs + 2));
+  l.seqrec = off;
+  off = align256(off + sizeof(int64_t) * SEQREC * static_cast<size_t>(n_seqs));
   l.carry = off;
   if (multi) off = align256(off + sizeof(float) * static_cast<size_t>(n_seqs) * Hv * DK * DV);
   l.vh = off;
@@ -1181,7 +1220,7 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
               cu_seqlens, n_seqs, T, Hk, Hv, total, scale, l2norm_qk, static_cast<int>(nc), 0, 0,
               reinterpret_cast<int32_t *>(ws + l.chunk_start), reinterpret_cast<u32x4 *>(ws + l.vh),
               reinterpret_cast<u32x4 *>(ws + l.kh), reinterpret_cast<float *>(ws + l.Ut),
-              reinterpret_cast<float *>(ws + l.carry)};
+              reinterpret_cast<float *>(ws + l.carry), reinterpret_cast<int64_t *>(ws + l.seqrec)};
   auto set_segment = [&](int64_t segment) {
     a.seg_begin = static_cast<int>(segment * seg);
     a.seg_end = static_cast<int>(std::min<int64_t>((segment + 1) * seg, nc));
@@ -1207,7 +1246,7 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
                          dim3(64 * SCAN_WAVES), 0, st, a);
   };
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (cu_seqlens) hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, s, a);
+  if (cu_seqlens || persist) hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, s, a);
   const int64_t nseg = seg > 0 ? (nc + seg - 1) / seg : 0;
   if (nseg == 0) {  // only empty sequences: they still pass their state through
     set_segment(0);
