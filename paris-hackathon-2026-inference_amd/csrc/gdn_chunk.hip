@@ -989,7 +989,13 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_persist_kernel(Chu
     int64_t s0, in, out;
     int ce, len, nxt;
   };
+  const bool arith = !a.cu && !a.h0_idx && !a.hT_idx;  // a dense batch without slot ids: no table
   auto rec_get = [&](int m) -> Rec {
+    if (arith) {
+      const int cpb = (a.T + CK - 1) / CK;
+      return Rec{static_cast<int64_t>(m) * a.T, a.h0 ? pool_row(nullptr, m, a.h0_rows) : -1,
+                 a.hT ? pool_row(nullptr, m, a.hT_rows) : -1, (m + 1) * cpb, a.T, m + 1};
+    }
     crec_t *r = recp + static_cast<int64_t>(m) * SEQREC;
     return Rec{r[SR_S0], r[SR_IN], r[SR_OUT], static_cast<int>(r[SR_CE]), static_cast<int>(r[SR_LEN]),
                static_cast<int>(r[SR_NXT])};
@@ -1246,7 +1252,10 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
                          dim3(64 * SCAN_WAVES), 0, st, a);
   };
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (cu_seqlens || persist) hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, s, a);
+  // the chunk table: chunk starts for varlen, per-sequence records for the persistent scan
+  // (which computes them itself for a dense batch without slot ids)
+  if (cu_seqlens || (persist && (h0_idx || hT_idx)))
+    hipLaunchKernelGGL(chunk_table_kernel, dim3(1), dim3(256), 0, s, a);
   const int64_t nseg = seg > 0 ? (nc + seg - 1) / seg : 0;
   if (nseg == 0) {  // only empty sequences: they still pass their state through
     set_segment(0);
