@@ -573,8 +573,9 @@ extern "C" int gdn_out_proj_decode(const void *x, int64_t x_stride, const void *
   args.y = static_cast<uint16_t *>(y);
   args.ys = y_stride;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (M == 1 && (args.split == 1 || args.split == 2 || args.split == 4 || args.split == 8)) {  // one GEMV kernel
-    switch (args.split) {
+  const int kb = K / 512;  // the GEMV kernel's 1 KiB row pieces
+  if (M == 1 && (kb == 1 || kb == 2 || kb == 4 || kb == 8)) {  // one GEMV kernel
+    switch (kb) {
       case 1: launch_out_gemv<1>(args, s); break;
       case 2: launch_out_gemv<2>(args, s); break;
       case 4: launch_out_gemv<4>(args, s); break;
