@@ -187,3 +187,26 @@ def test_segments_equal_split_calls():
         oi, si = chunk_gated_delta_rule(q[:, a:b], k[:, a:b], v[:, a:b], g[:, a:b], beta[:, a:b],
                                         initial_state=h0[i:i + 1], **kw)
         assert torch.equal(o[:, a:b], oi) and torch.equal(s[i:i + 1], si), i
+
+    print("chunk segments: slot pool, varlen 4500 + 0 + 100 + 4000", flush=True)
+    lens = [4500, 0, 100, 4000]
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=DEV)
+    c = configs.config2(seed=25, t=sum(lens))
+    q, k, v, g, beta = (c[x].to(DEV) for x in ("q", "k", "v", "g", "beta"))
+    pool0 = torch.randn(7, 32, 128, 128, generator=torch.Generator().manual_seed(26)).mul(0.1).to(DEV)
+    slots = torch.tensor([5, 2, 0, 3], device=DEV)
+    pool = pool0.clone()
+    o, ret = chunk_gated_delta_rule(q, k, v, g, beta, initial_state=pool, ssm_state_indices=slots,
+                                    inplace_final_state=True, cu_seqlens=cu, use_qk_l2norm_in_kernel=True)
+    assert ret is pool
+    starts = np.concatenate([[0], np.cumsum(lens)])
+    for i, slot in enumerate(slots.tolist()):
+        a, b = int(starts[i]), int(starts[i + 1])
+        if a == b:
+            assert torch.equal(pool[slot], pool0[slot]), i
+            continue
+        oi, si = chunk_gated_delta_rule(q[:, a:b], k[:, a:b], v[:, a:b], g[:, a:b], beta[:, a:b],
+                                        initial_state=pool0[slot:slot + 1], **kw)
+        assert torch.equal(o[:, a:b], oi) and torch.equal(pool[slot:slot + 1], si), i
+    untouched = [r for r in range(pool.shape[0]) if r not in slots.tolist()]
+    assert torch.equal(pool[untouched], pool0[untouched])
