@@ -106,6 +106,64 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_kernel(NormArgs a) {
   if (valid) store8(a.y, t * a.ys + static_cast<int64_t>(hh) * ND + c0, a.y_dt, y);
 }
 
+// 8 two-byte values (bf16 or fp16) as one 16-byte load, converted apart
+// from the load so that a kernel can issue all of its loads first.
+__device__ __forceinline__ u32x4 raw8(const void *p, int64_t i) {
+  return *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(p) + i);
+}
+
+__device__ __forceinline__ void cvt8(const u32x4 a, int dt, float (&v)[8]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (dt == GDN_DTYPE_BF16) {
+      v[2 * e] = bf16_bits_to_f32(a[e] & 0xffffu);
+      v[2 * e + 1] = bf16_bits_to_f32(a[e] >> 16);
+    } else {
+      v[2 * e] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(a[e] & 0xffffu)));
+      v[2 * e + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(a[e] >> 16)));
+    }
+  }
+}
+
+// x, z and y in 2-byte types (the layer's case; the weight in fp32 when
+// W32): the same rows and arithmetic as rmsnorm_gated_kernel, with the x, z
+// and weight loads issued back to back before any conversion, so that a
+// workgroup waits for one memory latency instead of three in turn.  Lanes
+// of a row past H load the last row and store nothing.
+template <bool W32>
+__global__ __launch_bounds__(256) void rmsnorm_gated_h_kernel(NormArgs a) {
+  const int64_t t = blockIdx.x;
+  const int hr = static_cast<int>(blockIdx.y) * ROWS_PER_WG + static_cast<int>(threadIdx.x >> 4);
+  const bool valid = hr < a.H;
+  const int hh = valid ? hr : a.H - 1;
+  const int c0 = (threadIdx.x & 15) * 8;
+  const u32x4 xr = raw8(a.x, t * a.xs + static_cast<int64_t>(hh) * ND + c0);
+  const u32x4 zr = raw8(a.z, t * a.zs + static_cast<int64_t>(hh) * ND + c0);
+  float x[8], z[8], w[8];
+  if constexpr (W32) {
+    const u32x4 w0 = *reinterpret_cast<const u32x4 *>(static_cast<const float *>(a.w) + c0);
+    const u32x4 w1 = *reinterpret_cast<const u32x4 *>(static_cast<const float *>(a.w) + c0 + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      w[e] = __uint_as_float(w0[e]);
+      w[4 + e] = __uint_as_float(w1[e]);
+    }
+  } else {
+    cvt8(raw8(a.w, c0), a.w_dt, w);
+  }
+  cvt8(xr, a.x_dt, x);
+  cvt8(zr, a.z_dt, z);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+  ss = row16_sum(ss);
+  const float r = rsqrtf(ss * (1.f / ND) + a.eps);
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = w[e] * (x[e] * r) * (z[e] / (1.f + __expf(-z[e])));
+  if (valid) store8(a.y, t * a.ys + static_cast<int64_t>(hh) * ND + c0, a.y_dt, y);
+}
+
 bool aligned_rows(const void *p, int dt, int64_t stride) {
   const int64_t unit = 8;  // rows start on 8-element boundaries: 16 bytes (2-byte types) or 32 (fp32)
   const size_t align = dt == GDN_DTYPE_F32 ? 32 : 16;
@@ -142,6 +200,13 @@ extern "C" int gdn_rmsnorm_gated_fwd(const void *x, int x_dtype, int64_t x_strid
   NormArgs a{x, z, weight, y, x_dtype, z_dtype, w_dtype, y_dtype, x_stride_t, z_stride_t, y_stride_t,
              n_tokens * H, H, eps};
   const dim3 grid(static_cast<unsigned>(n_tokens), static_cast<unsigned>((H + ROWS_PER_WG - 1) / ROWS_PER_WG));
-  hipLaunchKernelGGL(rmsnorm_gated_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  const auto st = static_cast<hipStream_t>(stream);
+  const bool half_io = x_dtype != GDN_DTYPE_F32 && z_dtype != GDN_DTYPE_F32 && y_dtype != GDN_DTYPE_F32;
+  if (half_io && w_dtype == GDN_DTYPE_F32)
+    hipLaunchKernelGGL(rmsnorm_gated_h_kernel<true>, grid, dim3(256), 0, st, a);
+  else if (half_io)
+    hipLaunchKernelGGL(rmsnorm_gated_h_kernel<false>, grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(rmsnorm_gated_kernel, grid, dim3(256), 0, st, a);
   return check_launch("gdn_rmsnorm_gated_fwd");
 }

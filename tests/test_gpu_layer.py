@@ -85,15 +85,19 @@ def test_recurrent_from_projections_matches_oracle_on_a_slot_pool():
     assert torch.equal(pool_gpu[untouched].cpu(), pool[untouched])
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_rms_norm_gated_matches_oracle(dtype):
+@pytest.mark.parametrize("dtype,w_dtype,h", [(torch.bfloat16, torch.bfloat16, 32), (torch.float32, torch.float32, 32),
+                                               (torch.bfloat16, torch.float32, 32), (torch.float16, torch.float16, 20)])
+def test_rms_norm_gated_matches_oracle(dtype, w_dtype, h):
+    """2-byte x / z / y take the kernel that issues all loads first (bf16 or
+    fp32 weight; H = 20 leaves a partial group of 16 rows), fp32 the
+    general one."""
     from engine.kernels import rms_norm_gated
     gen = torch.Generator().manual_seed(33)
-    t, h = 37, 32
+    t = 37
     x = (torch.randn(t, h, 128, generator=gen) * 3.0).to(dtype)
     zz = torch.randn(t, 2 * h * 128, generator=gen).to(dtype)   # z as a strided view of a packed projection
     z = zz[:, h * 128:].view(t, h, 128)
-    w = (1.0 + 0.3 * torch.randn(128, generator=gen)).to(dtype)
+    w = (1.0 + 0.3 * torch.randn(128, generator=gen)).to(w_dtype)
     y = rms_norm_gated(x.to(DEV), zz.to(DEV)[:, h * 128:].view(t, h, 128), w.to(DEV), eps=1e-6)
     assert y.dtype == dtype and y.shape == x.shape
     y_ref = gdn.rms_norm_gated(np64(x), np64(z), np64(w), eps=1e-6)
