@@ -205,37 +205,45 @@ def bench_decode_batches(torch, batches=(1, 4, 16, 64), reps=50):
     return out
 
 
-def bench_prefill(torch, reps=20, warmup=3, repeat_qk=False):
+def bench_prefill(torch, reps=24, warmup=3, repeat_qk=False, n_sets=3):
     """Configuration 2.  With repeat_qk, q and k arrive repeated to the 32 v-heads
     (HF's repeat_interleave before the call), the layout the reference's boundary
-    actually receives; otherwise they keep their 16 heads (native GQA)."""
+    actually receives; otherwise they keep their 16 heads (native GQA).  Calls
+    rotate over ``n_sets`` input sets (about 100 MB each), so that the inputs of
+    a call were last touched ``n_sets`` calls earlier and the 256 MB Infinity
+    Cache does not serve them from the previous call."""
     from engine import configs
     from engine.kernels import chunk_gated_delta_rule
 
-    c = configs.config2()
     dev = torch.device("cuda", 0)
-    q, k, v, g, beta = (c[x].to(dev) for x in ("q", "k", "v", "g", "beta"))
-    if repeat_qk:
-        rep = v.shape[2] // q.shape[2]
-        q, k = q.repeat_interleave(rep, dim=2), k.repeat_interleave(rep, dim=2)
-    t = q.shape[1]
+    sets = []
+    for i in range(n_sets):  # configuration 2's generator with one seed per set
+        c = configs.config2(seed=2 + 1000 * i)
+        q, k, v, g, beta = (c[x].to(dev) for x in ("q", "k", "v", "g", "beta"))
+        if repeat_qk:
+            rep = v.shape[2] // q.shape[2]
+            q, k = q.repeat_interleave(rep, dim=2), k.repeat_interleave(rep, dim=2)
+        sets.append((q, k, v, g, beta))
+    t = sets[0][0].shape[1]
 
-    def run():
-        return chunk_gated_delta_rule(q, k, v, g, beta, output_final_state=True, use_qk_l2norm_in_kernel=True)
+    def run(i):
+        return chunk_gated_delta_rule(*sets[i % n_sets], output_final_state=True, use_qk_l2norm_in_kernel=True)
 
-    for _ in range(warmup):
-        run()
+    for i in range(warmup):
+        run(i)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    for _ in range(reps):
-        run()
+    for i in range(reps):
+        run(i)
     e1.record(stream)
     torch.cuda.synchronize()
     per = e0.elapsed_time(e1) * 1e-3 / reps
     flop = PREFILL_FLOP_PER_CHUNK_HEAD * ((t + 63) // 64) * 32
-    return {"config": f"prefill B=1 T=4096 Hk={q.shape[2]} Hv=32 d=128 bf16, chunk 64, zero h0, final state out",
+    set_mb = sum(x.numel() * x.element_size() for x in sets[0]) / 1e6
+    return {"config": f"prefill B=1 T=4096 Hk={sets[0][0].shape[2]} Hv=32 d=128 bf16, chunk 64, zero h0, "
+                      f"final state out; {n_sets} input sets of {set_mb:.0f} MB rotated call by call",
             "tok_per_s": t / per, "ms": per * 1e3,
             "mfma": {"achieved": flop / per / 1e12, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
                      "frac": flop / per / MFMA_BF16_PEAK, "flop_per_call": flop}}
@@ -458,55 +466,132 @@ def _median_time(fn, min_reps=5, budget_s=3.0):
     return times[len(times) // 2], len(times)
 
 
-def cpu_baseline(budget_s=12.0):
-    """CPU oracle (numpy fp32) on bounded samples: the decode workload
-    (configuration 1, the headline value) with sequences split across the host
-    cores this process may use, the same on one thread, and the prefill
-    (configuration 2, all 32 heads of the 4096 tokens) with heads split across
-    the cores."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(budget_s=6.0):
+    """CPU oracle (numpy fp32) on bounded samples of configurations 0-4, each
+    split over the host cores this run may use, plus configuration 1 on one
+    thread.  Threads: the cores in this process's affinity mask, capped at
+    OMP_NUM_THREADS (the GPU box gives one GPU's job a 16-core share of its
+    host and sets OMP_NUM_THREADS=16 accordingly).  Each figure is the median
+    of timed runs after one warmup (time.perf_counter)."""
     import numpy as np
     from engine import configs
-    from oracle import gdn
+    from oracle import conv, gdn
 
+    affinity = len(os.sched_getaffinity(0))
+    n = max(1, min(affinity, int(os.environ.get("OMP_NUM_THREADS", affinity) or affinity)))
+    ex = cf.ThreadPoolExecutor(n)
+    out = {"cores": n, "affinity_cores": affinity, "cpu_model": _cpu_model(), "kind": "port",
+           "unit": "tok/s"}
+
+    def split(total, parts):
+        parts = max(1, min(parts, total))
+        return [slice(i * total // parts, (i + 1) * total // parts) for i in range(parts)]
+
+    # configuration 1 (the headline): one decode step over 64 gathered slot states
     c = configs.config1()
     args = [c[x].float().numpy() for x in ("q", "k", "v", "g", "beta")]
     h0 = c["pool"].numpy()[c["slots"].numpy()]
-    n = min(16, len(os.sched_getaffinity(0)))
-    parts = [slice(i * 64 // n, (i + 1) * 64 // n) for i in range(n)]
 
     def run_part(sl):
         return gdn.recurrent_gated_delta_rule(*(a[sl] for a in args), initial_state=h0[sl], dtype=np.float32)
 
-    with cf.ThreadPoolExecutor(n) as ex:
-        per, reps = _median_time(lambda: list(ex.map(run_part, parts)), budget_s=budget_s)
+    per, reps = _median_time(lambda: list(ex.map(run_part, split(64, n))), budget_s=budget_s)
     per1, reps1 = _median_time(lambda: run_part(slice(0, 64)), budget_s=3.0)
+    out.update({"value": 64 / per, "gb_per_s": DECODE_BYTES / per / 1e9,
+                "sample": f"configuration 1 decode steps (B=64, one layer, 64 gathered slot states) with the numpy "
+                          f"fp32 oracle, sequences split over {n} threads; median of {reps} steps after one warmup, "
+                          f"{per * 1e3:.1f} ms/step",
+                "one_thread": {"value": 64 / per1, "unit": "tok/s", "cores": 1,
+                               "sample": f"the same step on one thread, median of {reps1}: {per1 * 1e3:.1f} ms/step"}})
 
-    # prefill: v-heads split into n groups of whole k-head pairs
+    def by_heads(q, k, v, g, beta, fn, **kw):
+        """Run fn over groups of whole k-heads (and their v-heads) in parallel."""
+        hk, hv = q.shape[2], v.shape[2]
+        grp = hv // hk
+
+        def run(ks):
+            vs = slice(ks.start * grp, ks.stop * grp)
+            return fn(q[:, :, ks], k[:, :, ks], v[:, :, vs], g[:, :, vs], beta[:, :, vs], dtype=np.float32, **kw)
+        return lambda: list(ex.map(run, split(hk, n)))
+
+    # configuration 0: fp32 recurrence, B=1, T=256
+    c0 = configs.config0()
+    a0 = [c0[x].numpy() for x in ("q", "k", "v", "g", "beta")]
+    per0, reps0 = _median_time(by_heads(*a0, gdn.recurrent_gated_delta_rule), min_reps=3, budget_s=3.0)
+    t0 = a0[0].shape[1]
+    out["config0"] = {"value": t0 / per0, "unit": "tok/s",
+                      "sample": f"configuration 0 (fp32 recurrence, T={t0}, 32 v-heads), k-head groups over {n} "
+                                f"threads; median of {reps0}, {per0 * 1e3:.1f} ms per run"}
+
+    # configuration 2: chunk prefill, T=4096
     c2 = configs.config2()
-    q, k, v, g, beta = (c2[x].float().numpy() for x in ("q", "k", "v", "g", "beta"))
-    hk, hv = q.shape[2], v.shape[2]
-    grp = hv // hk
-    n2 = min(n, hk)
-    kparts = [slice(i * hk // n2, (i + 1) * hk // n2) for i in range(n2)]
+    a2 = [c2[x].float().numpy() for x in ("q", "k", "v", "g", "beta")]
+    per2, reps2 = _median_time(by_heads(*a2, gdn.chunk_gated_delta_rule), min_reps=3, budget_s=3.0)
+    t2 = a2[0].shape[1]
+    flop2 = PREFILL_FLOP_PER_CHUNK_HEAD * ((t2 + 63) // 64) * 32
+    out["prefill"] = {"value": t2 / per2, "unit": "tok/s", "gflop_per_s": flop2 / per2 / 1e9,
+                      "sample": f"configuration 2 (T={t2}, all 32 v-heads) through the numpy fp32 chunk oracle, "
+                                f"k-head groups over {n} threads; median of {reps2} runs after one warmup, "
+                                f"{per2:.2f} s per run"}
 
-    def run_heads(ks):
-        vs = slice(ks.start * grp, ks.stop * grp)
-        return gdn.chunk_gated_delta_rule(q[:, :, ks], k[:, :, ks], v[:, :, vs], g[:, :, vs], beta[:, :, vs],
-                                          dtype=np.float32)
+    # configuration 3 (bounded): the first 4 of its 16 sequences -- conv over the 8192-wide
+    # projection, then the chunk rule with cu_seqlens and initial states
+    c3 = configs.config3()
+    cu = c3["cu_seqlens"].numpy()[:5]
+    n3 = int(cu[-1])
+    x3 = c3["x"][:n3].float().numpy()
+    w3 = c3["conv_w"].float().numpy()
+    g3, b3 = c3["g"][:, :n3].numpy(), c3["beta"][:, :n3].numpy()
+    h03 = c3["h0"][:4].numpy()
 
-    with cf.ThreadPoolExecutor(n2) as ex:
-        per2, reps2 = _median_time(lambda: list(ex.map(run_heads, kparts)), min_reps=3, budget_s=3.0)
-    t2 = q.shape[1]
-    return {"value": 64 / per, "unit": "tok/s", "cores": n, "kind": "port",
-            "sample": f"configuration 1 decode steps (B=64, one layer, 64 gathered slot states) with the numpy "
-                      f"fp32 oracle, sequences split over {n} threads; median of {reps} steps after one warmup, "
-                      f"{per * 1e3:.1f} ms/step",
-            "one_thread": {"value": 64 / per1, "unit": "tok/s", "cores": 1,
-                           "sample": f"the same step on one thread, median of {reps1}: {per1 * 1e3:.1f} ms/step"},
-            "prefill": {"value": t2 / per2, "unit": "tok/s", "cores": n2,
-                        "sample": f"configuration 2 (T={t2}, all {hv} v-heads) through the numpy fp32 chunk oracle, "
-                                  f"k-head groups split over {n2} threads; median of {reps2} runs after one "
-                                  f"warmup, {per2:.2f} s per run"}}
+    def run3():
+        cparts = split(x3.shape[1], n)
+        ys = list(ex.map(lambda sl: conv.causal_conv1d_varlen(x3[:, sl], w3[sl], cu, activation="silu",
+                                                              dtype=np.float32)[0], cparts))
+        y = np.concatenate(ys, axis=1)
+        q = y[:, :2048].reshape(1, n3, 16, 128)
+        k = y[:, 2048:4096].reshape(1, n3, 16, 128)
+        v = y[:, 4096:].reshape(1, n3, 32, 128)
+
+        def heads(ks):
+            vs = slice(ks.start * 2, ks.stop * 2)
+            return gdn.chunk_gated_delta_rule_varlen(q[:, :, ks], k[:, :, ks], v[:, :, vs], g3[:, :, vs],
+                                                     b3[:, :, vs], cu, h03[:, vs], dtype=np.float32)
+        return list(ex.map(heads, split(16, n)))
+
+    per3, reps3 = _median_time(run3, min_reps=3, budget_s=4.0)
+    out["config3"] = {"value": n3 / per3, "unit": "tok/s",
+                      "sample": f"configuration 3's first 4 sequences ({n3} tokens): numpy fp32 conv (channel groups) "
+                                f"then the chunk oracle with cu_seqlens and h0 (k-head groups), {n} threads; median "
+                                f"of {reps3}, {per3:.2f} s per run"}
+
+    # configuration 4: speculative verify, B=32, T=4, snapshots and commit
+    c4 = configs.config4()
+    a4 = [c4[x].float().numpy() for x in ("q", "k", "v", "g", "beta")]
+    pool4, slots4, acc4 = c4["pool"].numpy(), c4["slots"].numpy(), c4["accepted"].numpy()
+
+    def run4_part(sl):  # each part gets the pool rows of its own slots
+        return gdn.spec_verify(pool4[slots4[sl]], np.arange(sl.stop - sl.start), *(a[sl] for a in a4), acc4[sl],
+                               dtype=np.float32)
+
+    per4, reps4 = _median_time(lambda: list(ex.map(run4_part, split(len(slots4), n))), min_reps=3, budget_s=3.0)
+    b4, tt4 = a4[0].shape[0], a4[0].shape[1]
+    out["config4"] = {"value": b4 * tt4 / per4, "unit": "verified tok/s",
+                      "sample": f"configuration 4 (B={b4}, T={tt4}: snapshots and commit) with the numpy fp32 oracle, "
+                                f"sequences over {n} threads; median of {reps4}, {per4 * 1e3:.1f} ms per step"}
+    ex.shutdown()
+    return out
 
 
 def bench_in_proj(torch, sets=6, reps=4):

@@ -25,8 +25,11 @@
  *     array (int64, one entry per sequence) selects rows of a pool; a NULL
  *     index array means row n for sequence n.  A negative slot id means
  *     "no slot": the initial state is taken as zero and no state is written.
- *     Non-negative slot ids must be distinct within one call (duplicates
- *     race).
+ *     An id equal to the id of an earlier sequence in the same index array
+ *     also means "no slot" (only the first sequence naming a slot reads and
+ *     writes it), so a batch padded by repeating a row -- what the
+ *     reference's CUDA-graph runner does, engine/runtime/cuda_graphs.py:
+ *     478-482 -- advances each slot exactly once.
  *   - v-head j uses q/k head j / (Hv / Hk) (HF's repeat_interleave GQA).
  */
 #ifndef GDN_CAPI_H
@@ -39,7 +42,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 6
+#define GDN_ABI_VERSION 7
 
 typedef enum {
   GDN_OK = 0,

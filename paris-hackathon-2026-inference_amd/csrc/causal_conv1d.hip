@@ -103,8 +103,9 @@ __device__ __forceinline__ float history_at(const ConvArgs &a, int64_t row, int 
   return ld1<T>(static_cast<const T *>(a.st_in) + (row * a.C + c) * SL + (SL - d));
 }
 
+// (n is the same across the calling lanes; a repeated slot id selects no row)
 __device__ __forceinline__ int64_t in_row_of(const ConvArgs &a, int n) {
-  return a.st_in ? pool_row(a.in_idx, n, a.in_rows) : -1;
+  return a.st_in ? pool_row_first(a.in_idx, n, a.in_rows) : -1;
 }
 
 template <typename T, int SL, bool SILU, int TILE_T>
@@ -265,7 +266,7 @@ __global__ __launch_bounds__(CONV_NT) void conv_final_state_kernel(ConvArgs a) {
   const int c = blockIdx.x * CONV_NT + threadIdx.x;
   const int n = blockIdx.y;
   if (c >= a.C) return;
-  const int64_t row = pool_row(a.out_idx, n, a.out_rows);
+  const int64_t row = pool_row_first(a.out_idx, n, a.out_rows);
   if (row < 0) return;
   int64_t s_beg;
   int len;
@@ -301,7 +302,7 @@ __global__ __launch_bounds__(CONV_NT) void conv_update_kernel(UpdArgs a) {
   const int c = blockIdx.x * CONV_NT + threadIdx.x;
   const int n = blockIdx.y;
   if (c >= a.C) return;
-  const int64_t row = pool_row(a.idx, n, a.rows);
+  const int64_t row = pool_row_first(a.idx, n, a.rows);
   T *st = row >= 0 ? static_cast<T *>(a.st) + (row * a.C + c) * SL : nullptr;
   float full[SL + 1];  // cached window (oldest first) followed by the new input
 #pragma unroll

@@ -203,8 +203,10 @@ __global__ __launch_bounds__(256) void chunk_table_kernel(ChunkArgs a) {
     while (k < a.n_seqs && a.chunk_start[k] == a.chunk_start[k + 1]) ++k;  // skip empty sequences
     int64_t *r = a.seqrec + static_cast<int64_t>(n) * SEQREC;
     r[SR_S0] = s0;
-    r[SR_IN] = a.h0 ? pool_row(a.h0_idx, n, a.h0_rows) : -1;
-    r[SR_OUT] = a.hT ? pool_row(a.hT_idx, n, a.hT_rows) : -1;
+    const int64_t rin = a.h0 ? pool_row(a.h0_idx, n, a.h0_rows) : -1;
+    const int64_t rout = a.hT ? pool_row(a.hT_idx, n, a.hT_rows) : -1;
+    r[SR_IN] = rin >= 0 && repeats_earlier_thread(a.h0_idx, n) ? -1 : rin;  // repeated slot ids: no row
+    r[SR_OUT] = rout >= 0 && repeats_earlier_thread(a.hT_idx, n) ? -1 : rout;
     r[SR_CE] = a.chunk_start[n + 1];
     r[SR_LEN] = len;
     r[SR_NXT] = k;
@@ -836,8 +838,8 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_kernel(ChunkArgs a
   const int cs = __builtin_amdgcn_readfirstlane(chunk_start_at(a, n));
   const int ce = __builtin_amdgcn_readfirstlane(max(cs, min(chunk_start_at(a, n + 1), a.max_chunks)));
   const int lo = max(cs, a.seg_begin), hi = min(ce, a.seg_end);
-  const int64_t in_row = a.h0 ? uniform64(pool_row(a.h0_idx, n, a.h0_rows)) : -1;
-  const int64_t out_row = a.hT ? uniform64(pool_row(a.hT_idx, n, a.hT_rows)) : -1;
+  const int64_t in_row = a.h0 ? uniform64(pool_row_first(a.h0_idx, n, a.h0_rows)) : -1;
+  const int64_t out_row = a.hT ? uniform64(pool_row_first(a.hT_idx, n, a.hT_rows)) : -1;
   const int64_t kv = static_cast<int64_t>(DK) * DV;
   const int row0 = 32 * q;  // first state row of a compute wave
   if (cs == ce) {  // empty sequence: the final state is the initial one (handled once)

@@ -19,7 +19,7 @@ __global__ __launch_bounds__(COMMIT_NT) void commit_kernel(float *pool, const in
                                                            int T, int H, int64_t kv) {
   const int h = blockIdx.x % H;
   const int b = blockIdx.x / H;
-  const int64_t slot = pool_row(slot_ids, b, rows);
+  const int64_t slot = pool_row_first(slot_ids, b, rows);  // a repeated slot id commits nothing
   const int a = acc[b];
   if (slot < 0 || a <= 0) return;
   const int t = a > T ? T - 1 : a - 1;
@@ -35,7 +35,7 @@ __global__ __launch_bounds__(COMMIT_NT) void conv_commit_kernel(T *pool, const i
                                                                 int steps) {
   const int b = blockIdx.y;
   const int c = blockIdx.x * COMMIT_NT + threadIdx.x;
-  const int64_t slot = pool_row(slot_ids, b, rows);
+  const int64_t slot = pool_row_first(slot_ids, b, rows);  // a repeated slot id commits nothing
   const int a = acc[b];
   if (c >= C || slot < 0 || a <= 0) return;
   const int first = a > steps ? steps : a;  // window after `first` tokens: history columns [first, first + S)

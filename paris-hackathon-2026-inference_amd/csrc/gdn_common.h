@@ -117,6 +117,46 @@ __device__ __forceinline__ int64_t pool_row(const int64_t *idx, int64_t n, int64
   return (r >= 0 && r < rows) ? r : -1;
 }
 
+// Slot ids repeated within one call.  The reference's CUDA-graph runner pads
+// a batch bucket by repeating row 0 (engine/runtime/cuda_graphs.py:478-482);
+// its cache gathers, computes and scatters with index_copy_, so the copies
+// are harmless there.  Here pools are read and written in place, so only the
+// first row that names a slot uses it: a row whose id equals the id of an
+// earlier row of the same index array selects no row (zero state in, nothing
+// written), like a negative id.
+//
+// repeats_earlier: n must be the same in every active lane (a workgroup- or
+// wave-level sequence index); the active lanes split the earlier ids among
+// themselves and vote.
+__device__ __forceinline__ bool repeats_earlier(const int64_t *idx, int64_t n) {
+  if (!idx || n <= 0) return false;
+  const uint64_t act = __builtin_amdgcn_read_exec();
+  const int cnt = __popcll(act);
+  const int pos = static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(act >> 32),
+                                                            __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(act), 0u)));
+  const int64_t id = idx[n];
+  for (int64_t base = 0; base < n; base += cnt) {
+    const int64_t m = base + pos;
+    if (__ballot(m < n && idx[m] == id)) return true;
+  }
+  return false;
+}
+
+// The same test when n differs between lanes (one thread per sequence).
+__device__ __forceinline__ bool repeats_earlier_thread(const int64_t *idx, int64_t n) {
+  if (!idx || n <= 0) return false;
+  const int64_t id = idx[n];
+  bool hit = false;
+  for (int64_t m = 0; m < n; ++m) hit |= idx[m] == id;
+  return hit;
+}
+
+// pool_row with repeated ids mapped to "no row" (n uniform as for repeats_earlier).
+__device__ __forceinline__ int64_t pool_row_first(const int64_t *idx, int64_t n, int64_t rows) {
+  const int64_t r = pool_row(idx, n, rows);
+  return (r >= 0 && repeats_earlier(idx, n)) ? -1 : r;
+}
+
 // Sequence n's token range [*t0, *t0 + *len), clamped to the [0, total)
 // tokens the caller passed, so that a malformed device-side cu_seqlens can
 // never move an access outside the tensors.

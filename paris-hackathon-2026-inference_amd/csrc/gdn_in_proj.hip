@@ -256,7 +256,15 @@ __global__ __launch_bounds__(64 * IP_WAVES) void in_proj_decode_kernel(InProjArg
   load_w<KS>(wr, rw, kq * S::KPART, a.K, lane);
   __builtin_amdgcn_sched_barrier(0);
   const int64_t id = a.idx ? static_cast<int64_t>(id_raw) : me;  // pool_row's rule
-  const int woff = conv && me < a.M && id >= 0 && id < a.rows ? static_cast<int>((id * a.n[0] + n) * 8) : IP_OOB;
+  // a row whose slot id repeats an earlier row's selects no window (the
+  // ids are uniform loads; the wave waits for them behind the weight stream)
+  bool rep = false;
+  if (conv && a.idx) {
+    const int mlast = min(m0 + 16 * kq + 15, a.M - 1);
+    for (int m = 0; m < mlast; ++m) rep |= m < me && a.idx[m] == id;
+  }
+  const int woff = conv && me < a.M && !rep && id >= 0 && id < a.rows ? static_cast<int>((id * a.n[0] + n) * 8)
+                                                                      : IP_OOB;
   u32x4_t win[2];
   win[0] = __builtin_amdgcn_raw_buffer_load_b128(rp, woff, 0, 0);
   win[1] = __builtin_amdgcn_raw_buffer_load_b128(rp, woff, 16, 0);
@@ -375,7 +383,7 @@ __global__ __launch_bounds__(64 * IP_WAVES) void in_proj_gemv_kernel(InProjArgs 
   const int n = col + c;
   if (mat == 0) {
     const int64_t id = a.idx ? a.idx[m] : m;  // pool_row's rule
-    const bool live = id >= 0 && id < a.rows;
+    const bool live = id >= 0 && id < a.rows && !(m == 1 && a.idx && a.idx[0] == id);  // (row 1 repeating row 0's slot: none)
     uint16_t win[4] = {0, 0, 0, 0};
     uint16_t *wp = a.pool + (live ? (id * a.n[0] + n) * 4 : 0);
     if (live)

@@ -83,7 +83,9 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(RecArgs a) {
   seq_range(a.cu, n, a.T, a.total, &t0, &len);
 
   const int64_t in_row = a.state_in ? pool_row(a.in_idx, n, a.in_rows) : -1;
-  const int64_t out_row = a.state_out ? pool_row(a.out_idx, n, a.out_rows) : -1;
+  int64_t out_row = a.state_out ? pool_row(a.out_idx, n, a.out_rows) : -1;
+  // (rows repeating an earlier row's slot id are found after the state loads
+  // are issued, so that the check adds no latency before the stream)
 
   // The state is touched exactly once per launch: non-temporal loads and
   // stores keep it from displacing reusable lines in the caches.  One
@@ -106,6 +108,11 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(RecArgs a) {
 #pragma unroll
     for (int r = 0; r < RPT; ++r) s[r] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  if (in_row >= 0 && repeats_earlier(a.in_idx, n)) {  // a repeated slot: zero state, like a padding row
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) s[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  if (out_row >= 0 && repeats_earlier(a.out_idx, n)) out_row = -1;  // ... and nothing written
 
   for (int t = 0; t < len; ++t) {
     const int64_t tok = t0 + t;

@@ -17,6 +17,14 @@ kernels.  Differences from the reference entry, all additive:
   zero state (a fresh prefill into its slot) while their final states still
   land in the pool.
 
+Like the reference entry, any ``chunk_size`` and any float q/k/v dtype is
+accepted: the reference falls back to its torch chunk path for
+``chunk_size != 64`` (:383-388) and upcasts q/k/v to fp32 (:396-400).  The
+result of the chunk algorithm does not depend on the chunk size, so the
+kernels always run with 64.  bf16 q/k/v take the MFMA chunk kernels; fp32 and
+fp16 q/k/v take the token-recurrence kernel, which computes in fp32 from the
+inputs as given (bf16 MFMA operands would round them).
+
 The reference's opt-out variable ``PARIS_DISABLE_HELION_DELTA=1`` keeps its
 meaning for :func:`install_delta_rule_monkeypatch` (nothing is patched);
 the functions here always run the HIP kernels and raise if the library is
@@ -58,8 +66,9 @@ def chunk_gated_delta_rule(
 
     Shapes: query, key ``[B, T, Hk, K]``; value ``[B, T, Hv, V]``; g, beta
     ``[B, T, Hv]``; ``initial_state`` ``[N, Hv, K, V]`` fp32 (N = B, or the
-    number of sequences with ``cu_seqlens`` [N+1], B = 1).  K = V = 128,
-    q/k/v bf16.
+    number of sequences with ``cu_seqlens`` [N+1], B = 1).  K = V = 128;
+    q/k/v bf16 (MFMA chunk kernels), fp16 or fp32 (token recurrence);
+    ``chunk_size`` any positive value (computed with 64).
 
     Returns ``(core_attn_out [B, T, Hv, V] in query's dtype,
     last_recurrent_state [N, Hv, K, V] fp32 or None)`` as the reference does
@@ -128,9 +137,10 @@ def _chunk(query, key, value, gates, chunk_size, initial_state, output_final_sta
            has_initial_state=None):
     """Shared body: shape checks, state / workspace plumbing and the launch.
     ``gates`` = (entry point, its gate arguments)."""
-    if chunk_size != CHUNK_SIZE:
-        raise ValueError(f"chunk_size={chunk_size}: the MI355X kernels are built for {CHUNK_SIZE} "
-                         "(the result does not depend on the chunk size)")
+    if int(chunk_size) <= 0:
+        raise ValueError(f"chunk_size={chunk_size} must be positive")
+    if chunk_size != CHUNK_SIZE:  # the chunk algorithm's result does not depend on it
+        log.debug("chunk_size=%s requested; computing with %d", chunk_size, CHUNK_SIZE)
     dev = _lib.require_gpu(query, key, value, initial_state)
     b, t, hk, dk = query.shape
     hv, dv = value.shape[2], value.shape[3]
@@ -179,14 +189,27 @@ def _chunk(query, key, value, gates, chunk_size, initial_state, output_final_sta
             raise ValueError(f"has_initial_state has {has.numel()} entries for {n_seqs} sequences")
         rows = idx if idx is not None else torch.arange(n_seqs, device=dev, dtype=torch.int64)
         h0_idx = torch.where(has, rows, torch.full_like(rows, -1))
-    elif output_final_state:
+    if output_final_state and not inplace_final_state:
         final = hT = torch.empty((n_seqs, hv, dk, dv), dtype=torch.float32, device=dev)
+        hT_idx = None
 
     lib = _lib.load()
-    ws_bytes = lib.gdn_chunk_workspace_bytes(n_seqs, total, hv, dk, dv)
-    ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=dev)
     o = torch.empty((b, t, hv, dv), dtype=query.dtype, device=dev)
     name, gate_args = gates
+    if query.dtype != torch.bfloat16:
+        # fp32 / fp16 q, k, v: the token recurrence, fp32 math on the inputs as given
+        rec = {"gdn_chunk_fwd": "gdn_recurrent_fwd", "gdn_chunk_fwd_gated": "gdn_recurrent_fwd_gated"}[name]
+        st = getattr(lib, rec)(
+            _lib.ptr(qx), _lib.ptr(kx), _lib.ptr(vx), _lib.dtype_code(query, "query"), qs, ks, vs,
+            *gate_args,
+            _lib.ptr(h0), _lib.ptr(h0_idx), _lib.rows_of(h0), _lib.ptr(hT), _lib.ptr(hT_idx), _lib.rows_of(hT),
+            _lib.ptr(o), _lib.dtype_code(o, "o"), None,
+            _lib.ptr(cu), n_seqs, total if cu is not None else t,
+            hk, hv, dk, dv, float(scale), int(bool(use_qk_l2norm_in_kernel)), _lib.stream_of(query))
+        _lib.check(st, rec)
+        return o, final
+    ws_bytes = lib.gdn_chunk_workspace_bytes(n_seqs, total, hv, dk, dv)
+    ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=dev)
     st = getattr(lib, name)(
         _lib.ptr(qx), _lib.ptr(kx), _lib.ptr(vx), _lib.dtype_code(query, "query"), qs, ks, vs,
         *gate_args,

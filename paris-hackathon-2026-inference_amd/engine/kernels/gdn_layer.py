@@ -214,7 +214,12 @@ def _forward_on_pools(self, hidden_states: torch.Tensor, pools, attention_mask: 
     if verify and seq_len != verify:
         raise ValueError(f"verify step bound for {verify} tokens, forward has {seq_len}")
 
-    if pools.decode and seq_len == 1 and _fused_decode_fits(self, hidden_states, conv_pool):
+    # a verify step of any length (one token included) keeps its conv history
+    # and per-token state snapshots for commit_verify, so it never takes the
+    # fused decode input side (which moves the window on) or the chunk kernels
+    # (which keep no snapshots)
+    step = pools.decode and seq_len == 1 and not verify
+    if step and _fused_decode_fits(self, hidden_states, conv_pool):
         mixed_qkv, z, b, a = _fused_decode(self, hidden_states, conv_pool, slots)
     else:
         mixed_qkv = self.in_proj_qkv(hidden_states).transpose(1, 2)  # [B, conv_dim, L]
@@ -222,7 +227,7 @@ def _forward_on_pools(self, hidden_states: torch.Tensor, pools, attention_mask: 
         b = self.in_proj_b(hidden_states)
         a = self.in_proj_a(hidden_states)
         conv_w = self.conv1d.weight.squeeze(1)
-        if pools.decode and seq_len == 1:
+        if step:
             mixed_qkv = causal_conv1d_update(mixed_qkv, conv_pool, conv_w, self.conv1d.bias, self.activation,
                                              conv_state_indices=slots)
         else:
@@ -236,7 +241,7 @@ def _forward_on_pools(self, hidden_states: torch.Tensor, pools, attention_mask: 
     query = query.reshape(batch_size, seq_len, -1, self.head_k_dim)
     key = key.reshape(batch_size, seq_len, -1, self.head_k_dim)
     value = value.reshape(batch_size, seq_len, -1, self.head_v_dim)
-    if pools.decode and seq_len <= _RECURRENT_MAX_T:
+    if verify or (pools.decode and seq_len <= _RECURRENT_MAX_T):
         core, _ = fused_recurrent_gated_delta_rule_from_projections(
             query, key, value, a, b, self.A_log, self.dt_bias, initial_state=rec_pool,
             use_qk_l2norm_in_kernel=True, ssm_state_indices=slots, inplace_final_state=True,

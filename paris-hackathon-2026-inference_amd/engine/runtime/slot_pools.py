@@ -109,6 +109,8 @@ class GDNSlotPools:
             raise ValueError(f"batch of {b} rows exceeds max_batch={self.max_batch}")
         if verify_tokens and is_prefill:
             raise ValueError("verify_tokens applies to decode steps only")
+        if int(verify_tokens) < 0:
+            raise ValueError(f"verify_tokens={verify_tokens} must be >= 0 (0: no verify step)")
         ok = (ids >= 0) & (ids < self.num_slots)
         if b > 1:
             earlier = torch.tril(ids.unsqueeze(0) == ids.unsqueeze(1), diagonal=-1).any(dim=1)

@@ -42,7 +42,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.gdn_abi_version() == _lib.ABI_VERSION == 6
+    assert lib.gdn_abi_version() == _lib.ABI_VERSION == 7
 
 
 def _rec_call(lib, **over):

@@ -115,8 +115,9 @@ def test_config3_varlen_after_conv():
                                                      c["h0"].numpy())
     err_o = np.abs(np64(o) - o_ref).max()
     err_s = gdn.state_rel_err(np64(s), s_ref)
-    print(f"config3: max|o-o_ref|={err_o:.3e} state rel={err_s:.3e} conv max err="
-          f"{np.abs(np64(y) - y_ref).max():.3e}")
+    err_c = (np.abs(np64(y) - y_ref) / np.maximum(1.0, np.abs(y_ref))).max()
+    print(f"config3: max|o-o_ref|={err_o:.3e} state rel={err_s:.3e} conv max err (rel to max(1,|y|))={err_c:.3e}")
+    assert err_c <= 2e-2  # conv of the bf16 projection with zero history: bf16 output rounding
     assert err_o < O_TOL and err_s < S_TOL
 
 
@@ -210,3 +211,93 @@ def test_segments_equal_split_calls():
         assert torch.equal(o[:, a:b], oi) and torch.equal(pool[slot:slot + 1], si), i
     untouched = [r for r in range(pool.shape[0]) if r not in slots.tolist()]
     assert torch.equal(pool[untouched], pool0[untouched])
+
+
+@pytest.mark.parametrize("dtype,t", [(torch.float32, 256), (torch.float16, 200)])
+def test_chunk_entry_accepts_fp32_and_fp16_inputs(dtype, t):
+    """The reference entry upcasts any float q/k/v (delta_rule.py:396-400):
+    fp32 at configuration 0's shape and fp16 at a ragged length, with an
+    initial state, against the oracle.  fp32 / fp16 inputs run the token
+    recurrence in fp32 (bf16 MFMA operands would round them), so the
+    tolerance is the fp32 one of configuration 0."""
+    print(f"chunk entry dtype={dtype} T={t}", flush=True)
+    c = configs.config0(seed=61, t=t)
+    h0 = torch.randn(1, 32, 128, 128, generator=torch.Generator().manual_seed(62)) * 0.1
+    q, k, v = (c[x].to(dtype) for x in ("q", "k", "v"))
+    o, s = chunk_gated_delta_rule(q.to(DEV), k.to(DEV), v.to(DEV), c["g"].to(DEV), c["beta"].to(DEV),
+                                  initial_state=h0.to(DEV), output_final_state=True, use_qk_l2norm_in_kernel=True)
+    assert o.dtype == dtype and s.dtype == torch.float32
+    o_ref, s_ref = gdn.chunk_gated_delta_rule(*(np64(x) for x in (q, k, v)), c["g"].numpy(), c["beta"].numpy(),
+                                              initial_state=h0.numpy())
+    err_o = np.abs(np64(o) - o_ref).max()
+    err_s = gdn.state_rel_err(np64(s), s_ref)
+    print(f"  max|o-o_ref|={err_o:.3e} state rel={err_s:.3e}")
+    assert err_o < (1e-4 if dtype == torch.float32 else 2e-3)  # fp16 output rounding
+    assert err_s < 1e-5
+
+
+def test_chunk_size_other_than_64_gives_the_same_result():
+    """The reference falls back to its torch path for chunk_size != 64
+    (delta_rule.py:383-388); the chunk algorithm's result does not depend on
+    the chunk size, so the kernels compute with 64: bit-identical results."""
+    c = configs.config2(seed=63, t=300)
+    args = [c[x].to(DEV) for x in ("q", "k", "v", "g", "beta")]
+    o64, s64 = chunk_gated_delta_rule(*args, output_final_state=True, use_qk_l2norm_in_kernel=True)
+    for cs in (32, 16, 128):
+        o, s = chunk_gated_delta_rule(*args, chunk_size=cs, output_final_state=True, use_qk_l2norm_in_kernel=True)
+        assert torch.equal(o, o64) and torch.equal(s, s64), cs
+    o_ref, s_ref = oracle_chunk(c)
+    assert np.abs(np64(o64) - o_ref).max() < O_TOL and gdn.state_rel_err(np64(s64), s_ref) < S_TOL
+
+
+def test_has_initial_state_with_a_new_final_state():
+    """has_initial_state with output_final_state (not in place) returns a new
+    final-state tensor: rows marked False start from zero, the pool is left
+    as it was."""
+    c = configs.config2(seed=64, t=2 * 70)
+    cu = torch.tensor([0, 70, 140], dtype=torch.int32)
+    pool = torch.randn(4, 32, 128, 128, generator=torch.Generator().manual_seed(65)) * 0.1
+    ids = torch.tensor([3, 1])
+    has = torch.tensor([True, False])
+    pool_d = pool.to(DEV)
+    o, s = chunk_gated_delta_rule(*(c[x].to(DEV) for x in ("q", "k", "v", "g", "beta")), initial_state=pool_d,
+                                  ssm_state_indices=ids.to(DEV), has_initial_state=has.to(DEV),
+                                  output_final_state=True, use_qk_l2norm_in_kernel=True, cu_seqlens=cu.to(DEV))
+    assert s is not None and s.shape == (2, 32, 128, 128)
+    assert torch.equal(pool_d.cpu(), pool)
+    h0 = np.stack([pool[3].numpy(), np.zeros((32, 128, 128), np.float32)])
+    o_ref, s_ref = gdn.chunk_gated_delta_rule_varlen(*(c[x].float().numpy() for x in ("q", "k", "v", "g", "beta")),
+                                                     cu.numpy(), h0)
+    assert np.abs(np64(o) - o_ref).max() < O_TOL and gdn.state_rel_err(np64(s), s_ref) < S_TOL
+
+
+def test_repeated_slot_ids_advance_a_slot_once():
+    """ids [s, s, t] with identical rows 0 and 1 (a bucket padded by
+    repeating row 0, cuda_graphs.py:478-482): slot s advances exactly once,
+    to the oracle's state for row 0, row 1 runs as a padding row (zero
+    state, nothing written), slot t as usual; the same for the prefill
+    (chunk) and decode (recurrent) kernels."""
+    c = configs.config2(seed=66, t=3 * 50)
+    x = {k: c[k].view(1, 3, 50, *c[k].shape[2:])[0] for k in ("q", "k", "v", "g", "beta")}
+    x = {k: torch.stack([v[0], v[0], v[2]]) for k, v in x.items()}  # rows 0 and 1 identical
+    pool = torch.randn(5, 32, 128, 128, generator=torch.Generator().manual_seed(67)) * 0.1
+    ids = torch.tensor([2, 2, 4])
+    s_ref_rows = []
+    for r, row in ((0, 2), (2, 4)):
+        _, sr = gdn.chunk_gated_delta_rule(*(x[k][r:r + 1].float().numpy() for k in ("q", "k", "v", "g", "beta")),
+                                           initial_state=pool[row:row + 1].numpy())
+        s_ref_rows.append(sr[0])
+    o0_pad, _ = gdn.chunk_gated_delta_rule(*(x[k][1:2].float().numpy() for k in ("q", "k", "v", "g", "beta")))
+    for fn in ("chunk", "recurrent"):
+        pd = pool.to(DEV)
+        args = [x[k].to(DEV) for k in ("q", "k", "v", "g", "beta")]
+        if fn == "chunk":
+            o, _ = chunk_gated_delta_rule(*args, initial_state=pd, ssm_state_indices=ids.to(DEV),
+                                          inplace_final_state=True, use_qk_l2norm_in_kernel=True)
+        else:
+            o, _ = fused_recurrent_gated_delta_rule(*args, initial_state=pd, ssm_state_indices=ids.to(DEV),
+                                                    inplace_final_state=True, use_qk_l2norm_in_kernel=True)
+        assert gdn.state_rel_err(np64(pd[2])[None], s_ref_rows[0][None]) < S_TOL, fn
+        assert gdn.state_rel_err(np64(pd[4])[None], s_ref_rows[1][None]) < S_TOL, fn
+        assert torch.equal(pd[[0, 1, 3]].cpu(), pool[[0, 1, 3]]), fn
+        assert np.abs(np64(o[1]) - o0_pad[0]).max() < O_TOL, fn  # the repeated row: zero initial state

@@ -156,3 +156,48 @@ def test_long_and_short_tiles_agree():
     y_ref, _ = conv.causal_conv1d_fn(x[:, :300].transpose(1, 2).float().numpy(), w.float().numpy(),
                                      activation="silu")
     assert bf16_close(y_long[:, :, :300], y_ref)
+
+
+def test_conv_state_commit_matches_update_over_the_accepted_prefix():
+    """gdn_conv_state_commit against the oracle: a verify step's history is
+    the window before the step followed by its T inputs; after committing
+    ``a`` accepted tokens a slot must hold the window that
+    causal_conv1d_update over exactly those ``a`` tokens leaves (the conv
+    half of the rollback spec_decode.py:81-87 leaves unimplemented).
+    a <= 0 and a repeated slot id leave the slot untouched."""
+    from engine.kernels import gdn_conv_state_commit
+    gen = torch.Generator().manual_seed(71)
+    n, c, s, t = 5, 256, 4, 6
+    win0 = torch.randn(n, c, s, generator=gen).to(torch.bfloat16)
+    x = torch.randn(n, c, t, generator=gen).to(torch.bfloat16)
+    w = torch.randn(c, 4, generator=gen).to(torch.bfloat16)
+    hist = torch.cat([win0, x], dim=2)
+    slots = torch.tensor([3, 0, 6, 3, 2])  # row 3 repeats row 0's slot
+    acc = torch.tensor([2, 6, 1, 4, 0])
+    pool0 = torch.randn(7, c, s, generator=gen).to(torch.bfloat16)
+    pool = pool0.to(DEV)
+    gdn_conv_state_commit(pool, slots.to(DEV), hist.to(DEV), acc.to(DEV))
+    for r in (0, 1, 2):
+        a = int(acc[r])
+        _, st_ref = conv.causal_conv1d_update(np64(x[r:r + 1, :, :a]), np64(win0[r:r + 1]), np64(w))
+        assert np.array_equal(np64(pool[int(slots[r])])[None], st_ref), r
+    assert torch.equal(pool[[1, 2, 4, 5]].cpu(), pool0[[1, 2, 4, 5]])  # a = 0 (row 4), unused slots
+
+
+def test_update_with_repeated_slot_ids_advances_a_slot_once():
+    """ids [s, s, t] with identical rows 0 and 1: slot s's window moves by one
+    token, row 1 runs as a padding row (zero window, nothing written)."""
+    gen = torch.Generator().manual_seed(72)
+    c = 512
+    pool0 = torch.randn(4, c, 4, generator=gen).to(torch.bfloat16)
+    x = torch.randn(2, c, 1, generator=gen).to(torch.bfloat16)
+    x = torch.cat([x[:1], x[:1], x[1:]])  # rows 0 and 1 identical
+    w = torch.randn(c, 4, generator=gen).to(torch.bfloat16)
+    pool = pool0.to(DEV)
+    y = causal_conv1d_update(x.to(DEV), pool, w.to(DEV), None, "silu", conv_state_indices=torch.tensor([2, 2, 0]).to(DEV))
+    y0, st0 = conv.causal_conv1d_update(np64(x[:1]), np64(pool0[2:3]), np64(w))
+    y1, _ = conv.causal_conv1d_update(np64(x[1:2]), np.zeros((1, c, 4)), np64(w))
+    y2, st2 = conv.causal_conv1d_update(np64(x[2:3]), np64(pool0[0:1]), np64(w))
+    assert bf16_close(y[0:1], y0) and bf16_close(y[1:2], y1) and bf16_close(y[2:3], y2)
+    assert np.array_equal(np64(pool[2])[None], st0) and np.array_equal(np64(pool[0])[None], st2)
+    assert torch.equal(pool[[1, 3]].cpu(), pool0[[1, 3]])

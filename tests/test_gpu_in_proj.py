@@ -18,6 +18,8 @@ import torch
 
 from oracle import proj
 
+import layer_cases as lc
+
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not torch.cuda.is_available(), reason="needs an MI355X")]
 
@@ -206,115 +208,60 @@ def test_graph_replays_match_eager():
         assert torch.equal(pool, after), step
 
 
-def test_layer_decode_takes_the_fused_kernel_and_matches_hf(monkeypatch):
-    """A 1024-wide GDN layer (the fused kernel's smallest K): prefill through
-    the slot pools, then decode steps, against HF's module per sequence."""
-    from transformers.cache_utils import DynamicCache
-    from transformers.models.qwen3_5_moe import modeling_qwen3_5_moe as hf
-    from transformers.models.qwen3_5_moe.configuration_qwen3_5_moe import Qwen3_5MoeTextConfig
-    from engine.kernels import gated_delta_net_forward, gdn_layer
-    from engine.runtime import GDNSlotPools
-    from oracle import gdn
-
-    cfg = Qwen3_5MoeTextConfig(hidden_size=1024, num_hidden_layers=1, layer_types=["linear_attention"],
-                               linear_num_key_heads=2, linear_num_value_heads=4, linear_key_head_dim=128,
-                               linear_value_head_dim=128, linear_conv_kernel_dim=4, rms_norm_eps=1e-6)
-    torch.manual_seed(84)
-    ref = hf.Qwen3_5MoeGatedDeltaNet(cfg, layer_idx=0).eval()
-    with torch.no_grad():
-        for p in ref.parameters():
-            p.copy_(p.to(torch.bfloat16).float())
-        ref.A_log.copy_(torch.log(torch.empty(4).uniform_(0.5, 4.0)).to(torch.bfloat16).float())
-    layer = hf.Qwen3_5MoeGatedDeltaNet(cfg, layer_idx=0).eval()
-    layer.load_state_dict(ref.state_dict())
-    layer = layer.to(DEV, torch.bfloat16)
-
+def _count_calls(monkeypatch):
+    from engine.kernels import gdn_layer
     calls, out_calls = [], []
     real = gdn_layer.gdn_in_proj_decode
     monkeypatch.setattr(gdn_layer, "gdn_in_proj_decode", lambda *a, **k: calls.append(1) or real(*a, **k))
     real_out = gdn_layer.gdn_out_proj_decode
     monkeypatch.setattr(gdn_layer, "gdn_out_proj_decode", lambda *a, **k: out_calls.append(1) or real_out(*a, **k))
+    return calls, out_calls
 
-    pools = GDNSlotPools.allocate([0], 6, conv_dim=2 * 2 * 128 + 4 * 128, num_v_heads=4, device=torch.device(DEV))
+
+def _layer_on_pools(name, slots, n_pre, n_dec, num_slots, state_heads, monkeypatch):
+    """Sequences prefilled one at a time into their slots, then batched decode
+    steps that take the fused input side, against HF's module run per
+    sequence with its own cache (fixture, tests/golden/make_golden.py)."""
+    from engine.kernels import gated_delta_net_forward
+    from engine.runtime import GDNSlotPools
+    golden = lc.load_golden()
+    cfg, layer = lc.gpu_layer(name, golden)
+    calls, out_calls = _count_calls(monkeypatch)
+    hv = cfg.linear_num_value_heads
+    conv_dim = 2 * cfg.linear_num_key_heads * 128 + hv * 128
+    pools = GDNSlotPools.allocate([0], num_slots, conv_dim=conv_dim, num_v_heads=hv, device=torch.device(DEV))
     cache = types.SimpleNamespace(gdn_slot_pools=pools)
-    gen = torch.Generator().manual_seed(85)
-    slots, lens = [4, 1, 2], [40, 7, 70]
-    hf_caches = [DynamicCache(config=cfg) for _ in slots]
-
-    def close(y, y_ref):
-        return np.abs(np64(y) - np64(y_ref)).max() <= 3e-2 * np.abs(np64(y_ref)).max()
-
-    for s, n, c in zip(slots, lens, hf_caches):
-        x = torch.randn(1, n, 1024, generator=gen).to(torch.bfloat16).float()
-        pools.bind(torch.tensor([s]), is_prefill=True)
+    for i in range(n_pre):
+        print(f"{name}: prefill {i} into slot {slots[i]}", flush=True)
+        pools.bind(torch.tensor([slots[i]]), is_prefill=True)
         with torch.no_grad():
-            y = gated_delta_net_forward(layer, x.to(DEV, torch.bfloat16), cache_params=cache)
-            assert close(y, ref(x, cache_params=c))
+            y = gated_delta_net_forward(layer, torch.from_numpy(golden[f"{name}.pre{i}.x"]).to(DEV, torch.bfloat16),
+                                        cache_params=cache)
+        assert lc.layer_close(y, golden[f"{name}.pre{i}.y"]), i
     assert not calls
-    for _ in range(3):
-        x = torch.randn(3, 1, 1024, generator=gen).to(torch.bfloat16).float()
+    for step in range(n_dec):
         pools.bind(torch.tensor(slots), is_prefill=False)
         with torch.no_grad():
-            y = gated_delta_net_forward(layer, x.to(DEV, torch.bfloat16), cache_params=cache)
-            for r, c in enumerate(hf_caches):
-                assert close(y[r:r + 1], ref(x[r:r + 1], cache_params=c)), r
-    assert len(calls) == 3 and len(out_calls) == 3
+            y = gated_delta_net_forward(layer, torch.from_numpy(golden[f"{name}.dec{step}.x"]).to(DEV, torch.bfloat16),
+                                        cache_params=cache)
+        assert lc.layer_close(y, golden[f"{name}.dec{step}.y"]), step
+    assert len(calls) == n_dec and len(out_calls) == n_dec
     conv_pool, rec_pool = pools.layer(0)
-    for s, c in zip(slots, hf_caches):
-        assert gdn.state_rel_err(np64(rec_pool[s])[None], np64(c.layers[0].recurrent_states[0])) < 1e-2
-        assert np.abs(np64(conv_pool[s])[None] - np64(c.layers[0].conv_states[0])).max() < 2e-2
+    for i, s in enumerate(slots):
+        assert lc.state_close(rec_pool[s], golden[f"{name}.seq{i}.state"], state_heads), i
+        assert lc.conv_close(conv_pool[s], golden[f"{name}.seq{i}.conv"]), i
+
+
+def test_layer_decode_takes_the_fused_kernel_and_matches_hf(monkeypatch):
+    """A 1024-wide GDN layer (the fused kernel's smallest K): three sequences
+    prefilled through the slot pools, then decode steps."""
+    _layer_on_pools("w1024", [4, 1, 2], 3, 3, 6, [0, 3], monkeypatch)
 
 
 def test_layer_decode_at_model_shapes_takes_the_fused_kernel(monkeypatch):
-    """The Qwen3.5-MoE GDN layer (hidden 2048, 16 k-heads, 32 v-heads):
-    two sequences prefilled into slots, then batched decode steps that take
-    the fused input side, against HF's module per sequence."""
-    from transformers.cache_utils import DynamicCache
-    from transformers.models.qwen3_5_moe import modeling_qwen3_5_moe as hf
-    from transformers.models.qwen3_5_moe.configuration_qwen3_5_moe import Qwen3_5MoeTextConfig
-    from engine.kernels import gated_delta_net_forward, gdn_layer
-    from engine.runtime import GDNSlotPools
-
-    cfg = Qwen3_5MoeTextConfig(hidden_size=2048, num_hidden_layers=1, layer_types=["linear_attention"],
-                               linear_num_key_heads=16, linear_num_value_heads=32, linear_key_head_dim=128,
-                               linear_value_head_dim=128, linear_conv_kernel_dim=4, rms_norm_eps=1e-6)
-    torch.manual_seed(96)
-    ref = hf.Qwen3_5MoeGatedDeltaNet(cfg, layer_idx=0).eval()
-    with torch.no_grad():
-        for p in ref.parameters():
-            p.copy_(p.to(torch.bfloat16).float())
-    layer = hf.Qwen3_5MoeGatedDeltaNet(cfg, layer_idx=0).eval()
-    layer.load_state_dict(ref.state_dict())
-    layer = layer.to(DEV, torch.bfloat16)
-    calls, out_calls = [], []
-    real = gdn_layer.gdn_in_proj_decode
-    monkeypatch.setattr(gdn_layer, "gdn_in_proj_decode", lambda *a, **k: calls.append(1) or real(*a, **k))
-    real_out = gdn_layer.gdn_out_proj_decode
-    monkeypatch.setattr(gdn_layer, "gdn_out_proj_decode", lambda *a, **k: out_calls.append(1) or real_out(*a, **k))
-
-    pools = GDNSlotPools.allocate([0], 4, conv_dim=2 * 16 * 128 + 32 * 128, num_v_heads=32, device=torch.device(DEV))
-    cache = types.SimpleNamespace(gdn_slot_pools=pools)
-    gen = torch.Generator().manual_seed(97)
-    slots, lens = [2, 0], [20, 9]
-    hf_caches = [DynamicCache(config=cfg) for _ in slots]
-
-    def close(y, y_ref):
-        return np.abs(np64(y) - np64(y_ref)).max() <= 3e-2 * np.abs(np64(y_ref)).max()
-
-    for s, n, c in zip(slots, lens, hf_caches):
-        x = torch.randn(1, n, 2048, generator=gen).to(torch.bfloat16).float()
-        pools.bind(torch.tensor([s]), is_prefill=True)
-        with torch.no_grad():
-            assert close(gated_delta_net_forward(layer, x.to(DEV, torch.bfloat16), cache_params=cache),
-                         ref(x, cache_params=c))
-    for step in range(2):
-        x = torch.randn(2, 1, 2048, generator=gen).to(torch.bfloat16).float()
-        pools.bind(torch.tensor(slots), is_prefill=False)
-        with torch.no_grad():
-            y = gated_delta_net_forward(layer, x.to(DEV, torch.bfloat16), cache_params=cache)
-            for r, c in enumerate(hf_caches):
-                assert close(y[r:r + 1], ref(x[r:r + 1], cache_params=c)), (step, r)
-    assert len(calls) == 2 and len(out_calls) == 2
+    """The Qwen3.5-MoE GDN layer (hidden 2048, 16 k-heads, 32 v-heads): two
+    sequences prefilled into slots, then batched decode steps."""
+    _layer_on_pools("model", [2, 0], 2, 2, 4, lc.MODEL_STATE_HEADS, monkeypatch)
 
 
 def run_out(x, w):

@@ -6,8 +6,9 @@
 * the gated RMS norm kernel against the oracle (pinned by HF's module);
 * the whole layer forward (``gated_delta_net_forward``: native GQA, fused
   gates, HIP conv / core / norm) against HF's own ``Qwen3_5MoeGatedDeltaNet``
-  forward run in fp32 on the CPU with the same (bf16-representable) weights
-  and inputs, for a prefill and for cached decode steps.
+  forward in fp32 with the same (bf16-exact) weights and inputs, for a
+  prefill and for cached decode steps; HF's values are fixtures written in
+  the build container (tests/golden/make_golden.py, golden_layer.npz).
 
 Tolerances: core outputs bf16 max abs error <= 2e-2 and fp32 states relative
 error <= 1e-3 (north star); the layer output, after five bf16 roundings of
@@ -18,6 +19,8 @@ import pytest
 import torch
 
 from oracle import gdn
+
+import layer_cases as lc
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not torch.cuda.is_available(), reason="needs an MI355X")]
@@ -106,67 +109,38 @@ def test_rms_norm_gated_matches_oracle(dtype, w_dtype, h):
 
 
 # ---------------------------------------------------------------- the HF layer
-def tiny_layer():
-    from transformers.models.qwen3_5_moe.configuration_qwen3_5_moe import Qwen3_5MoeTextConfig
-    from transformers.models.qwen3_5_moe import modeling_qwen3_5_moe as hf
-    cfg = Qwen3_5MoeTextConfig(hidden_size=64, num_hidden_layers=1, layer_types=["linear_attention"],
-                               linear_num_key_heads=2, linear_num_value_heads=4, linear_key_head_dim=128,
-                               linear_value_head_dim=128, linear_conv_kernel_dim=4, rms_norm_eps=1e-6)
-    torch.manual_seed(34)
-    layer = hf.Qwen3_5MoeGatedDeltaNet(cfg, layer_idx=0).eval()
-    with torch.no_grad():
-        for p in layer.parameters():
-            p.copy_(bf16r(p))
-        layer.norm.weight.copy_(bf16r(1.0 + 0.2 * torch.randn(128)))
-        layer.dt_bias.copy_(bf16r(torch.randn(4)))
-        layer.A_log.copy_(bf16r(torch.log(torch.empty(4).uniform_(0.5, 4.0))))
-    return cfg, hf, layer
-
-
-def hf_torch_paths_intact(hf):
-    # the reference run below must use HF's own torch paths, not patched ones
-    from engine import kernels
-    return all(getattr(hf, n) is not getattr(kernels, m, None) for n, m in (
-        ("torch_chunk_gated_delta_rule", "chunk_gated_delta_rule"),
-        ("torch_recurrent_gated_delta_rule", "recurrent_gated_delta_rule"),
-        ("causal_conv1d_fn", "causal_conv1d_fn"), ("causal_conv1d_update", "causal_conv1d_update")))
-
-
 def test_layer_prefill_matches_hf_module():
+    """The layer forward without a cache against HF's forward (fixture)."""
     from engine.kernels import gated_delta_net_forward
-    cfg, hf, layer = tiny_layer()
-    if not hf_torch_paths_intact(hf):
-        pytest.skip("HF module functions were patched in this process")
-    x = bf16r(torch.randn(1, 150, 64, generator=torch.Generator().manual_seed(35)))
+    golden = lc.load_golden()
+    _, gpu = lc.gpu_layer("tiny", golden)
+    x = torch.from_numpy(golden["prefill.x"])
     with torch.no_grad():
-        y_ref = layer(x)                                   # HF forward, fp32, CPU
-        gpu = layer.to(DEV, torch.bfloat16)
         y = gated_delta_net_forward(gpu, x.to(DEV, torch.bfloat16))
-    err = np.abs(np64(y) - np64(y_ref)).max()
-    print(f"layer prefill: max|y-y_ref|={err:.3e} max|y_ref|={np64(y_ref).__abs__().max():.3e}")
-    assert err < LAYER_TOL * np.abs(np64(y_ref)).max()
+    y_ref = golden["prefill.y"]
+    err = np.abs(np64(y) - y_ref).max()
+    print(f"layer prefill: max|y-y_ref|={err:.3e} max|y_ref|={np.abs(y_ref).max():.3e}")
+    assert lc.layer_close(y, y_ref, LAYER_TOL)
 
 
 def test_layer_decode_with_cache_matches_hf_module():
+    """Prefill then three cached decode steps through transformers' own
+    DynamicCache (HF's cache protocol, the kernels updating its tensors),
+    against HF's forward with its own cache (fixture): outputs, the final
+    recurrent states and conv windows."""
     from transformers.cache_utils import DynamicCache
     from engine.kernels import gated_delta_net_forward
-    cfg, hf, layer = tiny_layer()
-    if not hf_torch_paths_intact(hf):
-        pytest.skip("HF module functions were patched in this process")
-    gen = torch.Generator().manual_seed(36)
-    steps = [bf16r(torch.randn(2, 70, 64, generator=gen))] + \
-        [bf16r(torch.randn(2, 1, 64, generator=gen)) for _ in range(3)]
-    cache_ref = DynamicCache(config=cfg)
+    golden = lc.load_golden()
+    cfg, gpu = lc.gpu_layer("tiny", golden)
+    cache = DynamicCache(config=cfg)
     with torch.no_grad():
-        y_ref = [layer(s, cache_params=cache_ref) for s in steps]   # prefill, then 3 cached decode steps
-        gpu = layer.to(DEV, torch.bfloat16)
-        cache = DynamicCache(config=cfg)
-        y = [gated_delta_net_forward(gpu, s.to(DEV, torch.bfloat16), cache_params=cache) for s in steps]
-    for i, (a, r) in enumerate(zip(y, y_ref)):
-        err = np.abs(np64(a) - np64(r)).max()
-        print(f"layer step {i}: max|y-y_ref|={err:.3e}")
-        assert err < LAYER_TOL * np.abs(np64(r)).max(), i
-    s_ref = np64(cache_ref.layers[0].recurrent_states[0])
+        for i in range(4):
+            y = gated_delta_net_forward(gpu, torch.from_numpy(golden[f"cache.x{i}"]).to(DEV, torch.bfloat16),
+                                        cache_params=cache)
+            err = np.abs(np64(y) - golden[f"cache.y{i}"]).max()
+            print(f"layer step {i}: max|y-y_ref|={err:.3e}")
+            assert lc.layer_close(y, golden[f"cache.y{i}"], LAYER_TOL), i
+    s_ref = golden["cache.state"].astype(np.float64)
     s_gpu = np64(cache.layers[0].recurrent_states[0])
     assert gdn.state_rel_err(s_gpu, s_ref) < 1e-2   # states after bf16 projections and conv
-    assert np.abs(np64(cache.layers[0].conv_states[0]) - np64(cache_ref.layers[0].conv_states[0])).max() < 2e-2
+    assert np.abs(np64(cache.layers[0].conv_states[0]) - golden["cache.conv"]).max() < 2e-2
