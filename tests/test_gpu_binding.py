@@ -68,7 +68,7 @@ def test_installer_binds_hf_gdn_functions_to_the_hip_entry_points(patched_hf):
     assert hf.causal_conv1d_fn is kernels.causal_conv1d_fn
     assert hf.causal_conv1d_update is kernels.causal_conv1d_update
     # the layer forward itself stays HF's (only its module functions are rebound)
-    assert hf.Qwen3_5MoeGatedDeltaNet.forward.__module__ == hf.__name__
+    assert hf.Qwen3_5MoeGatedDeltaNet.forward is not kernels.gated_delta_net_forward
 
 
 def test_hf_forward_through_the_installed_kernels_matches_hf(patched_hf):
