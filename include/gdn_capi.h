@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 7
+#define GDN_ABI_VERSION 8
 
 typedef enum {
   GDN_OK = 0,
@@ -288,6 +288,25 @@ int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w_qkv, const
 size_t gdn_out_proj_workspace_bytes(int32_t M, int32_t K, int32_t N);
 int gdn_out_proj_decode(const void *x, int64_t x_stride, const void *w, int32_t M, int32_t K, int32_t N,
                         void *y, int64_t y_stride, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * gdn_out_proj_decode without a workspace argument: allocates nothing.
+ *
+ * No counterpart in the reference.  It is for callers that cannot allocate
+ * device memory at call time -- code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc: the split-K partial sums go to a
+ * scratch array built into the library (GDN_OUT_PROJ_NOALLOC_MAX_BYTES per
+ * GPU, held from the library's first use on that GPU until the process
+ * ends), so the caller passes only x, w and y.  Calls that need more partial
+ * sums than that (gdn_out_proj_workspace_bytes(M, K, N) > the maximum; 64
+ * rows at K = 4096, N = 2048 need 4 MiB) fail with GDN_ERR_UNSUPPORTED.  All
+ * calls on one GPU share the scratch: calls that overlap on one GPU (on two
+ * streams) race.  The stream must belong to the current device.  Results are
+ * bit-identical to gdn_out_proj_decode's.
+ */
+#define GDN_OUT_PROJ_NOALLOC_MAX_BYTES ((size_t)8 << 20)
+int gdn_out_proj_decode_noalloc(const void *x, int64_t x_stride, const void *w, int32_t M, int32_t K, int32_t N,
+                                void *y, int64_t y_stride, void *stream);
 
 /*
  * Speculative-verify commit: pool[slot_ids[b]] = snapshots[b, accepted_len[b]-1].

@@ -40,6 +40,8 @@
 // small kernel adds the partials in split order and writes bf16.  (Letting
 // the last workgroup of a column block add them needs agent-scope fences,
 // whose L2 writeback and invalidate per workgroup measured 111 us.)
+#include <mutex>
+
 #include "gdn_common.h"
 
 namespace gdn {
@@ -603,6 +605,61 @@ extern "C" int gdn_out_proj_decode(const void *x, int64_t x_stride, const void *
     default: hipLaunchKernelGGL(out_proj_sum_kernel<0>, rgrid, dim3(OP_RED_NT), 0, s, args); break;
   }
   return check_launch("gdn_out_proj_decode");
+}
+
+namespace gdn {
+namespace {
+
+// Scratch of gdn_out_proj_decode_noalloc: the split-K partial sums, in a
+// file-scope device array instead of a caller workspace.  Each GPU the
+// library runs on holds its own copy (one per loaded code object) until the
+// process ends; every call on that GPU shares it, so calls that overlap on
+// one GPU (two streams) race.  The partial kernel writes every partial the
+// sum kernel reads, so nothing is cleared between calls.
+constexpr size_t OP_SCRATCH_BYTES = GDN_OUT_PROJ_NOALLOC_MAX_BYTES;
+__device__ __align__(256) float scratch[OP_SCRATCH_BYTES / sizeof(float)];
+
+// `scratch` as a device address, per device: in host code the array's name
+// is only a host-side stand-in, so kernels get the address that
+// hipGetSymbolAddress returns with that device current (looked up on the
+// first call on each device).
+constexpr int OP_MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void *scratch_addr[OP_MAX_DEVICES];
+
+int scratch_on_current_device(void **out, const char *name) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= OP_MAX_DEVICES)
+    return fail(GDN_ERR_LAUNCH, "%s: no current device (or device index %d beyond %d)", name, dev, OP_MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_addr[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(GDN_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", name, dev,
+                  hipGetErrorString(e));
+    scratch_addr[dev] = p;
+  }
+  *out = scratch_addr[dev];
+  return GDN_OK;
+}
+
+}  // namespace
+}  // namespace gdn
+
+extern "C" int gdn_out_proj_decode_noalloc(const void *x, int64_t x_stride, const void *w, int32_t M, int32_t K,
+                                           int32_t N, void *y, int64_t y_stride, void *stream) {
+  using namespace gdn;
+  const size_t need = gdn_out_proj_workspace_bytes(M, K, N);
+  if (need > OP_SCRATCH_BYTES)
+    return fail(GDN_ERR_UNSUPPORTED,
+                "gdn_out_proj_decode_noalloc: M=%d K=%d N=%d needs %zu bytes of partial sums, the built-in scratch "
+                "holds %zu (use gdn_out_proj_decode with a workspace)",
+                M, K, N, need, OP_SCRATCH_BYTES);
+  void *ws = nullptr;
+  const int st = scratch_on_current_device(&ws, "gdn_out_proj_decode_noalloc");
+  if (st != GDN_OK) return st;
+  return gdn_out_proj_decode(x, x_stride, w, M, K, N, y, y_stride, ws, OP_SCRATCH_BYTES, stream);
 }
 
 extern "C" int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w_qkv, const void *w_z,

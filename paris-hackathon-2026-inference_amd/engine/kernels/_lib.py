@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libgdn_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 GDN_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
@@ -96,6 +96,10 @@ SIGNATURES = {
         _i32, _i32, _i32,                           # M K N
         _c_void_p, _i64,                            # y y_stride
         _c_void_p, _size, _c_void_p]),              # workspace bytes stream
+    "gdn_out_proj_decode_noalloc": (_int, [
+        _c_void_p, _i64, _c_void_p,                 # x x_stride w
+        _i32, _i32, _i32,                           # M K N
+        _c_void_p, _i64, _c_void_p]),               # y y_stride stream
     "causal_conv1d_fwd": (_int, [
         _c_void_p, _i64, _c_void_p, _c_void_p,      # x x_stride w bias
         _c_void_p, _i64,                            # y y_stride

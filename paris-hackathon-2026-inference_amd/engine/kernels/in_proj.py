@@ -129,3 +129,29 @@ def gdn_out_proj_decode(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
                                  _lib.ptr(y), n, _lib.ptr(ws), ws.numel(), _lib.stream_of(x2))
     _lib.check(st, "gdn_out_proj_decode")
     return y.view(m, 1, n) if x.dim() == 3 else y
+
+
+def gdn_out_proj_decode_noalloc(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """:func:`gdn_out_proj_decode` into a caller's ``out`` ``[M, N]`` bf16
+    (row stride a multiple of 4, 8-byte aligned), with the partial sums in the
+    library's built-in per-GPU scratch: the call allocates nothing, so it can
+    run where allocation is not allowed (under graph capture, in a serving
+    loop).  x ``[M, K]`` bf16 with unit column stride, row stride a multiple
+    of 8 and 16-byte alignment, weight ``[N, K]`` contiguous bf16.  At most
+    GDN_OUT_PROJ_NOALLOC_MAX_BYTES of partial sums (64 rows at K = 4096,
+    N = 2048 need 4 MiB); calls that overlap on one GPU race.  Same bits as
+    :func:`gdn_out_proj_decode`."""
+    _lib.require_gpu(x, weight, out)
+    if x.dim() != 2 or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or out.dtype != torch.bfloat16:
+        raise ValueError("x [M, K], weight [N, K] and out [M, N] must be bf16 2-d tensors")
+    m, k = x.shape
+    n = weight.shape[0]
+    if weight.shape != (n, k) or not weight.is_contiguous() or out.shape != (m, n):
+        raise ValueError(f"shapes x{tuple(x.shape)} weight{tuple(weight.shape)} out{tuple(out.shape)}")
+    if x.stride(1) != 1 or out.stride(1) != 1:
+        raise ValueError("x and out need unit column stride (no copy is made)")
+    st = _lib.load().gdn_out_proj_decode_noalloc(
+        _lib.ptr(x), x.stride(0) if m > 1 else k, _lib.ptr(weight), m, k, n, _lib.ptr(out),
+        out.stride(0) if m > 1 else n, _lib.stream_of(x))
+    _lib.check(st, "gdn_out_proj_decode_noalloc")
+    return out

@@ -31,7 +31,7 @@ def test_header_lists_the_entry_points():
         "causal_conv1d_fwd", "causal_conv1d_update", "gdn_abi_version", "gdn_chunk_fwd",
         "gdn_chunk_fwd_gated", "gdn_chunk_workspace_bytes", "gdn_last_error_string", "gdn_recurrent_fwd",
         "gdn_recurrent_fwd_gated", "gdn_rmsnorm_gated_fwd", "gdn_state_commit", "gdn_conv_state_commit", "gdn_in_proj_decode",
-        "gdn_out_proj_decode", "gdn_out_proj_workspace_bytes"])
+        "gdn_out_proj_decode", "gdn_out_proj_workspace_bytes", "gdn_out_proj_decode_noalloc"])
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -42,7 +42,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.gdn_abi_version() == _lib.ABI_VERSION == 7
+    assert lib.gdn_abi_version() == _lib.ABI_VERSION == 8
 
 
 def _rec_call(lib, **over):
@@ -245,3 +245,11 @@ def test_out_proj_python_gate():
     assert fused_out_proj_supported(4096, 2048) and fused_out_proj_supported(2048, 1024)
     assert not fused_out_proj_supported(4000, 2048) and not fused_out_proj_supported(4096, 2000)
     assert not fused_out_proj_supported(16384, 2048)
+
+
+def test_out_proj_noalloc_rejects_sizes_beyond_its_scratch(lib):
+    """Host-side check, no launch: 256 rows at K = 4096, N = 2048 need 16 MiB
+    of partial sums, past the 8 MiB built-in scratch."""
+    st = lib.gdn_out_proj_decode_noalloc(16, 4096, 16, 256, 4096, 2048, 16, 2048, None)
+    assert st == 2  # GDN_ERR_UNSUPPORTED
+    assert b"scratch" in lib.gdn_last_error_string()
