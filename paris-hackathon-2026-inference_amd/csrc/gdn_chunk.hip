@@ -1484,6 +1484,22 @@ __device__ __forceinline__ bf16x8 frag_tr_v(const uint16_t *tile, int s, int lan
   return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+// "c8" order of the k dimension in the fused scan: lane group g of an MFMA
+// operand over k-step s holds k indices 32 s + 8 g + 0..7 (contiguous, so
+// that a q row fragment is one 16-byte load).  A state tile t of a 32-row
+// block at c0 holds rows c0 + 8 (m / 4) + 4 t + m % 4 (m its D row), and two
+// tiles t = 0, 1 pack into one c8 operand.  The fragment of X^T whose 16 rows
+// are those columns of X (k-step s over the rows of X), read transposed:
+__device__ __forceinline__ bf16x8 frag_tr_c8(const uint16_t *tile, int s, int c0, int lane) {
+  const int L = lane & 15, g4 = lane >> 4;
+  auto rd = [&](int j0) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4 *)(const_cast<uint16_t *>(tile) + nsw(j0 + (L >> 2), c0 + 8 * (L & 3))));
+  };
+  const s16x4 lo = rd(32 * s + 4 * g4), hi = rd(32 * s + 16 + 4 * g4);
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 // Per-workgroup constants of the fused scan.
 struct F2Ctx {
   int n, h, hk, ct, nch, c0, ratio;
@@ -1507,12 +1523,12 @@ __device__ __forceinline__ void f2_chain(const ChunkArgs &a, const F2Ctx &x, con
                                          const float *src, float *dst) {
   const int g4 = lane >> 4, row0 = 32 * p, col = 16 * x.ct + (lane & 15);
   (void)col;
-  f32x4 S[2];  // state rows row0 + 16t + 4g + e of this lane's column
+  f32x4 S[2];  // state rows row0 + 8g + 4t + e of this lane's column (c8 order)
   if (src) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) S[t][e] = src[(row0 + 16 * t + 4 * g4 + e) * DV];
+      for (int e = 0; e < 4; ++e) S[t][e] = src[(row0 + 8 * g4 + 4 * t + e) * DV];
   } else {
 #pragma unroll
     for (int t = 0; t < 2; ++t) S[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1532,11 +1548,11 @@ __device__ __forceinline__ void f2_chain(const ChunkArgs &a, const F2Ctx &x, con
     f32x4 vp = __builtin_bit_cast(f32x4, hd[(HD_U + p) * 64 + lane]);
 #pragma unroll
     for (int s = 0; s < 4; ++s) vp = mfma(as_bf16x8(hd[(HD_W + 4 * p + s) * 64 + lane]), sb[s], vp);
-    bf16x8 kt[4];  // K^T rows row0 + 16t, k-step s: [2t + s]
+    bf16x8 kt[4];  // K^T of state tile t (c8 rows of block row0), k-step s: [2t + s]
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int s = 0; s < 2; ++s) kt[2 * t + s] = frag_tr(kn, s, row0 + 16 * t, lane);
+      for (int s = 0; s < 2; ++s) kt[2 * t + s] = frag_tr_c8(kn, s, row0 + 4 * t, lane);
     const f32x4 sk = *reinterpret_cast<const f32x4 *>(scf + S2_SK * CK + 16 * p + 4 * g4);
     const f32x4 nk = *reinterpret_cast<const f32x4 *>(scf + S2_NK * CK + 16 * p + 4 * g4);
     const float eL = scf[S2_EL * CK];
@@ -1578,12 +1594,12 @@ __device__ __forceinline__ void f2_chain(const ChunkArgs &a, const F2Ctx &x, con
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) dst[(row0 + 16 * t + 4 * g4 + e) * DV] = S[t][e];
+      for (int e = 0; e < 4; ++e) dst[(row0 + 8 * g4 + 4 * t + e) * DV] = S[t][e];
   }
 }
 
 struct F2Q {        // one chunk's operands of a side wave's output rows
-  bf16x8 qm[4];     // q rows 16p.., k-steps 0..3 (B operand of Q S)
+  bf16x8 qm[4];     // q rows 16p.., k-steps 0..3 in c8 order (B operand of Q S)
   u32x4 am[2];      // A' rows 16p.., k-steps 0, 1
 };
 struct F2T {        // one chunk's T_u fragments of a side wave's U row blocks
@@ -1594,7 +1610,11 @@ struct F2T {        // one chunk's T_u fragments of a side wave's U row blocks
 template <int W> __device__ __forceinline__ constexpr int tu_pb(int i) { return W == 0 ? 3 : W == 1 ? 2 : (i < 2 ? 1 : 0); }
 template <int W> __device__ __forceinline__ constexpr int tu_s(int i) { return W < 2 ? (i >> 1) : 0; }
 
-template <int W, bool BF16_OUT>
+// Side wave of role ROW (W = its output row block: Q S, the output, q and A'
+// loads) or COL (W = its k-step of -W, its U row blocks, its share of the
+// stage copies and the T_u loads).
+enum { F2_ROW = 0, F2_COL = 1 };
+template <int W, int ROLE, bool BF16_OUT>
 __device__ __forceinline__ void f2_side(const ChunkArgs &a, const F2Ctx &x, const F2Lds &L, int lane) {
   constexpr int P = W;  // output row block
   constexpr int NA = ksteps(P);
@@ -1604,7 +1624,7 @@ __device__ __forceinline__ void f2_side(const ChunkArgs &a, const F2Ctx &x, cons
   int koff[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) koff[m] = rl * ks2 + 16 * (ps ^ ((4 * m + rl) & 15));
-  const int qoff = static_cast<int>((16 * P + r16) * a.qs * 2) + 8 * g4;
+  const int qoff = static_cast<int>((16 * P + r16) * a.qs * 2) + 16 * g4;
 
   // this wave's share of chunk c's stage, loaded into registers, later written to LDS
   auto load_stage = [&](u32x4 (&sg)[ST_SHARE], int c) {
@@ -1630,13 +1650,12 @@ __device__ __forceinline__ void f2_side(const ChunkArgs &a, const F2Ctx &x, cons
 #pragma unroll
     for (int d = st_lo(W); d < st_lo(W + 1); ++d) st[d * 64 + lane] = sg[d - st_lo(W)];
   };
-  auto load_qa = [&](F2Q &qa, int c) {
+  auto load_q = [&](F2Q &qa, int c) {
     const auto rq = brsrc_of(a.q + x.t0(c) * a.qs + (int64_t)x.hk * DK, (x.len(c) - 1) * a.qs * 2 + DK * 2);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const u32x2 x0 = vload8(rq, qoff + 64 * s), x1 = vload8(rq, qoff + 64 * s + 32);
-      qa.qm[s] = as_bf16x8(u32x4{x0.x, x0.y, x1.x, x1.y});
-    }
+    for (int s = 0; s < 4; ++s) qa.qm[s] = as_bf16x8(vload16(rq, qoff + 64 * s, 0));
+  };
+  auto load_am = [&](F2Q &qa, int c) {
     const auto rr = brsrc_of(x.rec(a, c), RB_N * 1024);
 #pragma unroll
     for (int s = 0; s < NA; ++s) qa.am[s] = vload16(rr, lane * 16, (RB_A + tfrag(P, s)) * 1024);
@@ -1647,18 +1666,19 @@ __device__ __forceinline__ void f2_side(const ChunkArgs &a, const F2Ctx &x, cons
     for (int i = 0; i < tu_count(W); ++i)
       tu.tu[i] = vload16(rr, lane * 16, ((i & 1 ? RB_TUL : RB_TUH) + tfrag(tu_pb<W>(i), tu_s<W>(i))) * 1024);
   };
-  // -W fragments of chunk c for k-step W of every row block, from the stage
-  auto w_units = [&](int c) {
+  // -W fragments of chunk c for k-step W of row blocks [pb0, pb1), from the stage
+  auto w_units = [&](int c, int pb0, int pb1) {
     const u32x4 *st = L.stage[c % F2_NST];
     u32x4 *hd = L.hand[c & 1];
     const uint16_t *kn = reinterpret_cast<const uint16_t *>(st + ST_K * 64);
-    bf16x8 kf[2][2];  // K^T of dk tiles 2W, 2W + 1, k-steps 0, 1
+    bf16x8 kf[2][2];  // K^T of the c8 state tiles t of k-step W, k-steps (positions) 0, 1
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int s = 0; s < 2; ++s) kf[t][s] = frag_tr(kn, s, 16 * (2 * W + t), lane);
+      for (int s = 0; s < 2; ++s) kf[t][s] = frag_tr_c8(kn, s, 32 * W + 4 * t, lane);
 #pragma unroll
     for (int pb = 0; pb < 4; ++pb) {
+      if (pb < pb0 || pb >= pb1) continue;
       f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < ksteps(pb); ++s) {
@@ -1714,46 +1734,63 @@ __device__ __forceinline__ void f2_side(const ChunkArgs &a, const F2Ctx &x, cons
   const int last = x.nch - 1;
   // ---- prologue: stages 0, 1, T_u of chunks 0, 1, q / A' of chunk 0; then
   // the hand-over of chunk 0 and the loads of "period -1"
-  load_stage(sg, 0);
-  write_stage(sg, 0);
-  load_stage(sg, min(1, last));
-  write_stage(sg, 1);
-  load_tu(tu0, 0);
-  load_tu(tu1, min(1, last));
-  load_qa(qa0, 0);
+  if constexpr (ROLE == F2_COL) {
+    load_stage(sg, 0);
+    write_stage(sg, 0);
+    load_stage(sg, min(1, last));
+    write_stage(sg, 1);
+    load_tu(tu0, 0);
+    load_tu(tu1, min(1, last));
+    load_stage(sg, min(2, last));
+  } else {
+    load_q(qa0, 0);
+    load_am(qa0, 0);
+    load_q(qa1, min(1, last));
+  }
   lds_barrier();  // prologue 1: chunks 0, 1 staged; initial state in LDS
-  w_units(0);
-  u_units(tu0, 0);
-  load_stage(sg, min(2, last));
-  load_qa(qa1, min(1, last));
-  load_tu(tu0, min(2, last));
+  if constexpr (ROLE == F2_COL) {
+    w_units(0, 0, 4);
+    u_units(tu0, 0);
+    load_tu(tu0, min(2, last));
+  } else {
+    load_am(qa1, min(1, last));
+  }
   lds_barrier();  // prologue 2: the hand-over of chunk 0
 
   auto period = [&](int c, F2Q &qa, F2T &tu) {
     // qa: q / A' of chunk c; tu: T_u of chunk c + 1; sg: stage share of c + 2
-    const float *scf = reinterpret_cast<const float *>(L.stage[c % F2_NST] + ST_SC * 64);
-    bf16x8 sb[4];
+    if constexpr (ROLE == F2_COL) {
+      // stage c + 2 goes to the buffer chunk c - 1 used (its last readers passed B2 of chunk c - 1)
+      write_stage(sg, c + 2);
+      load_stage(sg, min(c + 3, last));
+      if (c + 1 < x.nch) w_units(c + 1, 2, 4);
+      lds_barrier();  // B1
+      if (c + 1 < x.nch) {
+        w_units(c + 1, 0, 2);
+        u_units(tu, c + 1);
+      }
+      load_tu(tu, min(c + 3, last));
+      lds_barrier();  // B2
+    } else {
+      const float *scf = reinterpret_cast<const float *>(L.stage[c % F2_NST] + ST_SC * 64);
+      bf16x8 sb[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) sb[s] = __builtin_bit_cast(bf16x8, L.xs[s][lane]);
-    const float sq = scf[S2_SQ * CK + 16 * P + r16];
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < 4; ++s) sb[s] = __builtin_bit_cast(bf16x8, L.xs[s][lane]);
+      const float sq = scf[S2_SQ * CK + 16 * P + r16];
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < 4; ++s) acc = mfma(sb[s], qa.qm[s], acc);
-    if (c + 1 < x.nch) w_units(c + 1);
-    lds_barrier();  // B1
-    f32x4 o = acc * sq;
+      for (int s = 0; s < 4; ++s) acc = mfma(sb[s], qa.qm[s], acc);
+      load_q(qa, min(c + 2, last));
+      lds_barrier();  // B1
+      f32x4 o = acc * sq;
 #pragma unroll
-    for (int s = 0; s < NA; ++s)
-      o = mfma(__builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(&L.xv[0][s][lane][0])),
-               as_bf16x8(qa.am[s]), o);
-    store_out(o, c);
-    if (c + 1 < x.nch) u_units(tu, c + 1);
-    // stage c + 2 goes to the buffer chunk c - 1 used (its last readers passed B1 of chunk c)
-    write_stage(sg, c + 2);
-    load_stage(sg, min(c + 3, last));
-    load_qa(qa, min(c + 2, last));
-    load_tu(tu, min(c + 3, last));
-    lds_barrier();  // B2
+      for (int s = 0; s < NA; ++s)
+        o = mfma(__builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(&L.xv[0][s][lane][0])),
+                 as_bf16x8(qa.am[s]), o);
+      store_out(o, c);
+      load_am(qa, min(c + 2, last));
+      lds_barrier();  // B2
+    }
   };
   for (int c = 0; c < x.nch; c += 2) {
     period(c, qa0, tu1);
@@ -1763,7 +1800,7 @@ __device__ __forceinline__ void f2_side(const ChunkArgs &a, const F2Ctx &x, cons
 }
 
 template <bool BF16_OUT>
-__global__ __launch_bounds__(512) void chunk_fused_kernel(ChunkArgs a) {
+__global__ __launch_bounds__(768) void chunk_fused_kernel(ChunkArgs a) {
   __shared__ u32x4 stage[F2_NST][ST_N * 64];  // 75 KiB
   __shared__ u32x4 hand[2][HD_N * 64];        // 40 KiB
   __shared__ u32x4 xs[4][64];
@@ -1825,14 +1862,20 @@ __global__ __launch_bounds__(512) void chunk_fused_kernel(ChunkArgs a) {
     const float *src = lo == cs ? (in_row >= 0 ? a.h0 + (in_row * a.Hv + x.h) * kv + col : nullptr) : carry;
     float *dst = hi == ce ? (out_row >= 0 ? a.hT + (out_row * a.Hv + x.h) * kv + col : nullptr) : carry;
     f2_chain<BF16_OUT>(a, x, L, wave, lane, src, dst);
-  } else if (wave == 4) {
-    f2_side<0, BF16_OUT>(a, x, L, lane);
-  } else if (wave == 5) {
-    f2_side<1, BF16_OUT>(a, x, L, lane);
-  } else if (wave == 6) {
-    f2_side<2, BF16_OUT>(a, x, L, lane);
+  } else if (wave < 8) {
+    switch (wave) {
+      case 4: f2_side<0, F2_ROW, BF16_OUT>(a, x, L, lane); break;
+      case 5: f2_side<1, F2_ROW, BF16_OUT>(a, x, L, lane); break;
+      case 6: f2_side<2, F2_ROW, BF16_OUT>(a, x, L, lane); break;
+      default: f2_side<3, F2_ROW, BF16_OUT>(a, x, L, lane); break;
+    }
   } else {
-    f2_side<3, BF16_OUT>(a, x, L, lane);
+    switch (wave) {
+      case 8: f2_side<0, F2_COL, BF16_OUT>(a, x, L, lane); break;
+      case 9: f2_side<1, F2_COL, BF16_OUT>(a, x, L, lane); break;
+      case 10: f2_side<2, F2_COL, BF16_OUT>(a, x, L, lane); break;
+      default: f2_side<3, F2_COL, BF16_OUT>(a, x, L, lane); break;
+    }
   }
 }
 
@@ -1994,11 +2037,11 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
   auto launch_scan = [&](hipStream_t st) {
     if (fused) {
       if (o_dtype == GDN_DTYPE_BF16)
-        hipLaunchKernelGGL((chunk_fused_kernel<true>), dim3(static_cast<unsigned>(scan_blocks)), dim3(512),
+        hipLaunchKernelGGL((chunk_fused_kernel<true>), dim3(static_cast<unsigned>(scan_blocks)), dim3(768),
                            0, st, a);
       else
         hipLaunchKernelGGL((chunk_fused_kernel<false>), dim3(static_cast<unsigned>(scan_blocks)),
-                           dim3(512), 0, st, a);
+                           dim3(768), 0, st, a);
       return;
     }
     if (persist) {
