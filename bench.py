@@ -80,20 +80,50 @@ def parse():
     ap.add_argument("--prefill-only", action="store_true",
                     help="time only the configuration 2 prefill (for counter profiles; prints no headline value)")
     ap.add_argument("--copy-probe", action="store_true",
-                    help="only run a plain 128 MiB device copy (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+                    help="only run the HBM ceiling probes: a plain 128 MiB device copy (also the "
+                         "rocprofv3 FETCH_SIZE/WRITE_SIZE calibration), the same bytes in place, and a "
+                         "1 GiB read-only stream")
     return ap.parse_args()
 
 
 def copy_probe(torch, reps=20):
-    """A plain device-to-device copy of 128 MiB, repeated: the HBM traffic counters of
-    this kernel calibrate the decode kernel's (known bytes: 128 MiB read + 128 MiB written)."""
+    """The box's HBM streaming ceilings for the decode kernel's traffic.
+
+    * copy: a plain device-to-device copy of 128 MiB each way (torch ``copy_``, run by ROCm
+      as ``__amd_rocclr_copyBuffer``), the 268 MB one B=64 decode step moves; its traffic
+      counters also calibrate the decode kernel's FETCH_SIZE / WRITE_SIZE;
+    * in place: the same 128 MiB read and written back in place (torch ``mul_``), the
+      decode kernel's own pattern (it updates the slot pool in place);
+    * read-only: a row-wise sum over 1 GiB of fp32 (rows of 4,096).
+    Each rotates over 4 buffers, so that no call reads what the previous one left in the
+    Infinity Cache; times are per call, from events around all calls (the rocprofv3 kernel
+    trace of the same run gives the kernels alone)."""
     n = (128 << 20) // 4
     src = [torch.randn(n, device="cuda") for _ in range(4)]
     dst = [torch.empty(n, device="cuda") for _ in range(4)]
-    for i in range(reps):
-        dst[i % 4].copy_(src[(i + 1) % 4])
-    torch.cuda.synchronize()
-    print(json.dumps({"copy_probe_bytes_each_way": 128 << 20, "reps": reps}), flush=True)
+    big = [torch.randn((1 << 30) // 4, device="cuda") for _ in range(2)]
+    rows = torch.empty((1 << 30) // 4 // 4096, device="cuda")
+
+    def timed(fn, count):
+        fn(0)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(count):
+            fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / count
+
+    t_copy = timed(lambda i: dst[i % 4].copy_(src[(i + 1) % 4]), reps)
+    t_inpl = timed(lambda i: src[i % 4].mul_(1.0000001), reps)
+    t_read = timed(lambda i: torch.sum(big[i % 2].view(-1, 4096), dim=1, out=rows), max(4, reps // 2))
+    mb = 2 * (128 << 20)
+    print(json.dumps({"copy_probe_bytes_each_way": 128 << 20, "reps": reps,
+                      "copy_us": t_copy * 1e6, "copy_tb_per_s": mb / t_copy / 1e12,
+                      "inplace_us": t_inpl * 1e6, "inplace_tb_per_s": mb / t_inpl / 1e12,
+                      "read_stream_bytes": 1 << 30, "read_us": t_read * 1e6,
+                      "read_tb_per_s": (1 << 30) / t_read / 1e12}), flush=True)
 
 
 def bench_decode(torch, steps, warmup, n_pools):

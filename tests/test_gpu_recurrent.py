@@ -225,3 +225,47 @@ def test_bf16_beta_and_no_l2norm():
                                                   use_qk_l2norm_in_kernel=False, scale=0.3)
     assert np.abs(np64(o) - o_ref).max() < O_TOL_BF16
     assert gdn.state_rel_err(np64(s), s_ref) < S_TOL
+
+
+@pytest.mark.parametrize("dtype,gated", [(torch.bfloat16, False), (torch.float32, False), (torch.bfloat16, True)])
+def test_decode_b37_on_a_slot_pool_with_bad_and_repeated_ids(dtype, gated):
+    """Single-token decode at B = 37 (4,736 column slices, not a whole number
+    of rounds of the grid) on a 48-slot pool whose ids hold a negative, an
+    out-of-range and a repeated id (each selects no row: zero state in,
+    nothing written).  q / k / v in bf16 or fp32; gates given as g / beta or as
+    the raw a / b projections (A_log, dt_bias)."""
+    from engine.kernels import fused_recurrent_gated_delta_rule_from_projections
+    gen = torch.Generator().manual_seed(61)
+    bsz, n_slots = 37, 48
+    q = torch.randn(bsz, 1, 16, 128, generator=gen).to(dtype)
+    k = torch.randn(bsz, 1, 16, 128, generator=gen).to(dtype)
+    v = torch.randn(bsz, 1, 32, 128, generator=gen).to(dtype)
+    pool = torch.randn(n_slots, 32, 128, 128, generator=gen) * 0.1
+    ids = torch.randperm(n_slots, generator=gen)[:bsz]
+    ids[5], ids[9], ids[20] = -1, n_slots, ids[3]
+    live = [i for i in range(bsz) if 0 <= int(ids[i]) < n_slots and int(ids[i]) not in ids[:i].tolist()]
+    h0 = np.zeros((bsz, 32, 128, 128))
+    h0[live] = pool[ids[live]].numpy()
+    pool_gpu = pool.to(DEV)
+    if gated:
+        a = torch.randn(bsz, 1, 32, generator=gen).to(torch.bfloat16)
+        b = torch.randn(bsz, 1, 32, generator=gen).to(torch.bfloat16)
+        A_log = torch.log(torch.empty(32).uniform_(0.5, 16.0, generator=gen))
+        dt_bias = torch.randn(32, generator=gen)
+        o, _ = fused_recurrent_gated_delta_rule_from_projections(
+            *cuda(q, k, v, a, b, A_log, dt_bias), initial_state=pool_gpu, ssm_state_indices=ids.to(DEV),
+            inplace_final_state=True)
+        g, beta = gdn.gdn_gates(np64(a), np64(b), np64(A_log), np64(dt_bias))
+    else:
+        g = -torch.rand(bsz, 1, 32, generator=gen) * 2
+        beta = torch.rand(bsz, 1, 32, generator=gen)
+        o, _ = fused_recurrent_gated_delta_rule(*cuda(q, k, v, g, beta), initial_state=pool_gpu,
+                                                ssm_state_indices=ids.to(DEV), inplace_final_state=True,
+                                                use_qk_l2norm_in_kernel=True)
+        g, beta = np64(g), np64(beta)
+    o_ref, s_ref = gdn.recurrent_gated_delta_rule(np64(q), np64(k), np64(v), g, beta, initial_state=h0)
+    tol = O_TOL_BF16 if o.dtype == torch.bfloat16 else 1e-4
+    assert np.abs(np64(o) - o_ref).max() < tol
+    assert gdn.state_rel_err(np64(pool_gpu[ids[live].to(DEV)]), s_ref[live]) < (S_TOL if dtype != torch.float32 else 1e-5)
+    untouched = np.setdiff1d(np.arange(n_slots), ids[live].numpy())
+    assert torch.equal(pool_gpu[untouched].cpu(), pool[untouched])
