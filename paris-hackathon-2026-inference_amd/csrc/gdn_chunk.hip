@@ -1472,6 +1472,27 @@ __device__ __forceinline__ u32x4 vload16(__amdgpu_buffer_rsrc_t rsrc, int voff, 
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, soff, 0));
 }
 
+// L2 warm-up: 4 bytes per lane from global memory into an LDS pad that
+// nothing reads (buffer_load_dword ... lds).  Inline asm, so the compiler
+// neither waits for it nor counts it; it writes no register, so nothing the
+// compiler tracks can be overwritten when its data returns.  Only the chain
+// waves issue it (they wait for no global load inside the loop) and they
+// drain it with s_waitcnt vmcnt(0) before they finish.
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4_t touch_rsrc(const void *base, int64_t bytes) {
+  const uint64_t pp = reinterpret_cast<uint64_t>(base);
+  const int n = bytes <= 0 ? 0 : bytes >= 0x7fffffff ? 0x7fffffff : static_cast<int>(bytes);
+  return i32x4_t{__builtin_amdgcn_readfirstlane(static_cast<int>(pp & 0xffffffffu)),
+                 __builtin_amdgcn_readfirstlane(static_cast<int>((pp >> 32) & 0xffff)),
+                 __builtin_amdgcn_readfirstlane(n), BUF_DWORD3};
+}
+__device__ __forceinline__ void touch4(const i32x4_t &rsrc, const void *pad, int voff) {
+  asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc),
+               "{m0}"(static_cast<uint32_t>(
+                   reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char *)pad))));
+}
+constexpr int F2_AHEAD = 4;  // chunks between a warm-up read and the first load of the same data
+
 // V slice [64 rows][16 columns] bf16, rows of 32 bytes: pi fragment of V over
 // the positions of k-step s (as the B operand: B[k][n] = V[pos k][col n]).
 __device__ __forceinline__ bf16x8 frag_tr_v(const uint16_t *tile, int s, int lane) {
@@ -1516,7 +1537,33 @@ struct F2Lds {
   u32x4 (*hand)[HD_N * 64];
   u32x4 (*xs)[64];            // state rows by k-step (bf16), lane order
   u32x2 (*xv)[2][64][2];      // nk V', V'' hi, V'' lo by k-step, lane, half
+  uint32_t (*pad)[64];        // landing pad of the warm-up reads, per chain wave
 };
+
+// Chain wave p's warm-up of chunk c: p = 0 this workgroup's eighth of the
+// chunk's solve record, p = 1 / 2 its share of the chunk's k / q lines (read
+// by the 8 Hv / Hk workgroups of one k-head), p = 3 the v lines it is the
+// first of four column tiles to read.  Lines past the sequence end read as
+// zero (range-checked offsets).
+__device__ __forceinline__ void f2_touch(const ChunkArgs &a, const F2Ctx &x, const F2Lds &L, int p, int lane, int c) {
+  const int len = x.len(c);
+  if (p == 0) {
+    if (lane < RB_N) touch4(touch_rsrc(x.rec(a, c), RB_N * 1024), L.pad[0], (RB_N * x.ct + lane) * 128);
+  } else if (p <= 2) {
+    const int per = max(1, 128 / (8 * x.ratio));  // 128-byte lines of the chunk's rows per workgroup
+    const int m = (x.h % x.ratio) * 8 + x.ct;
+    const int64_t stride = p == 1 ? a.ks : a.qs;
+    const uint16_t *base = (p == 1 ? a.k : a.q) + x.t0(c) * stride + (int64_t)x.hk * DK;
+    const int li = (m * per + lane) & 127;  // row li / 2, half li % 2
+    if (lane < per)
+      touch4(touch_rsrc(base, (len - 1) * stride * 2 + DK * 2), L.pad[p],
+             static_cast<int>((li >> 1) * stride * 2) + 128 * (li & 1));
+  } else if (lane < 16) {
+    const uint16_t *base = a.v + x.t0(c) * a.vs + (int64_t)x.h * DV + 16 * x.ct;
+    touch4(touch_rsrc(base, (len - 1) * a.vs * 2 + 32), L.pad[3],
+           static_cast<int>((4 * lane + (x.ct & 3)) * a.vs * 2));
+  }
+}
 
 template <bool BF16_OUT>
 __device__ __forceinline__ void f2_chain(const ChunkArgs &a, const F2Ctx &x, const F2Lds &L, int p, int lane,
@@ -1534,6 +1581,7 @@ __device__ __forceinline__ void f2_chain(const ChunkArgs &a, const F2Ctx &x, con
     for (int t = 0; t < 2; ++t) S[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   L.xs[p][lane] = __builtin_bit_cast(u32x4, pack_hi(S[0], S[1]));
+  for (int c = 2; c < 2 + F2_AHEAD && c < x.nch; ++c) f2_touch(a, x, L, p, lane, c);
   lds_barrier();  // prologue 1: initial state in LDS
   lds_barrier();  // prologue 2: the hand-over of chunk 0
   for (int c = 0; c < x.nch; ++c) {
@@ -1572,6 +1620,7 @@ __device__ __forceinline__ void f2_chain(const ChunkArgs &a, const F2Ctx &x, con
     }
 #pragma unroll
     for (int t = 0; t < 2; ++t) S[t] = S[t] * eL;
+    if (c + 2 + F2_AHEAD < x.nch) f2_touch(a, x, L, p, lane, c + 2 + F2_AHEAD);
     lds_barrier();  // B1
     // ---- R2: S += K^T V''
     bf16x8 vh[2], vl[2];
@@ -1596,6 +1645,7 @@ __device__ __forceinline__ void f2_chain(const ChunkArgs &a, const F2Ctx &x, con
 #pragma unroll
       for (int e = 0; e < 4; ++e) dst[(row0 + 8 * g4 + 4 * t + e) * DV] = S[t][e];
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the warm-up reads
 }
 
 struct F2Q {        // one chunk's operands of a side wave's output rows
@@ -1805,6 +1855,7 @@ __global__ __launch_bounds__(768) void chunk_fused_kernel(ChunkArgs a) {
   __shared__ u32x4 hand[2][HD_N * 64];        // 40 KiB
   __shared__ u32x4 xs[4][64];
   __shared__ u32x2 xv[3][2][64][2];
+  __shared__ uint32_t pad[4][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   F2Ctx x;
@@ -1855,7 +1906,7 @@ __global__ __launch_bounds__(768) void chunk_fused_kernel(ChunkArgs a) {
   const int64_t seq_off = static_cast<int64_t>(lo - cs) * CK;
   x.tok0 = s0 + seq_off;
   x.rem = slen - seq_off;
-  const F2Lds L{stage, hand, xs, xv};
+  const F2Lds L{stage, hand, xs, xv, pad};
 
   if (wave < 4) {
     float *carry = a.carry + (static_cast<int64_t>(x.n) * a.Hv + x.h) * kv + col;
