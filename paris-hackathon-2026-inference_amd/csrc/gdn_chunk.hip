@@ -62,17 +62,14 @@ constexpr int DK = 128;    // k head dim
 constexpr int DV = 128;    // v head dim
 constexpr int SCAL = 256;  // per (chunk, v-head) scalars: sq[64], sk[64], eL (1 KiB block)
 
-// Operand blocks (64 lanes x 16 bytes) per chunk, in two contiguous regions
-// so that one chunk's scan operands are two straight copies:
-//   per (chunk, v-head): -W [p 0..3][s 0..3], A [p 0..3][s 0..1] (6 used), scalars
-//   per (chunk, k-head): Q [p 0..3][s 0..3], K^T [i 0..7][s 0..1]
+// Operand blocks (64 lanes x 16 bytes) per (chunk, v-head), one contiguous
+// region so that a chunk's prep operands are one straight copy:
+// -W [p 0..3][s 0..3], A [p 0..3][s 0..1] (6 used), scalars.  (The scan reads
+// q and k rows from the inputs themselves.)
 constexpr int NB_W = 16;
 constexpr int NB_A = 8;
 constexpr int NB_SC = SCAL / 64;  // scalars as blocks (1)
-constexpr int NB_Q = 16;
-constexpr int NB_KT = 16;
 constexpr int VH_W = 0, VH_A = VH_W + NB_W, VH_SC = VH_A + NB_A, NB_VH = VH_SC + NB_SC;
-constexpr int KH_Q = 0, KH_KT = KH_Q + NB_Q, NB_KH = KH_KT + NB_KT;
 
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -129,7 +126,6 @@ struct ChunkArgs {
   // workspace
   int32_t *chunk_start;  // [n_seqs + 2]: chunk starts, then the empty-sequence count
   u32x4 *vh;             // [SEG][Hv][NB_VH][64]   -W, A, scalars
-  u32x4 *kh;             // [SEG][Hk][NB_KH][64]   Q, K^T
   float *Ut;             // [SEG][Hv][8 x 4 blocks][64][4]  U, fp32
   float *carry;          // [n_seqs][Hv][128][128] state between segments
   int64_t *seqrec;       // [n_seqs][SEQREC]: per-sequence record for the persistent scan
@@ -311,7 +307,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   const int len = min(CK, slen - c * CK);
   if (len <= 0) return;
   const int hk = h / ratio;
-  const bool khead_writer = (h % ratio) == 0;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -319,7 +314,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   const int g4 = lane >> 4;
   const int r16 = lane & 15;
   const size_t ch = static_cast<size_t>(jl) * a.Hv + h;
-  const size_t chk = static_cast<size_t>(jl) * a.Hk + hk;
   const int irow = 16 * p + r16;  // this lane's chunk row in row-layout / pi fragments
 
   // ---- global loads: K, V rows (16 bytes per thread), this wave's Q rows as
@@ -388,12 +382,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
     }
     gam_s[lane] = gv;
     beta_s[lane] = bv;
-  }
-  // the scan's Q operand blocks are this wave's pi fragments
-  if (khead_writer) {
-    u32x4 *qop = a.kh + chk * (NB_KH * 64) + KH_Q * 64;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) qop[(4 * p + s) * 64 + lane] = __builtin_bit_cast(u32x4, qf[s]);
   }
   __syncthreads();
 
@@ -526,8 +514,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
     ut[nb] = z4;
   }
   const int nsteps = p >= 2 ? 2 : 1;  // T is lower triangular
-  const bool kt_writer = khead_writer && p >= 2;
-  u32x4 *kop = a.kh + chk * (NB_KH * 64) + KH_KT * 64;
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     if (s < nsteps) {
@@ -546,9 +532,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
         wt[nb] = mfma(kt, wlo, wt[nb]);
         ut[nb] = mfma(uhi, vf, ut[nb]);
         ut[nb] = mfma(ulo, vf, ut[nb]);
-        // the scan's K^T operand blocks (i, s) are these fragments: waves 2
-        // and 3 (which read both k-steps) write tiles 0-3 and 4-7
-        if (kt_writer && (nb >> 2) == p - 2) kop[(2 * nb + s) * 64 + lane] = __builtin_bit_cast(u32x4, kt);
       }
     }
   }
@@ -869,9 +852,11 @@ constexpr int SG_MFMA = 0x8, SG_DS_RD = 0x100;
 // follows its last read, and read only after the barrier that follows the
 // wait for its copies.  The barriers fence LDS only (the loaders wait for
 // their copies with an explicit vmcnt).
-constexpr int RS_VH = 0, RS_KH = NB_VH, RS_U = NB_VH + NB_KH, RS_BLOCKS = RS_U + 4;  // 61 blocks of 1 KiB
-constexpr int RS_LOADER0 = NB_VH + 4;  // loader 0: v-head region + U blocks; loader 1: k-head region
-constexpr int RS_LOADER1 = NB_KH;
+// stage blocks per chunk: the v-head region, K and Q rows (raw, 4 rows per
+// block, swizzled as nsw), U
+constexpr int RS_VH = 0, RS_K = NB_VH, RS_Q = RS_K + 16, RS_U = RS_Q + 16, RS_BLOCKS = RS_U + 4;  // 61 blocks
+constexpr int RS_LOADER0 = NB_VH + 4;  // loader 0: v-head region + U blocks; loader 1: K and Q rows
+constexpr int RS_LOADER1 = 32;
 constexpr int SCAN_WAVES = 6;
 constexpr int SCAN_COLS = 16;  // state columns per workgroup
 constexpr int SCAN_PERSIST_BLOCKS = 256;  // one scan workgroup per CU (MI355X: 256 CUs)
@@ -884,18 +869,75 @@ struct RowOps {     // one chunk's operands of one compute wave
   f32x4 u, sk;      // U rows 16q + 4g + e of this lane's column; their V'' scales
   float sq, eL;     // output scale of position 16q + (lane % 16); e^{gamma_63}
 };
-struct RowSrc {     // one chunk's operand regions in the workspace (per v-head, per k-head, U)
-  __amdgpu_buffer_rsrc_t vh, kh, ut;
+// Token ranges of global chunks visited in increasing order (a scan
+// loader's walk): one search for the first chunk's sequence, then the next
+// sequence is entered when a chunk crosses the current one's end, with that
+// sequence's table entries read one crossing earlier.  Uniform; the chunk
+// table and cu_seqlens are read as scalar loads.
+struct ChunkWalk {
+  int n, cs, next_cs, slen;
+  int64_t s0;
+  int p_cs, p_slen;  // the next sequence's end chunk and length, read one crossing ahead
+  int64_t p_s0;
+  __device__ void prefetch(const ChunkArgs &a) {
+    const int m = min(n + 1, a.n_seqs - 1);
+    p_cs = chunk_start_at(a, m + 1);
+    seq_bounds(a, m, &p_s0, &p_slen);
+  }
+  __device__ void start(const ChunkArgs &a, int j) {
+    int lo = 0, hi = a.n_seqs;  // last n with chunk_start[n] <= j
+    if (!a.cu) {
+      lo = j / ((a.T + CK - 1) / CK);
+    } else {
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (a.chunk_start[mid] <= j) lo = mid; else hi = mid;
+      }
+    }
+    n = lo;
+    cs = chunk_start_at(a, lo);
+    next_cs = chunk_start_at(a, lo + 1);
+    seq_bounds(a, lo, &s0, &slen);
+    prefetch(a);
+  }
+  // chunk j's first token and length (j at or after the previous call's)
+  __device__ void at(const ChunkArgs &a, int j, int64_t *t0, int *len) {
+    while (j >= next_cs && n + 1 < a.n_seqs) {  // (empty sequences have no chunks: cs == next_cs)
+      ++n;
+      cs = next_cs;
+      next_cs = p_cs;
+      s0 = p_s0;
+      slen = p_slen;
+      prefetch(a);
+    }
+    const int c = j - cs;
+    *t0 = s0 + static_cast<int64_t>(c) * CK;
+    *len = min(CK, slen - c * CK);
+  }
 };
-__device__ __forceinline__ RowSrc row_src(const ChunkArgs &a, size_t ch, size_t chk) {
+struct RowSrc {     // one chunk's sources: its workspace regions (v-head operands, U) and raw k, q rows
+  __amdgpu_buffer_rsrc_t vh, ut, k, q;
+};
+// ch: the (chunk, v-head) index within the workspace; the chunk's tokens
+// [t0, t0 + len).  Rows past the chunk's end read as zero (their offsets are
+// range checked).
+__device__ __forceinline__ RowSrc row_src(const ChunkArgs &a, size_t ch, int64_t t0, int len, int hk) {
+  const int64_t kb = (len - 1) * a.ks * 2 + DK * 2, qb = (len - 1) * a.qs * 2 + DK * 2;
   return RowSrc{__builtin_amdgcn_make_buffer_rsrc(a.vh + ch * (NB_VH * 64), 0, NB_VH * 1024, BUF_DWORD3),
-                __builtin_amdgcn_make_buffer_rsrc(a.kh + chk * (NB_KH * 64), 0, NB_KH * 1024, BUF_DWORD3),
-                __builtin_amdgcn_make_buffer_rsrc(a.Ut + ch * (DV * CK), 0, DV * CK * 4, BUF_DWORD3)};
+                __builtin_amdgcn_make_buffer_rsrc(a.Ut + ch * (DV * CK), 0, DV * CK * 4, BUF_DWORD3),
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.k) + t0 * a.ks + (int64_t)hk * DK, 0,
+                                                  static_cast<int>(kb < 0 ? 0 : kb), BUF_DWORD3),
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.q) + t0 * a.qs + (int64_t)hk * DK, 0,
+                                                  static_cast<int>(qb < 0 ? 0 : qb), BUF_DWORD3)};
 }
 
-// Loader ld's copies [i0, i1) of one chunk into stage st (1 KiB each, lane l's 16 bytes at 16 l).
+// Loader ld's copies [i0, i1) of one chunk into stage st (1 KiB each, lane l's
+// 16 bytes at 16 l; a raw row block i holds rows 4i .. 4i + 3, LDS segment ps
+// of a row holding its logical segment ps ^ (row & 15), the nsw layout).
 template <int LD>
-__device__ __forceinline__ void stage_copy(u32x4 *st, const RowSrc &r, int ct, int i0, int i1, int lane) {
+__device__ __forceinline__ void stage_copy(u32x4 *st, const RowSrc &r, const ChunkArgs &a, int ct, int i0, int i1,
+                                           int lane) {
+  const int rl = lane >> 4, ps = lane & 15;
   for (int i = i0; i < i1; ++i) {
     if constexpr (LD == 0) {
       if (i < NB_VH)
@@ -904,7 +946,14 @@ __device__ __forceinline__ void stage_copy(u32x4 *st, const RowSrc &r, int ct, i
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r.ut, st + (RS_U + i - NB_VH) * 64, 16, lane * 16,
                                                  (4 * ct + i - NB_VH) * 1024, 0, 0);
     } else {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(r.kh, st + (RS_KH + i) * 64, 16, lane * 16, i * 1024, 0, 0);
+      const int b = i & 15, row = 4 * b + rl;
+      const int seg = 16 * (ps ^ (row & 15));  // (the whole offset is in the range-checked vector offset)
+      if (i < 16)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r.k, st + (RS_K + b) * 64, 16, row * static_cast<int>(a.ks * 2) + seg,
+                                                 0, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r.q, st + (RS_Q + b) * 64, 16, row * static_cast<int>(a.qs * 2) + seg,
+                                                 0, 0, 0);
     }
   }
 }
@@ -920,12 +969,16 @@ __device__ __forceinline__ void read_rows(RowOps &op, const u32x4 *st, int q, in
     op.u = __builtin_bit_cast(f32x4, st[(RS_U + q) * 64 + lane]);
     op.sk = *reinterpret_cast<const f32x4 *>(sc + CK + 16 * q + 4 * (lane >> 4));
     op.eL = sc[2 * CK];
-  } else if constexpr (G == 1) {  // Q S
+  } else if constexpr (G == 1) {  // Q S: pi fragments of q rows 16q..
+    const uint16_t *qn = reinterpret_cast<const uint16_t *>(st + RS_Q * 64);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) op.qm[s] = st[(RS_KH + KH_Q + 4 * q + s) * 64 + lane];
-  } else if constexpr (G == 2) {  // S += K^T V''
+    for (int s = 0; s < 4; ++s) op.qm[s] = __builtin_bit_cast(u32x4, frag_pi(qn, 16 * q, s, lane));
+  } else if constexpr (G == 2) {  // S += K^T V'': K^T tiles 2q + t, read transposed from the k rows
+    const uint16_t *kn = reinterpret_cast<const uint16_t *>(st + RS_K * 64);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) op.kt[j] = st[(RS_KH + KH_KT + 4 * q + j) * 64 + lane];
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) op.kt[2 * t + s] = __builtin_bit_cast(u32x4, frag_tr(kn, s, 32 * q + 16 * t, lane));
   } else {  // the output
     op.am[0] = st[(RS_VH + VH_A + 2 * q) * 64 + lane];
     op.am[1] = st[(RS_VH + VH_A + 2 * q + 1) * 64 + lane];  // (unused for q < 2)
@@ -1051,13 +1104,18 @@ __device__ __forceinline__ void scan_rows_loader(u32x4 (*stage)[RS_BLOCKS * 64],
                                                  const ChunkArgs &a, int c0, int h, int hk) {
   constexpr int N = LD == 0 ? RS_LOADER0 : RS_LOADER1;  // copies per chunk
   constexpr int H = N / 2;                               // of which before barrier 1
-  auto src_of = [&](int c) {
+  ChunkWalk walk;
+  walk.start(a, a.seg_begin + c0);
+  auto src_of = [&](int c) {  // (called with increasing c)
     const size_t j = static_cast<size_t>(c0 + c);
-    return row_src(a, j * a.Hv + h, j * a.Hk + hk);
+    int64_t t0;
+    int len;
+    walk.at(a, a.seg_begin + c0 + c, &t0, &len);
+    return row_src(a, j * a.Hv + h, t0, len, hk);
   };
-  stage_copy<LD>(stage[0], src_of(0), ct, 0, N, lane);
+  stage_copy<LD>(stage[0], src_of(0), a, ct, 0, N, lane);
   if (nch > 1) {
-    stage_copy<LD>(stage[1], src_of(1), ct, 0, N, lane);
+    stage_copy<LD>(stage[1], src_of(1), a, ct, 0, N, lane);
     __builtin_amdgcn_s_waitcnt(vmcnt_only(N));  // chunk 0 landed
   } else {
     __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
@@ -1067,10 +1125,10 @@ __device__ __forceinline__ void scan_rows_loader(u32x4 (*stage)[RS_BLOCKS * 64],
   for (int c = 0; c < nch; ++c) {
     if (c + 2 < nch) {
       const RowSrc r = src_of(c + 2);
-      stage_copy<LD>(stage[c & 1], r, ct, 0, H, lane);
+      stage_copy<LD>(stage[c & 1], r, a, ct, 0, H, lane);
       __builtin_amdgcn_s_waitcnt(vmcnt_only(H));  // chunk c + 1 landed
       __builtin_amdgcn_s_barrier();
-      stage_copy<LD>(stage[c & 1], r, ct, H, N, lane);
+      stage_copy<LD>(stage[c & 1], r, a, ct, H, N, lane);
     } else {
       __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
       __builtin_amdgcn_s_barrier();
@@ -1946,12 +2004,12 @@ constexpr int SEG_CHUNKS = 64;
 // there are several) and the scan operands of one segment.
 struct WsLayout {
   size_t chunk_start, seqrec, carry, total;
-  size_t vh, kh, Ut;
+  size_t vh, Ut;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-WsLayout ws_layout(int n_seqs, int64_t seg_chunks, int Hv, int Hk, bool multi) {
+WsLayout ws_layout(int n_seqs, int64_t seg_chunks, int Hv, bool multi) {
   WsLayout l;
   size_t off = 0;
   l.chunk_start = off;
@@ -1962,8 +2020,6 @@ WsLayout ws_layout(int n_seqs, int64_t seg_chunks, int Hv, int Hk, bool multi) {
   if (multi) off = align256(off + sizeof(float) * static_cast<size_t>(n_seqs) * Hv * DK * DV);
   l.vh = off;
   off = align256(off + 16ull * seg_chunks * Hv * NB_VH * 64);
-  l.kh = off;
-  off = align256(off + 16ull * seg_chunks * Hk * NB_KH * 64);
   l.Ut = off;
   off = align256(off + sizeof(float) * seg_chunks * Hv * DV * CK);
   l.total = off;
@@ -1987,7 +2043,7 @@ WsLayout ws_layout_fused(int n_seqs, int64_t seg_chunks, int Hv, bool multi) {
   if (multi) off = align256(off + sizeof(float) * static_cast<size_t>(n_seqs) * Hv * DK * DV);
   l.vh = off;
   off = align256(off + 1024ull * RB_N * seg_chunks * Hv);
-  l.kh = l.Ut = off;
+  l.Ut = off;
   l.total = off;
   return l;
 }
@@ -2015,7 +2071,7 @@ extern "C" size_t gdn_chunk_workspace_bytes(int32_t n_seqs, int64_t total_tokens
   // Upper bound valid with or without cu_seqlens and for either kernel path;
   // k-head blocks counted at Hk = Hv.
   const int64_t nc = (total_tokens + CK - 1) / CK + n_seqs;
-  const size_t old_path = ws_layout(n_seqs, std::min<int64_t>(nc, SEG_CHUNKS), Hv, Hv, nc > SEG_CHUNKS).total;
+  const size_t old_path = ws_layout(n_seqs, std::min<int64_t>(nc, SEG_CHUNKS), Hv, nc > SEG_CHUNKS).total;
   const size_t fused = ws_layout_fused(n_seqs, std::min<int64_t>(nc, SEG_FUSED), Hv, nc > SEG_FUSED).total;
   return std::max(old_path, fused);
 }
@@ -2060,7 +2116,7 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
   const bool persist = !fused && n_seqs > 1 && static_cast<int64_t>(Hv) * (DV / SCAN_COLS) >= SCAN_PERSIST_BLOCKS;
   const int64_t seg = std::min<int64_t>(nc, fused ? SEG_FUSED : SEG_CHUNKS);
   const WsLayout l = fused ? ws_layout_fused(n_seqs, seg, Hv, nc > SEG_FUSED)
-                           : ws_layout(n_seqs, seg, Hv, Hk, nc > SEG_CHUNKS);
+                           : ws_layout(n_seqs, seg, Hv, nc > SEG_CHUNKS);
   if (!workspace || workspace_bytes < l.total)
     return fail(GDN_ERR_WORKSPACE, "%s: workspace %zu bytes < %zu needed", name, workspace_bytes, l.total);
   if (reinterpret_cast<uintptr_t>(workspace) % 256)
@@ -2073,7 +2129,7 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
               q_stride_t, k_stride_t, v_stride_t, gate, h0, h0_idx, h0_rows, hT, hT_idx, hT_rows, o, o_dtype,
               cu_seqlens, n_seqs, T, Hk, Hv, total, scale, l2norm_qk, static_cast<int>(nc), 0, 0,
               reinterpret_cast<int32_t *>(ws + l.chunk_start), reinterpret_cast<u32x4 *>(ws + l.vh),
-              reinterpret_cast<u32x4 *>(ws + l.kh), reinterpret_cast<float *>(ws + l.Ut),
+              reinterpret_cast<float *>(ws + l.Ut),
               reinterpret_cast<float *>(ws + l.carry), reinterpret_cast<int64_t *>(ws + l.seqrec)};
   auto set_segment = [&](int64_t segment) {
     a.seg_begin = static_cast<int>(segment * seg);
