@@ -671,7 +671,7 @@ def bench_in_proj(torch, sets=6, reps=4):
             "fused_eager_us": t_eager,
             "roofline": {"bound": "hbm", "achieved": byts / t_fused / 1e3, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                          "frac": byts / (t_fused * 1e-6) / HBM_PEAK, "bytes_per_launch": byts,
-                         "kernel": "gdn::in_proj_decode_kernel<16>"}}
+                         "kernel": "gdn::in_proj_xs_kernel<16, 4>"}}
 
 
 def bench_out_proj(torch, sets=16, reps=4):

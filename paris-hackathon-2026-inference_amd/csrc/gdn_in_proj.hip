@@ -13,33 +13,27 @@
 // bias, SiLU) to the qkv columns before anything is written, so the qkv
 // projection never round-trips through memory.
 //
-// Work split: one workgroup per 64 output columns of one matrix (b and a
-// share one block: column groups 0, 1 take b's first 32 columns, 2, 3 a's)
-// and per 64 hidden rows.  Its 16 waves are 4 column groups of 16 columns x
-// 4 quarters of K: a lone wave per 16 columns cannot keep enough weight
-// loads in flight (measured: 193 workgroups of 4 waves stream the 50.6 MB at
-// 3.0 TB/s, of 16 waves at 4.9 TB/s).  A wave issues all its weight loads
-// (16 columns x K/4 as MFMA A operands: lane (r, g) reads row r, 16 bytes
-// at k = 32 s + 8 g) at the start and multiplies each as it arrives with the
-// hidden rows of its quarter, which the workgroup copies into LDS by LDS DMA
-// (contiguous 1 KiB reads, row-major in LDS with a chunk swizzle): the first
-// half of every quarter (all 64 rows, 128 KiB) before the weights are
-// requested, the second half into the same buffer once the first is
-// consumed, its copy overlapping the tail of the weight stream.  (Loads
-// retire in order: rows requested after the weights wait for all of them.)
-// The four quarters' partial sums meet in LDS;
-// wave (column group, quarter q) adds them in quarter order for row tile q
-// and runs the epilogue on it.  Lane (c, g) of a row tile's accumulator
-// holds out[16 t + c][16 w + 4 g .. + 3]: four consecutive channels of one
-// row, also the unit of the conv pool ([rows, C, 4] bf16: 32 bytes).
+// Work split (in_proj_xs_kernel): the hidden rows stay in registers, the
+// weights stream past them.  Every CU gets a workgroup; its 16 waves split
+// K, each holding its K / 16 columns of all 64 rows as MFMA B operands, and
+// walk the workgroup's tiles of 16 output columns (3-4 per workgroup for
+// the Qwen3.5-MoE layer), each wave multiplying its K / 16 of a tile's
+// weight rows as they arrive.  The waves' partial products meet in LDS,
+// and waves 0-3 add them in wave order and run the epilogue for one row
+// tile each.  Lane (c, g) of a row tile's accumulator holds
+// out[16 t + c][col + 4 g .. + 3]: four consecutive channels of one row,
+// also the unit of the conv pool ([rows, C, 4] bf16: 32 bytes).
 //
-// The same scheme serves out_proj at decode ([Hv*V -> D], modeling_qwen3_5_moe.py:540:
-// 16.8 MB of weights for 64 rows): there the 2048 output columns give only
-// 32 blocks of 64, so K is split over workgroups as well (512 of K each, 256
-// workgroups), each writing its fp32 partial block to a workspace; a second
-// small kernel adds the partials in split order and writes bf16.  (Letting
+// out_proj at decode ([Hv*V -> D], modeling_qwen3_5_moe.py:540: 16.8 MB of
+// weights for 64 rows) has only 2048 output columns, so there K is split
+// over workgroups (512 of K each, 256 workgroups): each stages its rows'
+// 512 columns in LDS by DMA, multiplies them with 64 columns of weights in
+// 16 waves (4 column groups x 4 parts of K) and writes its fp32 partial
+// block to a workspace; a second small kernel adds the partials in split
+// order and writes bf16.  (Letting
 // the last workgroup of a column block add them needs agent-scope fences,
 // whose L2 writeback and invalidate per workgroup measured 111 us.)
+#include <algorithm>
 #include <mutex>
 
 #include "gdn_common.h"
@@ -55,6 +49,7 @@ constexpr int IP_WAVES = 16;         // waves per workgroup
 constexpr int IP_ROWS = 64;          // hidden rows per workgroup (4 row tiles)
 constexpr int IP_OOB = 0x40000000;   // buffer offset past every conv pool: loads read 0, nothing stored
 constexpr int IP_GEMV_ROWS = 2;      // up to this many rows: in_proj_gemv_kernel (more spill at K = 2048)
+constexpr int IP_COLS = 64;          // n_qkv and n_z come in multiples of this (the GEMV kernel's column blocks)
 
 // Workgroup shape: CG column groups of 16 x KQ parts of K (CG KQ = 16
 // waves); a wave holds KS k-steps (of 32) of weights; the hidden rows reach
@@ -71,8 +66,6 @@ struct ProjShape {
   static_assert(CG * KQ == IP_WAVES && KS % NPH == 0 && 64 % CH == 0 && (KQ * CH) % IP_WAVES == 0, "shape");
   static_assert(LDS_BLOCKS * 16 <= 128 * 1024 && KQ * CG * 4 * 64 <= LDS_BLOCKS, "LDS");
 };
-using InProjShape2048 = ProjShape<4, 4, 16, 2>;  // input projections, K = 2048
-using InProjShape1024 = ProjShape<4, 4, 8, 2>;   // input projections, K = 1024
 using OutProjShape = ProjShape<4, 4, 4, 1>;      // out_proj: 64 columns x 512 of K per workgroup
 constexpr int OP_KSPAN = 4 * OutProjShape::KPART;  // K per workgroup (512)
 constexpr int OP_MAX_SPLIT = 16;                  // workgroups per column block (K <= 8192)
@@ -196,118 +189,222 @@ __device__ __forceinline__ f32x4_t proj_phases(u32x4_t *xl, const u32x4_t (&wr)[
   return o;
 }
 
-// S: InProjShape2048 or InProjShape1024.
-template <class S>
-__global__ __launch_bounds__(64 * IP_WAVES) void in_proj_decode_kernel(InProjArgs a) {
-  __shared__ u32x4_t xl[S::LDS_BLOCKS];  // one phase of the hidden rows: 128 KiB at K = 2048
-  constexpr int KS = S::KS;
+// Conv update of one row's 4 consecutive qkv channels n .. n + 3 (the conv
+// update kernel's arithmetic: fp32, bias first, taps oldest first): o the
+// projection (fp32 sums, rounded to bf16 as the nn.Linear output), w01 / w23
+// the taps of channels n, n + 1 / n + 2, n + 3, bias4 their bf16 biases,
+// win0 / win1 their windows (oldest first).  Writes y_qkv and, unless woff
+// is IP_OOB, the advanced windows at byte offset woff of the pool.
+__device__ __forceinline__ void conv_epilogue(const InProjArgs &a, const f32x4_t &o, const u32x4_t &w01,
+                                              const u32x4_t &w23, uint64_t bias4, const u32x4_t &win0,
+                                              const u32x4_t &win1, int woff, int me, int n) {
+  float y[4];
+  uint32_t nw[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const u32x4_t &tv = e < 2 ? w01 : w23;
+    const uint32_t tlo = tv[2 * (e & 1)], thi = tv[2 * (e & 1) + 1];
+    const u32x4_t &v = e < 2 ? win0 : win1;
+    const uint32_t lo = v[2 * (e & 1)], hi = v[2 * (e & 1) + 1];
+    const uint16_t xb = f32_to_bf16_bits(o[e]);
+    float acc_c = bf16_bits_to_f32(static_cast<uint16_t>(bias4 >> (16 * e)));
+    acc_c += bf16_bits_to_f32(tlo & 0xffffu) * bf16_bits_to_f32(lo >> 16);
+    acc_c += bf16_bits_to_f32(tlo >> 16) * bf16_bits_to_f32(hi & 0xffffu);
+    acc_c += bf16_bits_to_f32(thi & 0xffffu) * bf16_bits_to_f32(hi >> 16);
+    acc_c += bf16_bits_to_f32(thi >> 16) * bf16_bits_to_f32(xb);
+    y[e] = a.silu ? silu_f(acc_c) : acc_c;
+    nw[2 * e] = (lo >> 16) | (hi << 16);                            // s1 | s2
+    nw[2 * e + 1] = (hi >> 16) | (static_cast<uint32_t>(xb) << 16);  // s3 | x
+  }
+  if (woff != IP_OOB) {
+    u32x4_t *st = reinterpret_cast<u32x4_t *>(reinterpret_cast<char *>(a.pool) + woff);
+    st[0] = u32x4_t{nw[0], nw[1], nw[2], nw[3]};
+    st[1] = u32x4_t{nw[4], nw[5], nw[6], nw[7]};
+  }
+  uint2 *yp = reinterpret_cast<uint2 *>(a.y[0] + static_cast<int64_t>(me) * a.n[0] + n);
+  *yp = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
+}
+
+// ---------------------------------------------------------------------------
+// Input projections, rows held in registers ("x-stationary").
+//
+// The four matrices are cut into tiles of 16 output columns (qkv, z, b, a in
+// that order: 772 tiles for the Qwen3.5-MoE layer); workgroup b of G takes
+// tiles b, b + G, ... (G = max(256, tiles / 4), so every CU works and a
+// workgroup has at most XS_MAX_TILES).  Its 16 waves split K: wave w holds
+// K / 16 columns of all 64 hidden rows as MFMA B operands in registers
+// (64 VGPRs at K = 2048), loaded once, and streams the matching K / 16 of
+// each tile's 16 weight rows, the next tile's requested as soon as the
+// current one is multiplied.  The 16 waves' partial
+// products of a tile meet in LDS; wave t < 4 adds them in wave order for row
+// tile t and runs the epilogue (the conv update for qkv columns, a bf16
+// store otherwise) from conv windows, taps and bias that LDS DMA fetched
+// at the start.  Per CU: the hidden rows once (256 KiB at K = 2048, L2
+// hits after the first) and 3-4 tiles of weights (64 KiB each).
+constexpr int XS_WAVES = 16;
+constexpr int XS_MAX_TILES = 4;
+constexpr int XS_MIN_WGS = 256;  // MI355X CUs
+
+struct XsTile {
+  int mat, col, live;  // matrix (0 qkv, 1 z, 2 b, 3 a), first column, columns in the matrix (<= 16)
+};
+
+__device__ __forceinline__ XsTile xs_tile(const InProjArgs &a, const int (&tiles)[4], int j) {
+  XsTile t;
+  int m = 0;
+  while (m < 3 && j >= tiles[m]) {
+    j -= tiles[m];
+    ++m;
+  }
+  // (uniform values: readfirstlane keeps the buffer descriptors in SGPRs)
+  t.mat = __builtin_amdgcn_readfirstlane(m);
+  t.col = __builtin_amdgcn_readfirstlane(16 * j);
+  const int n = t.mat == 0 ? a.n[0] : t.mat == 1 ? a.n[1] : t.mat == 2 ? a.n[2] : a.n[3];
+  t.live = __builtin_amdgcn_readfirstlane(max(0, min(16, n - t.col)));
+  return t;
+}
+
+// NW waves, KSW k-steps (of 32) per wave: K = NW * 32 * KSW.
+template <int NW, int KSW>
+__global__ __launch_bounds__(64 * NW) void in_proj_xs_kernel(InProjArgs a) {
+  constexpr int K = NW * 32 * KSW;
+  static_assert(NW >= 5, "waves 0-3 run the epilogue, wave 4 fetches the taps");
+  __shared__ f32x4_t red[NW][4][64];                       // partial products of one tile
+  __shared__ u32x4_t win[XS_MAX_TILES][4][2][64];          // conv windows by tile, row tile, half, lane: 32 KiB
+  __shared__ u32x4_t tap[XS_MAX_TILES][64];                // lanes 0-7 taps (2 channels each), 8-9 bias
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int cg = wave % S::CG, kq = wave / S::CG;
+  const int c = lane & 15, g = lane >> 4;
   const int m0 = blockIdx.y * IP_ROWS;
   const int mb = min(IP_ROWS, a.M - m0);
+  const int tiles[4] = {(a.n[0] + 15) / 16, (a.n[1] + 15) / 16, (a.n[2] + 15) / 16, (a.n[3] + 15) / 16};
+  const int ntiles = tiles[0] + tiles[1] + tiles[2] + tiles[3];
+  const int G = gridDim.x;
+  const int nt = __builtin_amdgcn_readfirstlane((ntiles - static_cast<int>(blockIdx.x) + G - 1) / G);  // <= XS_MAX_TILES
+  const int kw = wave * 32 * KSW;  // this wave's columns of K
 
-  // this wave's matrix and first column
-  int mat, col;
-  const int bid = blockIdx.x;
-  if (bid < a.blocks_qkv) {
-    mat = 0;
-    col = bid * S::COLS + 16 * cg;
-  } else if (bid < a.blocks_qkv + a.blocks_z) {
-    mat = 1;
-    col = (bid - a.blocks_qkv) * S::COLS + 16 * cg;
-  } else {
-    mat = 2 + (cg >> 1);
-    col = 16 * (cg & 1);
-  }
-  mat = __builtin_amdgcn_readfirstlane(mat);
-  col = __builtin_amdgcn_readfirstlane(col);
-  // (selects, not a.w[mat]: an indexed kernel-argument array is not known to be uniform)
-  const uint16_t *wmat = mat == 0 ? a.w[0] : mat == 1 ? a.w[1] : mat == 2 ? a.w[2] : a.w[3];
-  const int nmat = mat == 0 ? a.n[0] : mat == 1 ? a.n[1] : mat == 2 ? a.n[2] : a.n[3];
-  const int live = __builtin_amdgcn_readfirstlane(max(0, min(16, nmat - col)));  // columns of this wave in its matrix
-  const auto rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(wmat) + static_cast<int64_t>(col) * a.K, 0,
-                                                    live * a.K * 2, BUF_DWORD3);
-  const uint16_t *xbase = a.x + static_cast<int64_t>(m0) * a.xs;
-  const int xbytes = static_cast<int>(((mb - 1) * a.xs + a.K) * 2);
-  const int c = lane & 15, g = lane >> 4;
-  const int n = col + 4 * g;
-  const int me = m0 + 16 * kq + c;  // the row this lane finishes
-  const bool conv = mat == 0;
-  const auto rp = __builtin_amdgcn_make_buffer_rsrc(a.pool, 0, conv ? static_cast<int>(a.rows * a.n[0] * 8) : 0,
-                                                    BUF_DWORD3);
-  const auto rc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.cw), 0, conv ? a.n[0] * 8 : 0,
-                                                    BUF_DWORD3);
-  const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.cb), 0, conv && a.cb ? a.n[0] * 2 : 0,
-                                                    BUF_DWORD3);
-
-  // Issue order: the epilogue's slot id, taps and bias; rows 0-31 (DMA);
-  // all weights; then the conv window, whose address needs the id (the
-  // oldest load, so waiting for it waits for nothing else).
-  // (through a buffer so that a missing id array reads 0 instead of branching on a load)
+  // slot id of the row this lane finishes (waves 0-3: row tile = wave)
+  const int me = m0 + 16 * wave + c;
   const auto ri = __builtin_amdgcn_make_buffer_rsrc(const_cast<int64_t *>(a.idx), 0, a.idx ? a.M * 8 : 0, BUF_DWORD3);
-  const uint64_t id_raw = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(ri, min(me, a.M - 1) * 8, 0, 0));
-  const u32x4_t w01 = __builtin_amdgcn_raw_buffer_load_b128(rc, n * 8, 0, 0);
-  const u32x4_t w23 = __builtin_amdgcn_raw_buffer_load_b128(rc, n * 8, 16, 0);
-  const uint64_t bias4 = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(rb, n * 2, 0, 0));
-  __builtin_amdgcn_sched_barrier(0);
-  dma_x<S>(xl, xbase, xbytes, a.xs, 0, wave, lane);
-  __builtin_amdgcn_sched_barrier(0);
-  u32x4_t wr[KS];
-  load_w<KS>(wr, rw, kq * S::KPART, a.K, lane);
-  __builtin_amdgcn_sched_barrier(0);
-  const int64_t id = a.idx ? static_cast<int64_t>(id_raw) : me;  // pool_row's rule
-  // a row whose slot id repeats an earlier row's selects no window (the
-  // ids are uniform loads; the wave waits for them behind the weight stream)
-  bool rep = false;
-  if (conv && a.idx) {
-    const int mlast = min(m0 + 16 * kq + 15, a.M - 1);
-    for (int m = 0; m < mlast; ++m) rep |= m < me && a.idx[m] == id;
-  }
-  const int woff = conv && me < a.M && !rep && id >= 0 && id < a.rows ? static_cast<int>((id * a.n[0] + n) * 8)
-                                                                      : IP_OOB;
-  u32x4_t win[2];
-  win[0] = __builtin_amdgcn_raw_buffer_load_b128(rp, woff, 0, 0);
-  win[1] = __builtin_amdgcn_raw_buffer_load_b128(rp, woff, 16, 0);
+  uint64_t id_raw = 0;
+  if (wave < 4) id_raw = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(ri, min(me, a.M - 1) * 8, 0, 0));
   __builtin_amdgcn_sched_barrier(0);
 
-  const f32x4_t o = proj_phases<S, 2>(
-      xl, wr, [&](int h) { dma_x<S>(xl, xbase, xbytes, a.xs, h, wave, lane); }, wave, lane);
-
-  // ---- epilogue of row tile kq: lane (c, g) holds row me, columns n .. n + 3
-  if (4 * g >= live || me >= a.M) return;  // (live is a multiple of 4)
-  if (conv) {
-    // the conv update kernel's arithmetic: fp32, bias first, taps oldest first
-    float y[4];
-    uint32_t nw[8];
+  // the hidden rows: B operand of row tile t, k-step s at lane (c, g) = row 16 t + c, k = kw + 32 s + 8 g
+  const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.x) + static_cast<int64_t>(m0) * a.xs, 0,
+                                                    static_cast<int>(((mb - 1) * a.xs + K) * 2), BUF_DWORD3);
+  u32x4_t xr[4][KSW];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const u32x4_t &tv = e < 2 ? w01 : w23;
-      const uint32_t tlo = tv[2 * (e & 1)], thi = tv[2 * (e & 1) + 1];
-      const u32x4_t &v = win[e >> 1];
-      const uint32_t lo = v[2 * (e & 1)], hi = v[2 * (e & 1) + 1];
-      const uint16_t xb = f32_to_bf16_bits(o[e]);
-      float acc_c = bf16_bits_to_f32(static_cast<uint16_t>(bias4 >> (16 * e)));
-      acc_c += bf16_bits_to_f32(tlo & 0xffffu) * bf16_bits_to_f32(lo >> 16);
-      acc_c += bf16_bits_to_f32(tlo >> 16) * bf16_bits_to_f32(hi & 0xffffu);
-      acc_c += bf16_bits_to_f32(thi & 0xffffu) * bf16_bits_to_f32(hi >> 16);
-      acc_c += bf16_bits_to_f32(thi >> 16) * bf16_bits_to_f32(xb);
-      y[e] = a.silu ? silu_f(acc_c) : acc_c;
-      nw[2 * e] = (lo >> 16) | (hi << 16);                            // s1 | s2
-      nw[2 * e + 1] = (hi >> 16) | (static_cast<uint32_t>(xb) << 16);  // s3 | x
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int s = 0; s < KSW; ++s)
+      xr[t][s] = __builtin_amdgcn_raw_buffer_load_b128(rx, static_cast<int>(((16 * t + c) * a.xs + kw + 32 * s + 8 * g) * 2),
+                                                       0, 0);
+  // a tile's weights: lane (r, g) of k-step s holds W[col + r][kw + 32 s + 8 g .. + 8] (rows past the matrix: 0)
+  auto load_tile = [&](u32x4_t (&w)[KSW], int i) {
+    const XsTile t = xs_tile(a, tiles, static_cast<int>(blockIdx.x) + G * i);
+    const uint16_t *wm = t.mat == 0 ? a.w[0] : t.mat == 1 ? a.w[1] : t.mat == 2 ? a.w[2] : a.w[3];
+    const auto rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(wm) + static_cast<int64_t>(t.col) * K, 0,
+                                                      t.live * K * 2, BUF_DWORD3);
+    const int voff = (c * K + kw + 8 * g) * 2;
+#pragma unroll
+    for (int s = 0; s < KSW; ++s) w[s] = __builtin_amdgcn_raw_buffer_load_b128(rw, voff, 64 * s, 0);
+  };
+  u32x4_t w[KSW];
+  load_tile(w, 0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // conv windows (waves 0-3, their row tile) and taps / bias (wave 4) of the qkv tiles into LDS
+  const int64_t id = a.idx ? static_cast<int64_t>(id_raw) : me;  // pool_row's rule
+  int wbase = -1;  // byte offset of this lane's row in the pool, -1: no window (waves 0-3)
+  if (wave < 4) {
+    // a row whose slot id repeats an earlier row's selects no window
+    bool rep = false;
+    if (a.idx) {
+      const int mlast = min(m0 + 16 * wave + 15, a.M - 1);
+      for (int m = 0; m < mlast; ++m) rep |= m < me && a.idx[m] == id;
     }
-    if (woff != IP_OOB) {
-      u32x4_t *st = reinterpret_cast<u32x4_t *>(reinterpret_cast<char *>(a.pool) + woff);
-      st[0] = u32x4_t{nw[0], nw[1], nw[2], nw[3]};
-      st[1] = u32x4_t{nw[4], nw[5], nw[6], nw[7]};
+    const bool has = me < a.M && !rep && id >= 0 && id < a.rows;
+    wbase = has ? static_cast<int>(id * a.n[0] * 8) : -1;  // (< IP_OOB: checked on the host)
+    const auto rp = __builtin_amdgcn_make_buffer_rsrc(a.pool, 0, static_cast<int>(a.rows * a.n[0] * 8), BUF_DWORD3);
+    for (int i = 0; i < nt; ++i) {
+      const XsTile t = xs_tile(a, tiles, static_cast<int>(blockIdx.x) + G * i);
+      if (t.mat != 0) continue;
+      const int woff = wbase >= 0 ? wbase + (t.col + 4 * g) * 8 : IP_OOB;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, &win[i][wave][h][0], 16, woff, 16 * h, 0, 0);
     }
-    uint2 *yp = reinterpret_cast<uint2 *>(a.y[0] + static_cast<int64_t>(me) * a.n[0] + n);
-    *yp = make_uint2(pack2(y[0], y[1]), pack2(y[2], y[3]));
-  } else {
-    uint16_t *ymat = mat == 1 ? a.y[1] : mat == 2 ? a.y[2] : a.y[3];
-    uint2 *yp = reinterpret_cast<uint2 *>(ymat + static_cast<int64_t>(me) * nmat + n);
-    *yp = make_uint2(pack2(o[0], o[1]), pack2(o[2], o[3]));
+  } else if (wave == 4) {
+    const auto rc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.cw), 0, a.n[0] * 8, BUF_DWORD3);
+    const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.cb), 0, a.cb ? a.n[0] * 2 : 0, BUF_DWORD3);
+    for (int i = 0; i < nt; ++i) {
+      const XsTile t = xs_tile(a, tiles, static_cast<int>(blockIdx.x) + G * i);
+      if (t.mat != 0) continue;
+      if (lane < 8)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, &tap[i][0], 16, (t.col + 2 * lane) * 8, 0, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, &tap[i][0], 16, lane < 10 ? (t.col + 8 * (lane - 8)) * 2 : IP_OOB, 0,
+                                                 0, 0);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  for (int i = 0; i < nt; ++i) {
+    f32x4_t acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KSW; ++s)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[t] = mfma16(w[s], xr[t][s], acc[t]);
+    // the next tile's weights into the same registers, in flight during the
+    // epilogue (a second buffer does not fit beside the rows of x)
+    const bool more = i + 1 < nt;
+    if (more) load_tile(w, i + 1);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) red[wave][t][lane] = acc[t];
+    if (i == 0) {  // the DMAs landed (only the weights just requested may still fly)
+      if (more)
+        __builtin_amdgcn_s_waitcnt(ip_vmcnt(KSW));
+      else
+        __builtin_amdgcn_s_waitcnt(ip_vmcnt(0));
+    }
+    __syncthreads();
+    if (wave < 4) {
+      // row tile `wave`: lane (c, g) holds row me, columns col + 4 g .. + 3; the
+      // partials in wave order, four read at a time (the registers hold x)
+      f32x4_t o = red[0][wave][lane];
+#pragma unroll 1
+      for (int q0 = 1; q0 < NW; q0 += 4) {
+        const f32x4_t p0 = red[q0][wave][lane];
+        const f32x4_t p1 = q0 + 1 < NW ? red[q0 + 1][wave][lane] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+        const f32x4_t p2 = q0 + 2 < NW ? red[q0 + 2][wave][lane] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+        const f32x4_t p3 = q0 + 3 < NW ? red[q0 + 3][wave][lane] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+        o += p0;
+        if (q0 + 1 < NW) o += p1;
+        if (q0 + 2 < NW) o += p2;
+        if (q0 + 3 < NW) o += p3;
+      }
+      const XsTile t = xs_tile(a, tiles, static_cast<int>(blockIdx.x) + G * i);
+      const int n = t.col + 4 * g;
+      if (4 * g < t.live && me < a.M) {
+        if (t.mat == 0) {
+          const u32x4_t w01 = tap[i][2 * g], w23 = tap[i][2 * g + 1];
+          const u32x4_t bb = tap[i][8 + (g >> 1)];
+          const uint64_t bias4 = (g & 1) ? (static_cast<uint64_t>(bb[3]) << 32 | bb[2])
+                                         : (static_cast<uint64_t>(bb[1]) << 32 | bb[0]);
+          const int woff = wbase >= 0 ? wbase + n * 8 : IP_OOB;
+          conv_epilogue(a, o, w01, w23, bias4, win[i][wave][0][lane], win[i][wave][1][lane], woff, me, n);
+        } else {
+          uint16_t *ymat = t.mat == 1 ? a.y[1] : t.mat == 2 ? a.y[2] : a.y[3];
+          const int nmat = t.mat == 1 ? a.n[1] : t.mat == 2 ? a.n[2] : a.n[3];
+          uint2 *yp = reinterpret_cast<uint2 *>(ymat + static_cast<int64_t>(me) * nmat + n);
+          *yp = make_uint2(pack2(o[0], o[1]), pack2(o[2], o[3]));
+        }
+      }
+    }
+    __syncthreads();  // the partials are consumed: the next tile's may go in
   }
 }
 
@@ -671,12 +768,12 @@ extern "C" int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w
   if (!x || !w_qkv || !w_z || !conv_w || !conv_pool || !y_qkv || !z || ((n_b > 0) && (!w_b || !b)) ||
       ((n_a > 0) && (!w_a || !a)))
     return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_in_proj_decode: null pointer argument");
-  if (M < 0 || n_qkv <= 0 || n_qkv % InProjShape2048::COLS || n_z < 0 || n_z % InProjShape2048::COLS || n_b < 0 || n_a < 0 || n_b % 4 ||
+  if (M < 0 || n_qkv <= 0 || n_qkv % IP_COLS || n_z < 0 || n_z % IP_COLS || n_b < 0 || n_a < 0 || n_b % 4 ||
       n_a % 4 || n_b > 32 || n_a > 32)
     return fail(GDN_ERR_UNSUPPORTED,
                 "gdn_in_proj_decode: need n_qkv and n_z multiples of %d, n_b and n_a multiples of 4 up to 32 "
                 "(got M=%d n=%d/%d/%d/%d)",
-                InProjShape2048::COLS, M, n_qkv, n_z, n_b, n_a);
+                IP_COLS, M, n_qkv, n_z, n_b, n_a);
   if (K != 1024 && K != 2048)
     return fail(GDN_ERR_UNSUPPORTED, "gdn_in_proj_decode: K=%d (built for 1024 and 2048)", K);
   if (x_stride < K || x_stride % 8)
@@ -711,8 +808,8 @@ extern "C" int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w
   args.n[1] = n_z;
   args.n[2] = n_b;
   args.n[3] = n_a;
-  args.blocks_qkv = n_qkv / InProjShape2048::COLS;
-  args.blocks_z = n_z / InProjShape2048::COLS;
+  args.blocks_qkv = n_qkv / IP_COLS;
+  args.blocks_z = n_z / IP_COLS;
   args.M = M;
   args.K = K;
   args.cw = static_cast<const uint16_t *>(conv_w);
@@ -735,9 +832,12 @@ extern "C" int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w
       launch_gemv<2>(args, grid.x, K / 512, s);
     return check_launch("gdn_in_proj_decode");
   }
+  const int ntiles = (n_qkv + 15) / 16 + (n_z + 15) / 16 + (n_b + 15) / 16 + (n_a + 15) / 16;
+  const int gx = std::min(ntiles, std::max(XS_MIN_WGS, (ntiles + XS_MAX_TILES - 1) / XS_MAX_TILES));
+  const dim3 xgrid(static_cast<unsigned>(gx), grid.y);
   switch (K) {
-    case 1024: hipLaunchKernelGGL(in_proj_decode_kernel<InProjShape1024>, grid, dim3(64 * IP_WAVES), 0, s, args); break;
-    case 2048: hipLaunchKernelGGL(in_proj_decode_kernel<InProjShape2048>, grid, dim3(64 * IP_WAVES), 0, s, args); break;
+    case 1024: hipLaunchKernelGGL((in_proj_xs_kernel<XS_WAVES, 2>), xgrid, dim3(64 * XS_WAVES), 0, s, args); break;
+    case 2048: hipLaunchKernelGGL((in_proj_xs_kernel<XS_WAVES, 4>), xgrid, dim3(64 * XS_WAVES), 0, s, args); break;
     default: return fail(GDN_ERR_UNSUPPORTED, "gdn_in_proj_decode: K=%d unsupported", K);
   }
   return check_launch("gdn_in_proj_decode");
