@@ -553,13 +553,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
 // D = diag(nk) (the k-row l2norm factors), L = diag(beta nk) M D for
 // M = strict_lower(K K^T * Gamma), so
 //   T = (I + L)^-1 = D^-1 T^ D,   T^ = (I + L^)^-1,   L^ = diag(beta nk^2) M,
-// and L^ needs each row's own norm only.  The record of (chunk, v-head):
-//   blocks 0..9    T^[p][b], b <= p, as block p (p + 1) / 2 + b, row layout
-//                  (lane (g, r): T^[16 p + r][16 b + 4 g .. 4 g + 3])
-//   blocks 10, 11  per-position scalars (float [SC_N][64], see SC_*)
-// The consumers form W = D^-1 T^ diag(beta e^gamma nk^2) K and
-// U = D^-1 T^ diag(beta nk) V, the same as T diag(beta e^gamma nk) K and
-// T diag(beta) V.
+// and L^ needs each row's own norm only.  The consumers form
+// W = D^-1 T^ diag(beta e^gamma nk^2) K and U = D^-1 T^ diag(beta nk) V, the
+// same as T diag(beta e^gamma nk) K and T diag(beta) V.
 // Solve record of one (chunk, v-head): 25 blocks of 1 KiB, lane l's 16 bytes
 // at 16 l.  Fragment f of a row block pb (f = tfrag(pb, s), k-step s < ksteps(pb),
 // the k-steps right of the diagonal being zero): lane (g, r) holds
@@ -855,7 +851,11 @@ constexpr int SG_MFMA = 0x8, SG_DS_RD = 0x100;
 // stage blocks per chunk: the v-head region, K and Q rows (raw, 4 rows per
 // block, swizzled as nsw), U
 constexpr int RS_VH = 0, RS_K = NB_VH, RS_Q = RS_K + 16, RS_U = RS_Q + 16, RS_BLOCKS = RS_U + 4;  // 61 blocks
-constexpr int RS_LOADER0 = NB_VH + 4;  // loader 0: v-head region + U blocks; loader 1: K and Q rows
+// Loader 0 copies the v-head region but for the two A blocks the compute
+// waves never read ((p, s) = (0, 1), (1, 1): zero, and left unwritten by the
+// prep), then the U blocks; loader 1 the K and Q rows.
+constexpr int RS_VH_COPIES = NB_VH - 2;
+constexpr int RS_LOADER0 = RS_VH_COPIES + 4;
 constexpr int RS_LOADER1 = 32;
 constexpr int SCAN_WAVES = 6;
 constexpr int SCAN_COLS = 16;  // state columns per workgroup
@@ -940,11 +940,13 @@ __device__ __forceinline__ void stage_copy(u32x4 *st, const RowSrc &r, const Chu
   const int rl = lane >> 4, ps = lane & 15;
   for (int i = i0; i < i1; ++i) {
     if constexpr (LD == 0) {
-      if (i < NB_VH)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r.vh, st + (RS_VH + i) * 64, 16, lane * 16, i * 1024, 0, 0);
-      else
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r.ut, st + (RS_U + i - NB_VH) * 64, 16, lane * 16,
-                                                 (4 * ct + i - NB_VH) * 1024, 0, 0);
+      if (i < RS_VH_COPIES) {
+        const int blk = i + (i > VH_A) + (i > VH_A + 1);  // (skips blocks VH_A + 1, VH_A + 3)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r.vh, st + (RS_VH + blk) * 64, 16, lane * 16, blk * 1024, 0, 0);
+      } else {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r.ut, st + (RS_U + i - RS_VH_COPIES) * 64, 16, lane * 16,
+                                                 (4 * ct + i - RS_VH_COPIES) * 1024, 0, 0);
+      }
     } else {
       const int b = i & 15, row = 4 * b + rl;
       const int seg = 16 * (ps ^ (row & 15));  // (the whole offset is in the range-checked vector offset)
@@ -2027,9 +2029,9 @@ WsLayout ws_layout(int n_seqs, int64_t seg_chunks, int Hv, bool multi) {
 }
 
 // Workspace of the solve + fused scan path: the chunk table, the carried
-// state (several segments), and one solve record (12 KiB) per (chunk,
-// v-head) of a segment of up to SEG_FUSED chunks (96 MiB at 32 v-heads; they
-// are read back right after they are written, from the Infinity Cache).
+// state (several segments), and one solve record (RB_N = 25 KiB) per (chunk,
+// v-head) of a segment of up to SEG_FUSED chunks (200 MiB at 32 v-heads;
+// they are read back right after they are written).
 constexpr int SEG_FUSED = 256;
 
 WsLayout ws_layout_fused(int n_seqs, int64_t seg_chunks, int Hv, bool multi) {
