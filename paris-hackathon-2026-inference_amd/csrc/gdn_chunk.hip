@@ -129,6 +129,10 @@ struct ChunkArgs {
   float *Ut;             // [SEG][Hv][8 x 4 blocks][64][4]  U, fp32
   float *carry;          // [n_seqs][Hv][128][128] state between segments
   int64_t *seqrec;       // [n_seqs][SEQREC]: per-sequence record for the persistent scan
+  // [SEG][Hv / 2]: the chunk's q and k rows of v-head 2i + 1 equal those of 2i
+  // (q and k given per v-head, Hk == Hv: the caller repeated them); null
+  // unless the prep checks and the scan uses it
+  int32_t *dup;
 };
 
 // Per-sequence record written by chunk_table_kernel for the persistent scan:
@@ -280,12 +284,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   __shared__ __align__(16) float gam_s[CK], beta_s[CK], nk_s[CK], nq_s[CK], colw_s[CK];
 
   const int ratio = a.Hv / a.Hk;
+  // the v-heads that read the same q / k rows (those of one k-head; a checked
+  // pair with repeated q / k) on one XCD: grp heads per group, hg groups
+  const int grp = a.dup ? 2 : ratio, hg = a.Hv / grp;
   int h = blockIdx.x, jl = blockIdx.y;  // v-head; chunk index within the segment's workspace
-  if ((a.Hk * static_cast<int>(gridDim.y)) % 8 == 0) {  // the v-heads of one k-head on one XCD
+  if ((hg * static_cast<int>(gridDim.y)) % 8 == 0) {
     int g, m;
-    xcd_group_order(blockIdx.x + gridDim.x * blockIdx.y, ratio, &g, &m);
-    h = (g % a.Hk) * ratio + m;
-    jl = g / a.Hk;
+    xcd_group_order(blockIdx.x + gridDim.x * blockIdx.y, grp, &g, &m);
+    h = (g % hg) * grp + m;
+    jl = g / hg;
   }
   const int j = a.seg_begin + jl;  // global chunk index
   if (j >= a.seg_end || j >= chunk_start_at(a, a.n_seqs)) return;
@@ -305,7 +312,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   const int c = j - chunk_start_at(a, n);
   const int64_t t0 = s0 + static_cast<int64_t>(c) * CK;
   const int len = min(CK, slen - c * CK);
-  if (len <= 0) return;
+  if (len <= 0) {
+    if (a.dup && (h & 1) && threadIdx.x == 0) a.dup[jl * (a.Hv / 2) + h / 2] = 1;  // (no rows: nothing differs)
+    return;
+  }
   const int hk = h / ratio;
 
   const int tid = threadIdx.x;
@@ -339,6 +349,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
         x1 = *reinterpret_cast<const u32x2 *>(qrow + 32 * s + 16);
       }
       qf[s] = as_bf16x8(u32x4{x0.x, x0.y, x1.x, x1.y});
+    }
+  }
+  // an odd v-head with per-v-head q / k (dup): its rows against the even
+  // partner's, the same loads from head hk - 1 (on this XCD's L2)
+  bool same = true;
+  if (a.dup && (h & 1)) {
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int row = (tid >> 4) + 16 * it;
+      if (row < len) {
+        const u32x4 kp = *reinterpret_cast<const u32x4 *>(a.k + (t0 + row) * a.ks + (int64_t)(hk - 1) * DK + seg * 8);
+        same = same && kp[0] == ku[it][0] && kp[1] == ku[it][1] && kp[2] == ku[it][2] && kp[3] == ku[it][3];
+      }
+    }
+    if (irow < len) {
+      const uint16_t *qrow = a.q + (t0 + irow) * a.qs + (int64_t)(hk - 1) * DK + 4 * g4;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const u32x2 x0 = *reinterpret_cast<const u32x2 *>(qrow + 32 * s);
+        const u32x2 x1 = *reinterpret_cast<const u32x2 *>(qrow + 32 * s + 16);
+        const u32x4 own = __builtin_bit_cast(u32x4, qf[s]);
+        same = same && x0.x == own[0] && x0.y == own[1] && x1.x == own[2] && x1.y == own[3];
+      }
     }
   }
   float gv = 0.f, bv = 0.f;
@@ -383,7 +416,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
     gam_s[lane] = gv;
     beta_s[lane] = bv;
   }
-  __syncthreads();
+  if (a.dup) {
+    const int all_same = __syncthreads_and(same);
+    if ((h & 1) && tid == 0) a.dup[jl * (a.Hv / 2) + h / 2] = all_same;
+  } else {
+    __syncthreads();
+  }
 
   // Per-position scalars: the scan's output / state-increment scales, and W's column scale.
   if (p == 0) {
@@ -1151,17 +1189,18 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_kernel(ChunkArgs a
   const int g4 = lane >> 4;
   const int nh = a.n_seqs * a.Hv;
   const int ratio = a.Hv / a.Hk;
+  const int grp = a.dup ? 2 : ratio, hg = a.Hv / grp;  // v-heads reading the same q / k rows
   int ct = blockIdx.x / nh;    // plain order: the column tiles of one head share bid % 8,
   int rest = blockIdx.x % nh;  // i.e. one XCD and its L2
-  if ((a.n_seqs * a.Hk) % 8 == 0) {  // also the v-heads of one k-head
+  if ((a.n_seqs * hg) % 8 == 0) {  // also the v-heads of one k-head (of a checked pair)
     int g, m;
-    xcd_group_order(blockIdx.x, ratio * (DV / SCAN_COLS), &g, &m);
+    xcd_group_order(blockIdx.x, grp * (DV / SCAN_COLS), &g, &m);
     ct = m % (DV / SCAN_COLS);
-    rest = (g / a.Hk) * a.Hv + (g % a.Hk) * ratio + m / (DV / SCAN_COLS);
+    rest = (g / hg) * a.Hv + (g % hg) * grp + m / (DV / SCAN_COLS);
   }
   const int n = rest / a.Hv;
   const int h = rest % a.Hv;
-  const int hk = h / ratio;
+  int hk = h / ratio;
   const int col = 16 * ct + (lane & 15);
 
   int64_t s0;
@@ -1193,6 +1232,14 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_kernel(ChunkArgs a
   const int nch = hi - lo;
   const int c0 = lo - a.seg_begin;                             // first chunk, workspace-local
   const int64_t seq_off = static_cast<int64_t>(lo - cs) * CK;  // its first token within the sequence
+  if (a.dup && (h & 1)) {  // every chunk of the range repeats the even partner's q / k rows: read that copy
+    bool all = true;
+    for (int i0 = 0; i0 < nch; i0 += 64) {
+      const int i = i0 + lane;
+      all = all && __all(i >= nch || a.dup[(c0 + i) * (a.Hv / 2) + h / 2] != 0);
+    }
+    if (all) hk = h - 1;
+  }
   if (wave >= 4) {
     if (wave == 4)
       scan_rows_loader<0>(stage, nch, ct, lane, a, c0, h, hk);
@@ -2006,7 +2053,7 @@ constexpr int SEG_CHUNKS = 64;
 // there are several) and the scan operands of one segment.
 struct WsLayout {
   size_t chunk_start, seqrec, carry, total;
-  size_t vh, Ut;
+  size_t vh, Ut, dup;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -2024,6 +2071,8 @@ WsLayout ws_layout(int n_seqs, int64_t seg_chunks, int Hv, bool multi) {
   off = align256(off + 16ull * seg_chunks * Hv * NB_VH * 64);
   l.Ut = off;
   off = align256(off + sizeof(float) * seg_chunks * Hv * DV * CK);
+  l.dup = off;
+  off = align256(off + sizeof(int32_t) * seg_chunks * ((Hv + 1) / 2));
   l.total = off;
   return l;
 }
@@ -2046,6 +2095,7 @@ WsLayout ws_layout_fused(int n_seqs, int64_t seg_chunks, int Hv, bool multi) {
   l.vh = off;
   off = align256(off + 1024ull * RB_N * seg_chunks * Hv);
   l.Ut = off;
+  l.dup = off;
   l.total = off;
   return l;
 }
@@ -2132,7 +2182,10 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
               cu_seqlens, n_seqs, T, Hk, Hv, total, scale, l2norm_qk, static_cast<int>(nc), 0, 0,
               reinterpret_cast<int32_t *>(ws + l.chunk_start), reinterpret_cast<u32x4 *>(ws + l.vh),
               reinterpret_cast<float *>(ws + l.Ut),
-              reinterpret_cast<float *>(ws + l.carry), reinterpret_cast<int64_t *>(ws + l.seqrec)};
+              reinterpret_cast<float *>(ws + l.carry), reinterpret_cast<int64_t *>(ws + l.seqrec), nullptr};
+  // q and k given per v-head (Hk == Hv): the prep checks each chunk's pairs
+  // of v-heads for repeated rows and the scan reads one copy of a repeated pair
+  if (!fused && !persist && Hk == Hv && Hv % 2 == 0) a.dup = reinterpret_cast<int32_t *>(ws + l.dup);
   auto set_segment = [&](int64_t segment) {
     a.seg_begin = static_cast<int>(segment * seg);
     a.seg_end = static_cast<int>(std::min<int64_t>((segment + 1) * seg, nc));

@@ -79,6 +79,40 @@ def test_batched_b2_and_gqa_native_equals_repeated():
     assert torch.equal(o2, o) and torch.equal(s2, s)
 
 
+@pytest.mark.parametrize("t", [300, 4200])
+def test_repeated_qk_single_sequence_equals_native(t):
+    """q and k given per v-head (Hk == Hv) as repeat_interleave makes them: the
+    prep finds every pair of v-heads repeated and the scan reads one copy of
+    each pair; the results are the GQA call's bits (4200 tokens: two workspace
+    segments)."""
+    c = configs.config2(seed=11, t=t)
+    o, s = run_chunk(c)
+    rep = dict(c)
+    rep["q"] = c["q"].repeat_interleave(2, 2)
+    rep["k"] = c["k"].repeat_interleave(2, 2)
+    o2, s2 = run_chunk(rep)
+    assert torch.equal(o2, o) and torch.equal(s2, s)
+
+
+def test_per_v_head_qk_with_partly_repeated_pairs():
+    """Hk == Hv with pairs that repeat in every chunk, pairs that differ in
+    one row of one chunk (q of head 5, k of head 9), and independent heads
+    (20-31): each v-head's own q and k rows are used wherever its pair differs."""
+    c = configs.config2(seed=12, t=300)
+    gen = torch.Generator().manual_seed(13)
+    q = c["q"].repeat_interleave(2, 2).clone()
+    k = c["k"].repeat_interleave(2, 2).clone()
+    q[0, 130, 5] = torch.randn(128, generator=gen).to(torch.bfloat16)
+    k[0, 200, 9] = torch.randn(128, generator=gen).to(torch.bfloat16)
+    q[:, :, 20:] = torch.randn(1, 300, 12, 128, generator=gen).to(torch.bfloat16)
+    k[:, :, 20:] = torch.randn(1, 300, 12, 128, generator=gen).to(torch.bfloat16)
+    mixed = dict(c, q=q, k=k)
+    o, s = run_chunk(mixed)
+    o_ref, s_ref = oracle_chunk(mixed)
+    assert np.abs(np64(o) - o_ref).max() < O_TOL
+    assert gdn.state_rel_err(np64(s), s_ref) < S_TOL
+
+
 def test_slot_pool_in_place():
     c = configs.config2(seed=8, t=100)
     cb = {x: torch.cat([c[x], c[x].flip(1)], 0) for x in c}
