@@ -215,45 +215,49 @@ __global__ __launch_bounds__(CONV_NT) void conv_fwd_kernel(ConvArgs a) {
   }
 
   // General tile: a sequence boundary or the end of the input falls inside it.
-  auto fetch = [&](Raw (&r)[PF], int64_t tb) {
+  // The tile is walked one sequence segment at a time.  Inside a segment the
+  // loads run one batch ahead as in the full tile (addresses clamped to the
+  // segment's last token, so a batch past its end re-reads a cached row) and
+  // only the token step is guarded; between segments the window is reloaded
+  // from the next sequence's history.
+  int64_t sb = tbeg;  // first token of the current segment
+  for (;;) {
+    const int64_t se = min(tend, s_end);  // sb < se
+    auto fetch = [&](Raw (&r)[PF], int64_t tb) {
 #pragma unroll
-    for (int u = 0; u < PF; ++u)
-      if (tb + u < tend) r[u] = Vec8<T>::load_raw(xc + (tb + u) * a.xs);
-  };
-  Raw r0[PF], r1[PF];
-  bool live = true;
-  // One batch: tokens tb .. tb + PF - 1 from registers cur, the next batch requested into nxt.
-  auto batch = [&](const Raw (&cur)[PF], Raw (&nxt)[PF], int64_t tb) {
-    if (tb + PF < tend) fetch(nxt, tb + PF);
+      for (int u = 0; u < PF; ++u) r[u] = Vec8<T>::load_raw(xc + min(tb + u, se - 1) * a.xs);
+    };
+    Raw r0[PF], r1[PF];
+    fetch(r0, sb);
+    for (int64_t tb = sb; tb < se; tb += 2 * PF) {
+      fetch(r1, tb + PF);
 #pragma unroll
-    for (int u = 0; u < PF; ++u) {
-      const int64_t t = tb + u;
-      if (!live || t >= tend) break;
-      if (t == s_end) {  // the next sequence starts inside this tile
-        ++n;
-        if (a.cu) {
-          while (n < a.n_seqs && a.cu[n + 1] <= t) ++n;  // skip empty sequences
-          if (n >= a.n_seqs) { live = false; break; }
-        }
-        {
-          int len;
-          seq_range(a.cu, n, a.T, a.total, &s_beg, &len);
-          s_end = s_beg + len;
-        }
-        if (t < s_beg || t >= s_end) { live = false; break; }
-        const int64_t hrow = in_row_of(a, n);
+      for (int u = 0; u < PF; ++u)
+        if (tb + u < se) token(r0[u], tb + u);
+      fetch(r0, tb + 2 * PF);
 #pragma unroll
-        for (int j = 0; j < WIN; ++j)
-#pragma unroll
-          for (int i = 0; i < CPT; ++i) win[j][i] = history_at<T, SL>(a, hrow, c0 + i, WIN - j);
-      }
-      token(cur[u], t);
+      for (int u = 0; u < PF; ++u)
+        if (tb + PF + u < se) token(r1[u], tb + PF + u);
     }
-  };
-  fetch(r0, tbeg);
-  for (int64_t tb = tbeg; live && tb < tend; tb += 2 * PF) {
-    batch(r0, r1, tb);
-    if (live && tb + PF < tend) batch(r1, r0, tb + PF);
+    if (se >= tend) return;
+    // the next sequence starts at se, inside this tile
+    ++n;
+    if (a.cu) {
+      while (n < a.n_seqs && a.cu[n + 1] <= se) ++n;  // skip empty sequences
+      if (n >= a.n_seqs) return;
+    }
+    {
+      int len;
+      seq_range(a.cu, n, a.T, a.total, &s_beg, &len);
+      s_end = s_beg + len;
+    }
+    if (se < s_beg || se >= s_end) return;  // tokens outside every sequence
+    const int64_t hrow = in_row_of(a, n);
+#pragma unroll
+    for (int j = 0; j < WIN; ++j)
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) win[j][i] = history_at<T, SL>(a, hrow, c0 + i, WIN - j);
+    sb = se;
   }
 }
 
