@@ -52,6 +52,19 @@ __device__ __forceinline__ float load_elem(const void *p, int64_t i, int dt) {
   return static_cast<float>(static_cast<const _Float16 *>(p)[i]);
 }
 
+// load_elem in two halves: the raw bits (f32, or a 2-byte type zero-extended)
+// and their conversion, so that a load can be issued long before its value is
+// needed without the conversion pulling the wait forward.
+__device__ __forceinline__ uint32_t load_bits(const void *p, int64_t i, int dt) {
+  if (dt == GDN_DTYPE_F32) return static_cast<const uint32_t *>(p)[i];
+  return static_cast<const uint16_t *>(p)[i];
+}
+__device__ __forceinline__ float bits_to_f32(uint32_t b, int dt) {
+  if (dt == GDN_DTYPE_F32) return __uint_as_float(b);
+  if (dt == GDN_DTYPE_BF16) return bf16_bits_to_f32(static_cast<uint16_t>(b));
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+}
+
 __device__ __forceinline__ void store_elem(void *p, int64_t i, int dt, float x) {
   if (dt == GDN_DTYPE_F32) {
     static_cast<float *>(p)[i] = x;
@@ -87,6 +100,50 @@ __device__ __forceinline__ void load_gates(const GateArgs &ga, int64_t tok, int 
   } else {
     *g = static_cast<const float *>(ga.g_or_a)[i];
     *beta = load_elem(ga.beta_or_b, i, ga.dt);
+  }
+}
+
+// load_bits for a wave-uniform address, always as a vector memory instruction
+// (a buffer load).  A plain uniform load becomes a scalar load for one dtype
+// and a vector load for another, and the dtype branches then serialise their
+// waits.
+__device__ __forceinline__ uint32_t load_bits_vmem(const void *p, int64_t i, int dt) {
+  const int es = dt == GDN_DTYPE_F32 ? 4 : 2;
+  const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(static_cast<const char *>(p) + i * es), 0, 4,
+                                                    BUF_DWORD3);
+  return dt == GDN_DTYPE_F32 ? static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, 0, 0, 0))
+                             : static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(rs, 0, 0, 0));
+}
+
+// load_gates in two halves (raw loads, then the gate math), for the same reason
+// as load_bits; tok and h are wave-uniform.
+struct GateRaw {
+  uint32_t ga, gb;        // a (or g) and b (or beta), raw bits
+  float a_log, dt_bias;   // raw mode only
+};
+__device__ __forceinline__ GateRaw load_gates_raw(const GateArgs &ga, int64_t tok, int h) {
+  const int64_t i = tok * ga.stride + h;
+  GateRaw r;
+  if (ga.A_log) {
+    r.ga = load_bits_vmem(ga.g_or_a, i, ga.dt);
+    r.a_log = ga.A_log[h];
+    r.dt_bias = ga.dt_bias[h];
+  } else {
+    r.ga = load_bits_vmem(ga.g_or_a, i, GDN_DTYPE_F32);
+    r.a_log = r.dt_bias = 0.f;
+  }
+  r.gb = load_bits_vmem(ga.beta_or_b, i, ga.dt);
+  return r;
+}
+__device__ __forceinline__ void gates_from_raw(const GateArgs &ga, const GateRaw &r, float *g, float *beta) {
+  if (ga.A_log) {
+    const float x = bits_to_f32(r.ga, ga.dt) + r.dt_bias;
+    const float sp = x > 20.f ? x : log1pf(expf(x));
+    *g = -expf(r.a_log) * sp;
+    *beta = 1.f / (1.f + expf(-bits_to_f32(r.gb, ga.dt)));
+  } else {
+    *g = __uint_as_float(r.ga);
+    *beta = bits_to_f32(r.gb, ga.dt);
   }
 }
 
@@ -137,6 +194,25 @@ __device__ __forceinline__ bool repeats_earlier(const int64_t *idx, int64_t n) {
   const int64_t id = idx[n];
   for (int64_t base = 0; base < n; base += cnt) {
     const int64_t m = base + pos;
+    if (__ballot(m < n && idx[m] == id)) return true;
+  }
+  return false;
+}
+
+// repeats_earlier in two halves for one full wave (all 64 lanes active, n
+// uniform): the earlier ids, one per lane, can be requested ahead of a long
+// stream of vector loads and tested after it.  Vector loads complete in order,
+// so the test then waits for these ids only, not for the stream.  `id` is
+// idx[n]; ids beyond the first 64 rows are read in the test itself.
+__device__ __forceinline__ int64_t earlier_id_of_lane(const int64_t *idx, int64_t n, int lane) {
+  return (idx && lane < n) ? idx[lane] : 0;
+}
+__device__ __forceinline__ bool repeats_earlier_wave(const int64_t *idx, int64_t n, int64_t id, int64_t lane_id,
+                                                     int lane) {
+  if (!idx || n <= 0) return false;
+  if (__ballot(lane < n && lane_id == id)) return true;
+  for (int64_t base = 64; base < n; base += 64) {
+    const int64_t m = base + lane;
     if (__ballot(m < n && idx[m] == id)) return true;
   }
   return false;

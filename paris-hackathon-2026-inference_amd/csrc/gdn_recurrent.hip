@@ -46,7 +46,9 @@ struct RecArgs {
 };
 
 // Workgroup shape: 32 state columns, 64 threads (one wave, 16 rows per
-// thread, 137 VGPRs, 3 waves per SIMD).  Measured at B=64 on MI355X: 56.0 us;
+// thread, 149 VGPRs, 3 waves per SIMD; capped at 128 it spills and takes
+// 64.3 us).  Measured at B=64 on MI355X, before the first token's inputs were
+// requested ahead of the state: 56.0 us;
 // 128 threads (8 rows per thread, 4 waves per SIMD) 58.5 us; 256 threads
 // 62.7 us -- more waves per workgroup cost a cross-wave reduction per token.
 constexpr int REC_VT = 32;
@@ -84,8 +86,38 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(RecArgs a) {
 
   const int64_t in_row = a.state_in ? pool_row(a.in_idx, n, a.in_rows) : -1;
   int64_t out_row = a.state_out ? pool_row(a.out_idx, n, a.out_rows) : -1;
-  // (rows repeating an earlier row's slot id are found after the state loads
-  // are issued, so that the check adds no latency before the stream)
+
+  // A token's inputs as raw bits: this lane's two elements of q and k, its
+  // four columns of v, and the gates.
+  struct TokIn {
+    uint32_t q[2], k[2], v[4];
+    GateRaw gate;
+  };
+  auto tok_load = [&](int64_t tok) {
+    TokIn r;
+    const int64_t qoff = tok * a.qs + (int64_t)hk * KD + 2 * lane;
+    const int64_t koff = tok * a.ks + (int64_t)hk * KD + 2 * lane;
+    const int64_t vo = tok * a.vs + (int64_t)h * VD + col0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      r.q[i] = load_bits(a.q, qoff + i, a.qkv_dt);
+      r.k[i] = load_bits(a.k, koff + i, a.qkv_dt);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r.v[c] = load_bits(a.v, vo + c, a.qkv_dt);
+    r.gate = load_gates_raw(a.gate, tok, h);
+    return r;
+  };
+
+  // The first token's inputs and the earlier rows' slot ids are requested
+  // before the state: vector loads complete in order, so the q/k prologue and
+  // the repeated-slot test wait for these few loads only, while the state
+  // stream is in flight, and nothing is left to fetch once the state is in.
+  TokIn cur{};
+  if (len > 0) cur = tok_load(t0);
+  const int64_t in_lane_id = in_row >= 0 ? earlier_id_of_lane(a.in_idx, n, lane) : 0;
+  const int64_t out_lane_id = out_row >= 0 ? earlier_id_of_lane(a.out_idx, n, lane) : 0;
+  __builtin_amdgcn_sched_barrier(0);
 
   // The state is touched exactly once per launch: non-temporal loads and
   // stores keep it from displacing reusable lines in the caches.  One
@@ -94,33 +126,31 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(RecArgs a) {
   // 16 accesses share one vector offset.
   const int voff = (rg * VD + col0) * 4;
   constexpr int ROW8 = NRG * VD * 4;  // bytes between a thread's rows
+  // (a row with no slot gets an empty range: its loads read zeros without
+  // touching memory, so the loads are issued on one path whatever the row)
   auto state_rsrc = [&](const float *pool, int64_t row) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(pool) + (row * a.Hv + h) * (int64_t)(KD * VD), 0,
-                                             KD * VD * 4, BUF_DWORD3);
+    return row >= 0 ? __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(pool) + (row * a.Hv + h) * (int64_t)(KD * VD),
+                                                        0, KD * VD * 4, BUF_DWORD3)
+                    : __builtin_amdgcn_make_buffer_rsrc(nullptr, 0, 0, BUF_DWORD3);
   };
   f32x4 s[RPT];
-  if (in_row >= 0) {
+  {
     const auto rs = state_rsrc(a.state_in, in_row);
 #pragma unroll
     for (int r = 0; r < RPT; ++r)
       s[r] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, r * ROW8, BUF_NT));
-  } else {
-#pragma unroll
-    for (int r = 0; r < RPT; ++r) s[r] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  if (in_row >= 0 && repeats_earlier(a.in_idx, n)) {  // a repeated slot: zero state, like a padding row
-#pragma unroll
-    for (int r = 0; r < RPT; ++r) s[r] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  if (out_row >= 0 && repeats_earlier(a.out_idx, n)) out_row = -1;  // ... and nothing written
+  __builtin_amdgcn_sched_barrier(0);
+  // A row whose slot id an earlier row already named: zero state, like a
+  // padding row, and nothing written.
+  const bool in_rep = in_row >= 0 && repeats_earlier_wave(a.in_idx, n, in_row, in_lane_id, lane);
+  if (out_row >= 0 && repeats_earlier_wave(a.out_idx, n, out_row, out_lane_id, lane)) out_row = -1;
 
   for (int t = 0; t < len; ++t) {
     const int64_t tok = t0 + t;
     // ---- q/k prologue: every wave reduces the full 128-vectors itself
-    const int64_t qoff = tok * a.qs + (int64_t)hk * KD + 2 * lane;
-    const int64_t koff = tok * a.ks + (int64_t)hk * KD + 2 * lane;
-    float q0 = load_elem(a.q, qoff, a.qkv_dt), q1 = load_elem(a.q, qoff + 1, a.qkv_dt);
-    float k0 = load_elem(a.k, koff, a.qkv_dt), k1 = load_elem(a.k, koff + 1, a.qkv_dt);
+    const float q0 = bits_to_f32(cur.q[0], a.qkv_dt), q1 = bits_to_f32(cur.q[1], a.qkv_dt);
+    const float k0 = bits_to_f32(cur.k[0], a.qkv_dt), k1 = bits_to_f32(cur.k[1], a.qkv_dt);
     const float sqq = wave_sum(q0 * q0 + q1 * q1);
     const float skk = wave_sum(k0 * k0 + k1 * k1);
     const float sqk = wave_sum(q0 * k0 + q1 * k1);
@@ -135,12 +165,16 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(RecArgs a) {
     }
     const float qk = sqk * qsc * rk;
     float gl, bt;
-    load_gates(a.gate, tok, h, &gl, &bt);
+    gates_from_raw(a.gate, cur.gate, &gl, &bt);
     const float eg = expf(gl);
     float vv[4];
-    const int64_t voff = tok * a.vs + (int64_t)h * VD + col0;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) vv[c] = load_elem(a.v, voff + c, a.qkv_dt);
+    for (int c = 0; c < 4; ++c) vv[c] = bits_to_f32(cur.v[c], a.qkv_dt);
+    if (t + 1 < len) cur = tok_load(tok + 1);  // the next token's inputs, during this one's update
+    if (t == 0 && in_rep) {
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) s[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     __syncthreads();
 
     // ---- partial k~^T S and q~^T S over this thread's rows
@@ -213,6 +247,10 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(RecArgs a) {
     __syncthreads();
   }
 
+  if (len <= 0 && in_rep) {
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) s[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   if (out_row >= 0) {
     const auto rs = state_rsrc(a.state_out, out_row);
 #pragma unroll
