@@ -352,32 +352,56 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
     }
   }
   // an odd v-head with per-v-head q / k (dup): its rows against the even
-  // partner's, the same loads from head hk - 1 (on this XCD's L2)
-  bool same = true;
-  if (a.dup && (h & 1)) {
+  // partner's, the same loads from head hk - 1 (on this XCD's L2), requested
+  // with its own rows and the gates and compared once all of them are in
+  const bool chk = a.dup && (h & 1);
+  u32x4 kpart[4], qpart[4];
+  if (chk) {  // rows clamped to the chunk's last one (len >= 1), those past it not compared
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
-      const int row = (tid >> 4) + 16 * it;
-      if (row < len) {
-        const u32x4 kp = *reinterpret_cast<const u32x4 *>(a.k + (t0 + row) * a.ks + (int64_t)(hk - 1) * DK + seg * 8);
-        same = same && kp[0] == ku[it][0] && kp[1] == ku[it][1] && kp[2] == ku[it][2] && kp[3] == ku[it][3];
-      }
+      const int row = min((tid >> 4) + 16 * it, len - 1);
+      kpart[it] = *reinterpret_cast<const u32x4 *>(a.k + (t0 + row) * a.ks + (int64_t)(hk - 1) * DK + seg * 8);
     }
-    if (irow < len) {
-      const uint16_t *qrow = a.q + (t0 + irow) * a.qs + (int64_t)(hk - 1) * DK + 4 * g4;
+    const uint16_t *qrow = a.q + (t0 + min(irow, len - 1)) * a.qs + (int64_t)(hk - 1) * DK + 4 * g4;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const u32x2 x0 = *reinterpret_cast<const u32x2 *>(qrow + 32 * s);
-        const u32x2 x1 = *reinterpret_cast<const u32x2 *>(qrow + 32 * s + 16);
-        const u32x4 own = __builtin_bit_cast(u32x4, qf[s]);
-        same = same && x0.x == own[0] && x0.y == own[1] && x1.x == own[2] && x1.y == own[3];
-      }
+    for (int s = 0; s < 4; ++s) {
+      const u32x2 x0 = *reinterpret_cast<const u32x2 *>(qrow + 32 * s);
+      const u32x2 x1 = *reinterpret_cast<const u32x2 *>(qrow + 32 * s + 16);
+      qpart[s] = u32x4{x0.x, x0.y, x1.x, x1.y};
     }
+  }
+  GateRaw graw{0u, 0u, 0.f, 0.f};
+  if (p == 0 && lane < len) {
+    const int64_t gi = (t0 + lane) * a.gate.stride + h;
+    graw.ga = load_bits(a.gate.g_or_a, gi, a.gate.A_log ? a.gate.dt : GDN_DTYPE_F32);
+    graw.gb = load_bits(a.gate.beta_or_b, gi, a.gate.dt);
+  }
+  if (a.gate.A_log) {
+    graw.a_log = a.gate.A_log[h];
+    graw.dt_bias = a.gate.dt_bias[h];
+  }
+  bool same = true;
+  if (chk) {
+    uint32_t diff = 0u;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      uint32_t d = 0u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) d |= kpart[it][e] ^ ku[it][e];
+      diff |= (tid >> 4) + 16 * it < len ? d : 0u;
+    }
+    uint32_t dq = 0u;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const u32x4 own = __builtin_bit_cast(u32x4, qf[s]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dq |= qpart[s][e] ^ own[e];
+    }
+    diff |= irow < len ? dq : 0u;
+    same = diff == 0u;
   }
   float gv = 0.f, bv = 0.f;
-  if (p == 0 && lane < len) {
-    load_gates(a.gate, t0 + lane, h, &gv, &bv);
-  }
+  if (p == 0 && lane < len) gates_from_raw(a.gate, graw, &gv, &bv);
 
   // ---- A.1: K, V rows into LDS; K row norms; chunk-local cumsum of g; Q row norms
 #pragma unroll
