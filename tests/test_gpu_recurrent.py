@@ -269,3 +269,36 @@ def test_decode_b37_on_a_slot_pool_with_bad_and_repeated_ids(dtype, gated):
     assert gdn.state_rel_err(np64(pool_gpu[ids[live].to(DEV)]), s_ref[live]) < (S_TOL if dtype != torch.float32 else 1e-5)
     untouched = np.setdiff1d(np.arange(n_slots), ids[live].numpy())
     assert torch.equal(pool_gpu[untouched].cpu(), pool[untouched])
+
+
+@pytest.mark.parametrize("t", [1, 3])
+def test_repeated_ids_beyond_the_first_64_rows(t):
+    """B = 100 rows on a 128-slot pool.  The repeated-slot test compares a
+    row's id with the first 64 rows' ids held one per lane and reads the
+    ids of rows 64 .. n-1 in a loop: row 70 repeats row 10 (found among the
+    lanes), row 90 repeats row 80 and row 99 repeats row 66 (found in the
+    loop).  Each repeat selects no row (zero state in, nothing written), so
+    the pool's repeated slots hold the first row's result."""
+    gen = torch.Generator().manual_seed(71)
+    bsz, n_slots = 100, 128
+    q = torch.randn(bsz, t, 16, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(bsz, t, 16, 128, generator=gen).to(torch.bfloat16)
+    v = torch.randn(bsz, t, 32, 128, generator=gen).to(torch.bfloat16)
+    g = -torch.rand(bsz, t, 32, generator=gen) * 2
+    beta = torch.rand(bsz, t, 32, generator=gen)
+    pool = torch.randn(n_slots, 32, 128, 128, generator=gen) * 0.1
+    ids = torch.randperm(n_slots, generator=gen)[:bsz]
+    ids[70], ids[90], ids[99] = ids[10], ids[80], ids[66]
+    live = [i for i in range(bsz) if int(ids[i]) not in ids[:i].tolist()]
+    assert len(live) == bsz - 3
+    h0 = np.zeros((bsz, 32, 128, 128))
+    h0[live] = pool[ids[live]].numpy()
+    pool_gpu = pool.to(DEV)
+    o, _ = fused_recurrent_gated_delta_rule(*cuda(q, k, v, g, beta), initial_state=pool_gpu,
+                                            ssm_state_indices=ids.to(DEV), inplace_final_state=True,
+                                            use_qk_l2norm_in_kernel=True)
+    o_ref, s_ref = gdn.recurrent_gated_delta_rule(np64(q), np64(k), np64(v), np64(g), np64(beta), initial_state=h0)
+    assert np.abs(np64(o) - o_ref).max() < O_TOL_BF16
+    assert gdn.state_rel_err(np64(pool_gpu[ids[live].to(DEV)]), s_ref[live]) < S_TOL
+    untouched = np.setdiff1d(np.arange(n_slots), ids[live].numpy())
+    assert torch.equal(pool_gpu[untouched].cpu(), pool[untouched])
