@@ -19,7 +19,8 @@ The JSON line also carries
   prefill       chunk-64 prefill at T=4096 (configuration 2): tok/s and the
                 dense-equivalent flop rate against the 2.5 PFLOP/s bf16 peak
                 (q/k at 16 heads; prefill_qk_repeated: q/k repeated to 32 heads
-                as HF passes them);
+                as HF passes them); prefill_b16_t1038 (and _qk_repeated): the
+                reference's own profiled shape, 16 sequences of 1038 tokens;
   layer_glue    the GDN layer glue around the prefill core at configuration 2's
                 shape: HF's torch glue (gates, q/k repeat, RMSNormGated) vs
                 the fused kernels, and the gated-norm kernel's HBM rate;
@@ -279,11 +280,12 @@ def bench_prefill(torch, reps=24, warmup=3, repeat_qk=False, n_sets=3):
                      "frac": flop / per / MFMA_BF16_PEAK, "flop_per_call": flop}}
 
 
-def bench_prefill_b16(torch, reps=10):
+def bench_prefill_b16(torch, reps=10, repeat_qk=False):
     """The reference's own profiled prefill shape (its profile of fla's chunk
     kernel: 1.659 ms per layer on H200): a dense batch of 16 sequences of 1038
-    tokens (17 chunks each), q/k at 16 heads, v at 32, zero h0, final states
-    out; the batch is scanned by the persistent scan."""
+    tokens (17 chunks each), q/k at 16 heads (with repeat_qk: repeated to the
+    32 v-heads, as HF passes them), v at 32, zero h0, final states out; the
+    batch is scanned by the persistent scan."""
     from engine import configs
     from engine.kernels import chunk_gated_delta_rule
 
@@ -291,13 +293,15 @@ def bench_prefill_b16(torch, reps=10):
     b, t = 16, 1038
     c = configs.config2(seed=47, t=b * t)
     q, k, v, g, beta = (c[x].to(dev).reshape(b, t, *c[x].shape[2:]) for x in ("q", "k", "v", "g", "beta"))
+    if repeat_qk:
+        q, k = q.repeat_interleave(2, dim=2), k.repeat_interleave(2, dim=2)
 
     def run():
         return chunk_gated_delta_rule(q, k, v, g, beta, output_final_state=True, use_qk_l2norm_in_kernel=True)
 
     per = _time(torch, run, reps)
     flop = PREFILL_FLOP_PER_CHUNK_HEAD * b * ((t + 63) // 64) * 32
-    return {"config": "B=16 x T=1038 (17 chunks each), Hk=16 Hv=32 d=128 bf16, zero h0, final states out",
+    return {"config": f"B=16 x T=1038 (17 chunks each), Hk={q.shape[2]} Hv=32 d=128 bf16, zero h0, final states out",
             "us": per * 1e6, "tok_per_s": b * t / per,
             "mfma": {"achieved": flop / per / 1e12, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
                      "frac": flop / per / MFMA_BF16_PEAK, "flop": flop},
@@ -841,6 +845,8 @@ def main():
             out["layer_glue"] = bench_layer_glue(torch)
         out["varlen"] = bench_varlen(torch)
         out["prefill_b16_t1038"] = bench_prefill_b16(torch)
+        if not args.no_prefill_repeated:
+            out["prefill_b16_t1038_qk_repeated"] = bench_prefill_b16(torch, repeat_qk=True)
     out["spec_verify"] = bench_spec_verify(torch)
     if not args.no_conv:
         out["conv_prefill"] = bench_conv_prefill(torch)

@@ -113,6 +113,28 @@ def test_per_v_head_qk_with_partly_repeated_pairs():
     assert gdn.state_rel_err(np64(s), s_ref) < S_TOL
 
 
+
+def test_per_v_head_qk_pairs_on_the_persistent_scan():
+    """A batch of three (the persistent scan walks all of their chunks) with
+    q and k given per v-head: pairs repeated in every chunk of every
+    sequence, a pair whose odd head differs in one row of the second
+    sequence (q of head 7), a pair whose even head differs in one row of the
+    third (k of head 12), and independent heads (24-31)."""
+    c = configs.config2(seed=14, t=150)
+    cb = {x: torch.cat([c[x], c[x].flip(1), c[x].roll(7, 1)], 0) for x in c}
+    gen = torch.Generator().manual_seed(15)
+    q = cb["q"].repeat_interleave(2, 2).clone()
+    k = cb["k"].repeat_interleave(2, 2).clone()
+    q[1, 77, 7] = torch.randn(128, generator=gen).to(torch.bfloat16)
+    k[2, 140, 12] = torch.randn(128, generator=gen).to(torch.bfloat16)
+    q[:, :, 24:] = torch.randn(3, 150, 8, 128, generator=gen).to(torch.bfloat16)
+    k[:, :, 24:] = torch.randn(3, 150, 8, 128, generator=gen).to(torch.bfloat16)
+    mixed = dict(cb, q=q, k=k)
+    o, s = run_chunk(mixed)
+    o_ref, s_ref = oracle_chunk(mixed)
+    assert np.abs(np64(o) - o_ref).max() < O_TOL
+    assert gdn.state_rel_err(np64(s), s_ref) < S_TOL
+
 def test_slot_pool_in_place():
     c = configs.config2(seed=8, t=100)
     cb = {x: torch.cat([c[x], c[x].flip(1)], 0) for x in c}
