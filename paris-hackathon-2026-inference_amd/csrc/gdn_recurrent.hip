@@ -54,6 +54,21 @@ struct RecArgs {
 constexpr int REC_VT = 32;
 constexpr int REC_NT = 64;
 
+// Resident workgroups per CU.  The registers allow 12 of these one-wave
+// workgroups per CU (3 waves per SIMD, 256 CUs: 3,072 at once).  A decode
+// grid (one token per sequence) of more than one such round (B > 24 at 32
+// v-heads) reserves dynamic LDS that leaves room for 4 per CU: the state
+// streams of 4 resident workgroups per CU reach HBM faster than those of 12
+// (B = 64 from graphs: 54.2 -> 51.7 us; B = 48: 41.4 -> 39.8 us; B = 32:
+// 28.3 -> 28.2 us), while a grid that fits one round runs best with all of
+// it resident (B = 16: 13.5 us, 15.4-16.0 us capped).  Per CU at B = 64
+// (eager launches): 2 / 3 / 4 / 5 / 6 / 8 / 12 workgroups 69.7 / 55.4 / 51.8
+// / 52.2 / 52.6 / 54.7 / 54.7 us.  Multi-token steps (spec verify, with its
+// snapshot stream) keep full occupancy: B = 32 x T = 4 capped at 5 per CU took
+// 71.8-72.4 us against 68.7 us.
+constexpr int64_t REC_ROUND = 12 * 256;     // workgroups resident at full occupancy
+constexpr unsigned REC_CAP_LDS = 36 * 1024;  // + 1.25 KiB static: 4 per CU in 160 KiB
+
 template <int VT, int NT>
 __global__ __launch_bounds__(NT) void recurrent_kernel(RecArgs a) {
   constexpr int NW = NT / 64;
@@ -299,7 +314,8 @@ int recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
             state_out, state_out_idx, state_out_rows, o, snapshots, cu_seqlens, n_seqs, T, Hk, Hv,
             cu_seqlens ? static_cast<int64_t>(T) : static_cast<int64_t>(n_seqs) * T,
             scale, l2norm_qk, qkv_dtype, o_dtype};
-  hipLaunchKernelGGL((recurrent_kernel<REC_VT, REC_NT>), dim3(static_cast<unsigned>(n_blocks)), dim3(REC_NT), 0,
+  const unsigned lds = T == 1 && n_blocks > REC_ROUND ? REC_CAP_LDS : 0u;
+  hipLaunchKernelGGL((recurrent_kernel<REC_VT, REC_NT>), dim3(static_cast<unsigned>(n_blocks)), dim3(REC_NT), lds,
                      static_cast<hipStream_t>(stream), a);
   return check_launch(name);
 }
