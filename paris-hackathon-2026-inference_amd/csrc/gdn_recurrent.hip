@@ -43,6 +43,7 @@ struct RecArgs {
   float scale;
   int l2norm;
   int qkv_dt, o_dt;
+  int head_major;  // workgroup order: v-head fastest (a capped decode grid) or column block fastest
 };
 
 // Workgroup shape: 32 state columns, 64 threads (one wave, 16 rows per
@@ -54,20 +55,26 @@ struct RecArgs {
 constexpr int REC_VT = 32;
 constexpr int REC_NT = 64;
 
-// Resident workgroups per CU.  The registers allow 12 of these one-wave
-// workgroups per CU (3 waves per SIMD, 256 CUs: 3,072 at once).  A decode
-// grid (one token per sequence) of more than one such round (B > 24 at 32
-// v-heads) reserves dynamic LDS that leaves room for 4 per CU: the state
-// streams of 4 resident workgroups per CU reach HBM faster than those of 12
-// (B = 64 from graphs: 54.2 -> 51.7 us; B = 48: 41.4 -> 39.8 us; B = 32:
-// 28.3 -> 28.2 us), while a grid that fits one round runs best with all of
-// it resident (B = 16: 13.5 us, 15.4-16.0 us capped).  Per CU at B = 64
-// (eager launches): 2 / 3 / 4 / 5 / 6 / 8 / 12 workgroups 69.7 / 55.4 / 51.8
-// / 52.2 / 52.6 / 54.7 / 54.7 us.  Multi-token steps (spec verify, with its
-// snapshot stream) keep full occupancy: B = 32 x T = 4 capped at 5 per CU took
-// 71.8-72.4 us against 68.7 us.
+// Resident workgroups per CU and their order.  The registers allow 12 of
+// these one-wave workgroups per CU (3 waves per SIMD, 256 CUs: 3,072 at
+// once).  A decode grid (one token per sequence) of more than one such round
+// (B > 24 at 32 v-heads) is launched
+//   * with dynamic LDS reserved so that 6 share a CU: the state streams of
+//     fewer resident workgroups reach HBM faster (B = 64, eager launches,
+//     per CU: 3 / 4 / 5 / 6 / 8 / 12 workgroups 53.7 / 50.7 / 48.8 / 48.6 /
+//     51.5 / 52.2 us with the order below);
+//   * head-major: the v-heads of one (sequence, column block) in consecutive
+//     workgroups, so that the 4 column blocks of a head are a multiple of 8
+//     workgroups apart and run on one XCD (workgroups are dealt to the 8 XCDs
+//     in turn): the two 64-byte halves of each 128-byte line of o meet in
+//     that XCD's L2 and the head's q/k rows are fetched once (at 4 per CU:
+//     49.9-50.3 us against 51.8-52.3 us column-block-major).
+// A grid that fits one round runs best with all of it resident and column-
+// block-major (B = 16: 13.1 us; head-major 14.8 us; capped 15.4-16.0 us), and
+// so do multi-token steps (spec verify B = 32 x T = 4: 67.9 us; head-major
+// 71.0 us; capped at 5 per CU 71.8-72.4 us).
 constexpr int64_t REC_ROUND = 12 * 256;     // workgroups resident at full occupancy
-constexpr unsigned REC_CAP_LDS = 36 * 1024;  // + 1.25 KiB static: 4 per CU in 160 KiB
+constexpr unsigned REC_CAP_LDS = 24 * 1024;  // + 1 KiB static: 6 per CU in 160 KiB
 
 template <int VT, int NT>
 __global__ __launch_bounds__(NT) void recurrent_kernel(RecArgs a) {
@@ -87,11 +94,19 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(RecArgs a) {
   const int c4 = tid % TPR;
   const int rg = tid / TPR;
 
-  int bid = blockIdx.x;
-  const int vt = bid % NSPLIT;
-  bid /= NSPLIT;
-  const int h = bid % a.Hv;
-  const int n = bid / a.Hv;
+  int bid = blockIdx.x, vt, h;
+  if (a.head_major) {
+    h = bid % a.Hv;
+    bid /= a.Hv;
+    vt = bid % NSPLIT;
+    bid /= NSPLIT;
+  } else {
+    vt = bid % NSPLIT;
+    bid /= NSPLIT;
+    h = bid % a.Hv;
+    bid /= a.Hv;
+  }
+  const int n = bid;
   const int hk = h / (a.Hv / a.Hk);
   const int col0 = vt * VT + c4 * 4;
 
@@ -314,7 +329,9 @@ int recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
             state_out, state_out_idx, state_out_rows, o, snapshots, cu_seqlens, n_seqs, T, Hk, Hv,
             cu_seqlens ? static_cast<int64_t>(T) : static_cast<int64_t>(n_seqs) * T,
             scale, l2norm_qk, qkv_dtype, o_dtype};
-  const unsigned lds = T == 1 && n_blocks > REC_ROUND ? REC_CAP_LDS : 0u;
+  const bool capped = T == 1 && n_blocks > REC_ROUND;
+  a.head_major = capped;
+  const unsigned lds = capped ? REC_CAP_LDS : 0u;
   hipLaunchKernelGGL((recurrent_kernel<REC_VT, REC_NT>), dim3(static_cast<unsigned>(n_blocks)), dim3(REC_NT), lds,
                      static_cast<hipStream_t>(stream), a);
   return check_launch(name);
