@@ -57,24 +57,26 @@ constexpr int REC_NT = 64;
 
 // Resident workgroups per CU and their order.  The registers allow 12 of
 // these one-wave workgroups per CU (3 waves per SIMD, 256 CUs: 3,072 at
-// once).  A decode grid (one token per sequence) of more than one such round
-// (B > 24 at 32 v-heads) is launched
+// once).  A decode grid (one token per sequence) of more than 2,304
+// workgroups (B > 18 at 32 v-heads) is launched
 //   * with dynamic LDS reserved so that 6 share a CU: the state streams of
 //     fewer resident workgroups reach HBM faster (B = 64, eager launches,
-//     per CU: 3 / 4 / 5 / 6 / 8 / 12 workgroups 53.7 / 50.7 / 48.8 / 48.6 /
-//     51.5 / 52.2 us with the order below);
+//     per CU: 3 / 4 / 5 / 6 / 7 / 8 / 12 workgroups 53.7 / 50.7 / 48.6 /
+//     48.6 / 50.2 / 51.5 / 52.2 us with the order below);
 //   * head-major: the v-heads of one (sequence, column block) in consecutive
 //     workgroups, so that the 4 column blocks of a head are a multiple of 8
 //     workgroups apart and run on one XCD (workgroups are dealt to the 8 XCDs
 //     in turn): the two 64-byte halves of each 128-byte line of o meet in
 //     that XCD's L2 and the head's q/k rows are fetched once (at 4 per CU:
 //     49.9-50.3 us against 51.8-52.3 us column-block-major).
-// A grid that fits one round runs best with all of it resident and column-
-// block-major (B = 16: 13.1 us; head-major 14.8 us; capped 15.4-16.0 us), and
-// so do multi-token steps (spec verify B = 32 x T = 4: 67.9 us; head-major
-// 71.0 us; capped at 5 per CU 71.8-72.4 us).
-constexpr int64_t REC_ROUND = 12 * 256;     // workgroups resident at full occupancy
-constexpr unsigned REC_CAP_LDS = 24 * 1024;  // + 1 KiB static: 6 per CU in 160 KiB
+// From graphs: B = 20 / 24 / 25 / 32 / 64 17.7 / 20.4 / 21.9 / 26.4 / 48.7 us
+// against 18.3 / 21.4 / 23.7 / 28.3 / 54.2 us at full occupancy, column-block-
+// major.  A smaller grid (1.5 capped rounds or less) runs best with all of it
+// resident and column-block-major (B = 16: 13.4 us; capped 15.4 us), and so do
+// multi-token steps (spec verify B = 32 x T = 4: 67.9 us; head-major 71.0 us;
+// capped at 5 per CU 71.8-72.4 us).
+constexpr int64_t REC_CAP_MIN_BLOCKS = 2304;  // 1.5 rounds of 6 per CU on 256 CUs
+constexpr unsigned REC_CAP_LDS = 24 * 1024;   // + 1 KiB static: 6 per CU in 160 KiB
 
 template <int VT, int NT>
 __global__ __launch_bounds__(NT) void recurrent_kernel(RecArgs a) {
@@ -329,7 +331,7 @@ int recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
             state_out, state_out_idx, state_out_rows, o, snapshots, cu_seqlens, n_seqs, T, Hk, Hv,
             cu_seqlens ? static_cast<int64_t>(T) : static_cast<int64_t>(n_seqs) * T,
             scale, l2norm_qk, qkv_dtype, o_dtype};
-  const bool capped = T == 1 && n_blocks > REC_ROUND;
+  const bool capped = T == 1 && n_blocks > REC_CAP_MIN_BLOCKS;
   a.head_major = capped;
   const unsigned lds = capped ? REC_CAP_LDS : 0u;
   hipLaunchKernelGGL((recurrent_kernel<REC_VT, REC_NT>), dim3(static_cast<unsigned>(n_blocks)), dim3(REC_NT), lds,
