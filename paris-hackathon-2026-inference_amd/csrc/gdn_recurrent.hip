@@ -72,11 +72,17 @@ constexpr int REC_NT = 64;
 // From graphs: B = 20 / 24 / 25 / 32 / 64 17.7 / 20.4 / 21.9 / 26.4 / 48.7 us
 // against 18.3 / 21.4 / 23.7 / 28.3 / 54.2 us at full occupancy, column-block-
 // major.  A smaller grid (1.5 capped rounds or less) runs best with all of it
-// resident and column-block-major (B = 16: 13.4 us; capped 15.4 us), and so do
-// multi-token steps (spec verify B = 32 x T = 4: 67.9 us; head-major 71.0 us;
-// capped at 5 per CU 71.8-72.4 us).
-constexpr int64_t REC_CAP_MIN_BLOCKS = 2304;  // 1.5 rounds of 6 per CU on 256 CUs
-constexpr unsigned REC_CAP_LDS = 24 * 1024;   // + 1 KiB static: 6 per CU in 160 KiB
+// resident and column-block-major (B = 16: 13.4 us; capped 15.4 us).
+// A multi-token step that writes per-token snapshots (spec verify) is a
+// write stream as much as a read stream: head-major with 4 per CU (B = 32 x
+// T = 4: 66.4-67.9 us; full occupancy 71.4-71.6, head-major alone 69.4-70.3,
+// at 3 / 5 / 6 per CU 81.0 / 71.6-72.3 / 68.9-69.5 us).  Without snapshots the
+// tokens' arithmetic needs the resident waves: full occupancy, column-block-
+// major (B = 32 / 64 x T = 4: 40.2-41.2 / 70.7-71.2 us; at 4 per CU 56.0-56.7 /
+// 103.2-104.6 us).
+constexpr int64_t REC_CAP_MIN_BLOCKS = 2304;   // 1.5 rounds of 6 per CU on 256 CUs
+constexpr unsigned REC_CAP_LDS = 24 * 1024;    // + 1 KiB static: 6 per CU in 160 KiB
+constexpr unsigned REC_SNAP_CAP_LDS = 36 * 1024;  // + 1 KiB static: 4 per CU
 
 template <int VT, int NT>
 __global__ __launch_bounds__(NT) void recurrent_kernel(RecArgs a) {
@@ -331,9 +337,9 @@ int recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
             state_out, state_out_idx, state_out_rows, o, snapshots, cu_seqlens, n_seqs, T, Hk, Hv,
             cu_seqlens ? static_cast<int64_t>(T) : static_cast<int64_t>(n_seqs) * T,
             scale, l2norm_qk, qkv_dtype, o_dtype};
-  const bool capped = T == 1 && n_blocks > REC_CAP_MIN_BLOCKS;
+  const bool capped = n_blocks > REC_CAP_MIN_BLOCKS && (T == 1 || snapshots);
   a.head_major = capped;
-  const unsigned lds = capped ? REC_CAP_LDS : 0u;
+  const unsigned lds = !capped ? 0u : T == 1 ? REC_CAP_LDS : REC_SNAP_CAP_LDS;
   hipLaunchKernelGGL((recurrent_kernel<REC_VT, REC_NT>), dim3(static_cast<unsigned>(n_blocks)), dim3(REC_NT), lds,
                      static_cast<hipStream_t>(stream), a);
   return check_launch(name);
