@@ -46,10 +46,20 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
 constexpr int IP_WAVES = 16;         // waves per workgroup
+// GEMV kernels (one or two rows): waves per workgroup.  Smaller workgroups
+// spread the weight stream over more CUs.  Measured from HIP graphs over 6
+// (in_proj) or 16 (out_proj) weight sets: out_proj at M = 1 5.8 us with 16
+// waves per workgroup (64 workgroups), 4.7 / 4.55 / 4.7 us with 8 / 4 / 2;
+// in_proj at M = 1 / 2 11.7 / 12.7 us with 16, 11.4 / 12.2 with 8, 12.1 /
+// 12.3 with 4; the layer step at B = 1 28.2 us before, 23.9-24.0 us with
+// 8 and 4.
+constexpr int IN_GEMV_WAVES = 8;
+constexpr int IN_GEMV_COLS = 4 * IN_GEMV_WAVES;  // in_proj columns per workgroup
+constexpr int OUT_GEMV_WAVES = 4;
 constexpr int IP_ROWS = 64;          // hidden rows per workgroup (4 row tiles)
 constexpr int IP_OOB = 0x40000000;   // buffer offset past every conv pool: loads read 0, nothing stored
 constexpr int IP_GEMV_ROWS = 2;      // up to this many rows: in_proj_gemv_kernel (more spill at K = 2048)
-constexpr int IP_COLS = 64;          // n_qkv and n_z come in multiples of this (the GEMV kernel's column blocks)
+constexpr int IP_COLS = 64;          // n_qkv and n_z come in multiples of this
 
 // Workgroup shape: CG column groups of 16 x KQ parts of K (CG KQ = 16
 // waves); a wave holds KS k-steps (of 32) of weights; the hidden rows reach
@@ -409,15 +419,15 @@ __global__ __launch_bounds__(64 * NW) void in_proj_xs_kernel(InProjArgs a) {
 }
 
 // One or two rows (the smallest decode batches): the projection is a GEMV stream.
-// Workgroup = 16 waves over 64 columns of one matrix (the same column
-// blocks as the MFMA kernel); wave w takes columns 4 w .. 4 w + 3 and reads
+// Workgroup = IN_GEMV_WAVES waves over 4 IN_GEMV_WAVES columns of one matrix (b and
+// a: 8 waves each); wave w takes columns 4 w .. 4 w + 3 and reads
 // each of its weight rows as K / 512 contiguous 1 KiB loads (lane l: 16
 // bytes at 16 l of every KiB), all issued at the start; the rows of x sit in
 // registers in the same lane layout.  Each lane sums its products in fp32,
 // a wave reduction gives the dot products, and lane c + 4 m writes (row m,
 // column c), through the same conv epilogue as the MFMA kernel.
 template <int MR, int KB>  // MR rows (1, 2); KB = K / 512
-__global__ __launch_bounds__(64 * IP_WAVES) void in_proj_gemv_kernel(InProjArgs a) {
+__global__ __launch_bounds__(64 * IN_GEMV_WAVES, 4) void in_proj_gemv_kernel(InProjArgs a) {  // 4 waves per SIMD: <= 128 VGPRs
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -425,13 +435,14 @@ __global__ __launch_bounds__(64 * IP_WAVES) void in_proj_gemv_kernel(InProjArgs 
   const int bid = blockIdx.x;
   if (bid < a.blocks_qkv) {
     mat = 0;
-    col = bid * 64 + 4 * wave;
+    col = bid * IN_GEMV_COLS + 4 * wave;
   } else if (bid < a.blocks_qkv + a.blocks_z) {
     mat = 1;
-    col = (bid - a.blocks_qkv) * 64 + 4 * wave;
-  } else {
-    mat = 2 + (wave >> 3);
-    col = 4 * (wave & 7);
+    col = (bid - a.blocks_qkv) * IN_GEMV_COLS + 4 * wave;
+  } else {  // b then a, 8 waves of 4 columns each
+    const int w = (bid - a.blocks_qkv - a.blocks_z) * IN_GEMV_WAVES + wave;
+    mat = 2 + (w >> 3);
+    col = 4 * (w & 7);
   }
   mat = __builtin_amdgcn_readfirstlane(mat);
   col = __builtin_amdgcn_readfirstlane(col);
@@ -510,9 +521,9 @@ __global__ __launch_bounds__(64 * IP_WAVES) void in_proj_gemv_kernel(InProjArgs 
 template <int MR>
 void launch_gemv(const InProjArgs &args, unsigned gx, int kb, hipStream_t s) {
   if (kb == 2)
-    hipLaunchKernelGGL((in_proj_gemv_kernel<MR, 2>), dim3(gx), dim3(64 * IP_WAVES), 0, s, args);
+    hipLaunchKernelGGL((in_proj_gemv_kernel<MR, 2>), dim3(gx), dim3(64 * IN_GEMV_WAVES), 0, s, args);
   else
-    hipLaunchKernelGGL((in_proj_gemv_kernel<MR, 4>), dim3(gx), dim3(64 * IP_WAVES), 0, s, args);
+    hipLaunchKernelGGL((in_proj_gemv_kernel<MR, 4>), dim3(gx), dim3(64 * IN_GEMV_WAVES), 0, s, args);
 }
 
 struct OutProjArgs {
@@ -586,16 +597,16 @@ __global__ __launch_bounds__(OP_RED_NT) void out_proj_sum_kernel(OutProjArgs a) 
   *reinterpret_cast<uint2 *>(a.y + static_cast<int64_t>(m) * a.ys + n) = make_uint2(pack2(t[0], t[1]), pack2(t[2], t[3]));
 }
 
-// One row: a GEMV stream in one kernel (no partial sums).  Workgroup = 16
-// waves over 32 columns; wave w takes columns 2 w, 2 w + 1 and streams each
+// One row: a GEMV stream in one kernel (no partial sums).  Workgroup =
+// OUT_GEMV_WAVES waves over 2 OUT_GEMV_WAVES columns; wave w takes columns 2 w, 2 w + 1 and streams each
 // weight row as K / 512 contiguous 1 KiB loads (all issued at the start),
 // the row of x in registers in the same lane layout; a wave reduction per
 // column, lanes 0 and 1 store.  KB = K / 512.
 template <int KB>
-__global__ __launch_bounds__(64 * IP_WAVES) void out_proj_gemv_kernel(OutProjArgs a) {
+__global__ __launch_bounds__(64 * OUT_GEMV_WAVES) void out_proj_gemv_kernel(OutProjArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int col = (blockIdx.x * IP_WAVES + wave) * 2;
+  const int col = (blockIdx.x * OUT_GEMV_WAVES + wave) * 2;
   constexpr int K = KB * 512;
   const auto rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.w) + static_cast<int64_t>(col) * K, 0,
                                                     2 * K * 2, BUF_DWORD3);
@@ -627,8 +638,8 @@ __global__ __launch_bounds__(64 * IP_WAVES) void out_proj_gemv_kernel(OutProjArg
 
 template <int KB>
 void launch_out_gemv(const OutProjArgs &args, hipStream_t s) {
-  hipLaunchKernelGGL((out_proj_gemv_kernel<KB>), dim3(static_cast<unsigned>(args.N / (2 * IP_WAVES))),
-                     dim3(64 * IP_WAVES), 0, s, args);
+  hipLaunchKernelGGL((out_proj_gemv_kernel<KB>), dim3(static_cast<unsigned>(args.N / (2 * OUT_GEMV_WAVES))),
+                     dim3(64 * OUT_GEMV_WAVES), 0, s, args);
 }
 
 }  // namespace
@@ -808,8 +819,8 @@ extern "C" int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w
   args.n[1] = n_z;
   args.n[2] = n_b;
   args.n[3] = n_a;
-  args.blocks_qkv = n_qkv / IP_COLS;
-  args.blocks_z = n_z / IP_COLS;
+  args.blocks_qkv = n_qkv / IN_GEMV_COLS;
+  args.blocks_z = n_z / IN_GEMV_COLS;
   args.M = M;
   args.K = K;
   args.cw = static_cast<const uint16_t *>(conv_w);
@@ -822,7 +833,7 @@ extern "C" int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w
   args.y[2] = static_cast<uint16_t *>(b);
   args.y[3] = static_cast<uint16_t *>(a);
   args.silu = silu;
-  const dim3 grid(static_cast<unsigned>(args.blocks_qkv + args.blocks_z + (n_b + n_a > 0 ? 1 : 0)),
+  const dim3 grid(static_cast<unsigned>(args.blocks_qkv + args.blocks_z + (n_b + n_a > 0 ? 16 / IN_GEMV_WAVES : 0)),
                   static_cast<unsigned>((M + IP_ROWS - 1) / IP_ROWS));
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (M <= IP_GEMV_ROWS) {  // a GEMV stream of the weights (one row block)
