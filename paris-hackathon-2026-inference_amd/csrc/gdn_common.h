@@ -52,32 +52,6 @@ __device__ __forceinline__ float load_elem(const void *p, int64_t i, int dt) {
   return static_cast<float>(static_cast<const _Float16 *>(p)[i]);
 }
 
-// Four consecutive elements x[0..3] to p[i .. i+3] as one store (i a multiple
-// of 4, p aligned to its element type times 4); non-temporal when NT.
-template <bool NT>
-__device__ __forceinline__ void store4_elem(void *p, int64_t i, int dt, const float *x) {
-  if (dt == GDN_DTYPE_F32) {
-    typedef __attribute__((ext_vector_type(4))) float f4;
-    const f4 v = {x[0], x[1], x[2], x[3]};
-    f4 *q = reinterpret_cast<f4 *>(static_cast<float *>(p) + i);
-    if (NT) __builtin_nontemporal_store(v, q); else *q = v;
-    return;
-  }
-  uint32_t w[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const uint32_t lo = dt == GDN_DTYPE_BF16 ? f32_to_bf16_bits(x[2 * j])
-                                             : __builtin_bit_cast(uint16_t, static_cast<_Float16>(x[2 * j]));
-    const uint32_t hi = dt == GDN_DTYPE_BF16 ? f32_to_bf16_bits(x[2 * j + 1])
-                                             : __builtin_bit_cast(uint16_t, static_cast<_Float16>(x[2 * j + 1]));
-    w[j] = lo | (hi << 16);
-  }
-  typedef __attribute__((ext_vector_type(2))) uint32_t u2;
-  const u2 v = {w[0], w[1]};
-  u2 *q = reinterpret_cast<u2 *>(static_cast<uint16_t *>(p) + i);
-  if (NT) __builtin_nontemporal_store(v, q); else *q = v;
-}
-
 // load_elem in two halves: the raw bits (f32, or a 2-byte type zero-extended)
 // and their conversion, so that a load can be issued long before its value is
 // needed without the conversion pulling the wait forward.
