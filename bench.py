@@ -80,6 +80,9 @@ def parse():
     ap.add_argument("--pools", type=int, default=4, help="rotating decode state pools")
     ap.add_argument("--prefill-only", action="store_true",
                     help="time only the configuration 2 prefill (for counter profiles; prints no headline value)")
+    ap.add_argument("--layer-only", action="store_true",
+                    help="time only the decode projections and the whole-layer decode steps (for counter "
+                         "profiles; prints no headline value)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run the HBM ceiling probes: a plain 128 MiB device copy (also the "
                          "rocprofv3 FETCH_SIZE/WRITE_SIZE calibration), the same bytes in place, and a "
@@ -809,6 +812,10 @@ def main():
         return
     if args.prefill_only:  # the prefill kernels alone (for counter profiles); no headline value
         print(json.dumps({"prefill": bench_prefill(torch)}), flush=True)
+        return
+    if args.layer_only:  # the decode projections and layer steps alone (for counter profiles)
+        print(json.dumps({"decode_in_proj": bench_in_proj(torch), "decode_out_proj": bench_out_proj(torch),
+                          "layer_decode": bench_layer_decode(torch)}), flush=True)
         return
     d = bench_decode(torch, args.steps, args.warmup, args.pools)
     wall = d["eager_wall"]
