@@ -44,7 +44,6 @@
 // by conversion to bf16 alone (in the scan, between waves, through LDS
 // without any reordering).
 #include <algorithm>
-#include <cstdlib>
 #include <type_traits>
 
 #include "gdn_common.h"
@@ -606,275 +605,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   float *Uout = a.Ut + ch * (DV * CK);
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) *reinterpret_cast<f32x4 *>(Uout + ((4 * nb + p) * 64 + lane) * 4) = ut[nb];
-}
-
-// ------------------------------------------------------------------ solve
-// The fused prefill's producer: per (chunk, v-head) only the parts that every
-// state-column tile of the head shares and that need the whole chunk at
-// once -- the triangular solve and its per-position scalars.  With
-// D = diag(nk) (the k-row l2norm factors), L = diag(beta nk) M D for
-// M = strict_lower(K K^T * Gamma), so
-//   T = (I + L)^-1 = D^-1 T^ D,   T^ = (I + L^)^-1,   L^ = diag(beta nk^2) M,
-// and L^ needs each row's own norm only.  The consumers form
-// W = D^-1 T^ diag(beta e^gamma nk^2) K and U = D^-1 T^ diag(beta nk) V, the
-// same as T diag(beta e^gamma nk) K and T diag(beta) V.
-// Solve record of one (chunk, v-head): 25 blocks of 1 KiB, lane l's 16 bytes
-// at 16 l.  Fragment f of a row block pb (f = tfrag(pb, s), k-step s < ksteps(pb),
-// the k-steps right of the diagonal being zero): lane (g, r) holds
-// X[16 pb + r][32 s + 4 g + e] and X[16 pb + r][32 s + 16 + 4 g + e], e < 4, in bf16.
-//   RB_TW:  T_w = -diag(1/nk) T^ diag(cw)   (-W = T_w K, bf16: W is rounded to bf16 anyway)
-//   RB_TUH, RB_TUL: T_u = diag(1/nk) T^ diag(du), bf16 hi + lo (U = T_u V, fp32 accurate)
-//   RB_A:   A' = lower(diag(nq) Q K^T * Gamma), raw q, k (the k norm is applied to V')
-//   RB_SC:  fp32 scalars of the 64 positions: sk, nk, sq; eL
-// with T^ = (I + L^)^-1, L^ = strict_lower(diag(beta nk^2) K K^T * Gamma), the
-// chunk's gate factors Gamma[i][j] = e^(gamma_i - gamma_j), cw_j = beta_j e^gamma_j nk_j^2,
-// du_j = beta_j nk_j, sk_j = e^(gamma_63 - gamma_j) nk_j, sq_i = e^gamma_i nq_i, eL = e^gamma_63.
-// (T = diag(1/nk) T^ diag(nk) is the reference's (I + L)^-1, so T_w K = W and T_u V = U.)
-constexpr int RB_TW = 0, RB_TUH = 6, RB_TUL = 12, RB_A = 18, RB_SC = 24, RB_N = 25;
-enum { S2_SK = 0, S2_NK = 1, S2_SQ = 2, S2_EL = 3 };
-__host__ __device__ constexpr int ksteps(int pb) { return pb < 2 ? 1 : 2; }
-__host__ __device__ constexpr int tfrag(int pb, int s) { return pb < 2 ? pb : 2 * pb - 2 + s; }
-
-// q rows 16p.. of a chunk as pi fragments (B operand: lane (g, r) holds row
-// 16p + r, k-step s); rows past the chunk's `len` read as zero.
-__device__ __forceinline__ void load_q_frags(bf16x8 (&qf)[4], const ChunkArgs &a, int64_t t0, int len, int hk, int p,
-                                             int lane) {
-  const int irow = 16 * p + (lane & 15), g4 = lane >> 4;
-  const uint16_t *qrow = a.q + (t0 + irow) * a.qs + (int64_t)hk * DK + 4 * g4;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    u32x2 x0 = {0u, 0u}, x1 = {0u, 0u};
-    if (irow < len) {
-      x0 = *reinterpret_cast<const u32x2 *>(qrow + 32 * s);
-      x1 = *reinterpret_cast<const u32x2 *>(qrow + 32 * s + 16);
-    }
-    qf[s] = as_bf16x8(u32x4{x0.x, x0.y, x1.x, x1.y});
-  }
-}
-
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void chunk_solve_kernel(ChunkArgs a) {
-  __shared__ __align__(16) uint16_t kn[CK * DK];  // K rows (swizzled)
-  __shared__ __align__(16) f32x4 sbuf[11 * 64 + 4 * 16 * 20 / 4];
-  f32x4 *lbuf = sbuf;            // [4 * 64] diagonal blocks of L^, row layout by lane
-  f32x4 *dxch = sbuf + 4 * 64;   // [4 * 64] diagonal blocks of T^, D layout by lane
-  f32x4 *txch = sbuf + 8 * 64;   // [3 * 64] T^[1][0], T^[2][1], T^[2][0], D layout by lane
-  float(*dtr)[16 * 20] = reinterpret_cast<float(*)[16 * 20]>(sbuf + 11 * 64);  // D -> row layout
-  __shared__ __align__(16) float gam_s[CK], beta_s[CK], nk_s[CK], cw_s[CK], du_s[CK];
-
-  const int ratio = a.Hv / a.Hk;
-  int h = blockIdx.x, jl = blockIdx.y;  // v-head; chunk index within the segment's workspace
-  if ((a.Hk * static_cast<int>(gridDim.y)) % 8 == 0) {  // the v-heads of one k-head on one XCD
-    int g, m;
-    xcd_group_order(blockIdx.x + gridDim.x * blockIdx.y, ratio, &g, &m);
-    h = (g % a.Hk) * ratio + m;
-    jl = g / a.Hk;
-  }
-  const int j = a.seg_begin + jl;  // global chunk index
-  if (j >= a.seg_end || j >= chunk_start_at(a, a.n_seqs)) return;
-  int lo = 0, hi = a.n_seqs;  // sequence owning chunk j: last n with chunk_start[n] <= j
-  if (!a.cu) {
-    lo = j / ((a.T + CK - 1) / CK);
-  } else {
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (a.chunk_start[mid] <= j) lo = mid; else hi = mid;
-    }
-  }
-  const int n = lo;
-  int64_t s0;
-  int slen;
-  seq_bounds(a, n, &s0, &slen);
-  const int c = j - chunk_start_at(a, n);
-  const int64_t t0 = s0 + static_cast<int64_t>(c) * CK;
-  const int len = min(CK, slen - c * CK);
-  if (len <= 0) return;
-  const int hk = h / ratio;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int p = tid >> 6;  // this wave's row block
-  const int g4 = lane >> 4;
-  const int r16 = lane & 15;
-  const int irow = 16 * p + r16;
-  u32x4 *rec = a.vh + (static_cast<size_t>(jl) * a.Hv + h) * (RB_N * 64);
-  float *sc = reinterpret_cast<float *>(rec + RB_SC * 64);
-
-  // ---- K rows (16 bytes per thread), q rows of this wave, the gates
-  const int seg = tid & 15;
-  u32x4 ku[4];
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int row = (tid >> 4) + 16 * it;
-    const int64_t tok = t0 + row;
-    const u32x4 z = {0u, 0u, 0u, 0u};
-    ku[it] = row < len ? *reinterpret_cast<const u32x4 *>(a.k + tok * a.ks + (int64_t)hk * DK + seg * 8) : z;
-  }
-  bf16x8 qm[4];
-  load_q_frags(qm, a, t0, len, hk, p, lane);
-  float gv = 0.f, bv = 0.f;
-  if (p == 0 && lane < len) load_gates(a.gate, t0 + lane, h, &gv, &bv);
-
-  // ---- K rows into LDS, their norms; chunk-local cumsum of g
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int row = (tid >> 4) + 16 * it;
-    *reinterpret_cast<u32x4 *>(kn + nsw(row, seg * 8)) = ku[it];
-    float sk = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t kw = ku[it][e];
-      const float k0 = bf16_bits_to_f32(kw & 0xffffu), k1 = bf16_bits_to_f32(kw >> 16);
-      sk += k0 * k0 + k1 * k1;
-    }
-    sk = row16_sum(sk);
-    if (seg == 0) nk_s[row] = a.l2norm ? rsqrtf(sk + 1e-6f) : 1.f;
-  }
-  if (p == 0) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float x = __shfl_up(gv, off, 64);
-      if (lane >= off) gv += x;
-    }
-    gam_s[lane] = gv;
-    beta_s[lane] = bv;
-  }
-  __syncthreads();
-
-  if (p == 0) {  // the per-position scalars
-    const float gl = gam_s[CK - 1], gm = gam_s[lane], nk = nk_s[lane], be = beta_s[lane];
-    cw_s[lane] = be * fast_exp(gm) * nk * nk;
-    du_s[lane] = be * nk;
-    sc[S2_SK * CK + lane] = fast_exp(gl - gm) * nk;
-    sc[S2_NK * CK + lane] = nk;
-    sc[S2_EL * CK + lane] = fast_exp(gl);
-  }
-
-  // ---- L^ blocks (p, cb), cb <= p: K_cb K_p^T on MFMA (lane holds k_j . k_i,
-  // i = 16 p + r this lane's row, j = 16 cb + 4 g + e), row layout; and the
-  // A' blocks from K_cb Q_p^T the same way
-  const float gi = gam_s[irow], nki = nk_s[irow];
-  const float li = beta_s[irow] * nki * nki;
-  float sq = 0.f;  // q row norm: this lane's 32 of the row's 128 values, the rest in lanes r + 16 g
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x = static_cast<float>(qm[s][e]);
-      sq += x * x;
-    }
-  sq += __shfl_xor(sq, 16, 64);
-  sq += __shfl_xor(sq, 32, 64);
-  const float nq = (a.l2norm ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
-  if (g4 == 0) sc[S2_SQ * CK + irow] = fast_exp(gi) * nq;
-  bf16x8 kown[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) kown[s] = frag_pi(kn, 16 * p, s, lane);
-  f32x4 lf[4], af[4];
-#pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
-    lf[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    af[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (cb <= p) {
-      f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const bf16x8 kc = frag_pi(kn, 16 * cb, s, lane);
-        kk = mfma(kc, kown[s], kk);
-        qk = mfma(kc, qm[s], qk);
-      }
-      const f32x4 gj = *reinterpret_cast<const f32x4 *>(gam_s + 16 * cb + 4 * g4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int jj = 16 * cb + 4 * g4 + e;
-        const float gf = fast_exp(gi - gj[e]);
-        lf[cb][e] = jj < irow ? li * kk[e] * gf : 0.f;
-        af[cb][e] = jj <= irow ? nq * qk[e] * gf : 0.f;
-      }
-    }
-  }
-
-  // ---- T^ = (I + L^)^-1: diagonal blocks by substitution (each lane one
-  // column, rows of L^ broadcast from LDS), then the blocks below the
-  // diagonal on fp32 MFMA: T^[p][b] = -T^[p][p] sum_{b <= kb < p} L^[p][kb] T^[kb][b]
-  f32x4 dl, drow;  // T^[p][p] in D layout and row layout
-  {
-    f32x4 *lb = lbuf + p * 64;
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
-      if (cb == p) lb[lane] = lf[cb];
-    __builtin_amdgcn_wave_barrier();
-    float x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float acc = i == r16 ? 1.f : 0.f;
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4)
-        if (4 * q4 < i) {
-          const f32x4 lrow = lb[i + 16 * q4];  // L^[i][4 q4 .. 4 q4 + 3]
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (4 * q4 + e < i) acc -= lrow[e] * x[4 * q4 + e];
-        }
-      x[i] = acc;
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      dl[e] = g4 == 0 ? x[e] : g4 == 1 ? x[4 + e] : g4 == 2 ? x[8 + e] : x[12 + e];
-    dxch[p * 64 + lane] = dl;
-    float *tr = dtr[p];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) tr[(4 * g4 + e) * 20 + r16] = dl[e];
-    __builtin_amdgcn_wave_barrier();
-    drow = *reinterpret_cast<const f32x4 *>(tr + r16 * 20 + 4 * g4);
-  }
-  __syncthreads();
-  f32x4 trow[4];  // T^[p][b], row layout
-  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int b = 0; b < 4; ++b) trow[b] = b == p ? drow : z4;
-#pragma unroll
-  for (int b = 0; b < 3; ++b)
-    if (b == p - 1) {
-      const f32x4 x = mm16(lf[b], dxch[b * 64 + lane], z4);
-      trow[b] = -mm16(x, drow, z4);
-      if (b <= 1) txch[b * 64 + lane] = -mm16(drow, x, z4);  // T^[1][0], T^[2][1]
-    }
-  __syncthreads();
-#pragma unroll
-  for (int b = 0; b < 2; ++b)
-    if (b == p - 2) {
-      f32x4 x = mm16(lf[b], dxch[b * 64 + lane], z4);
-      x = mm16(lf[b + 1], txch[b * 64 + lane], x);
-      trow[b] = -mm16(x, drow, z4);
-      if (b == 0) txch[2 * 64 + lane] = -mm16(drow, x, z4);  // T^[2][0]
-    }
-  __syncthreads();
-  if (p == 3) {
-    f32x4 x = mm16(lf[0], dxch[lane], z4);
-    x = mm16(lf[1], txch[lane], x);
-    x = mm16(lf[2], txch[2 * 64 + lane], x);
-    trow[0] = -mm16(x, drow, z4);
-  }
-
-  // ---- the fragments of row block p: T_w, T_u (hi, lo), A'
-  const float rnk = 1.f / nki;
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    if (s < ksteps(p)) {
-      const int f = tfrag(p, s);
-      const f32x4 t0 = trow[2 * s] * rnk, t1 = trow[2 * s + 1] * rnk;
-      const f32x4 c0 = *reinterpret_cast<const f32x4 *>(cw_s + 32 * s + 4 * g4);
-      const f32x4 c1 = *reinterpret_cast<const f32x4 *>(cw_s + 32 * s + 16 + 4 * g4);
-      const f32x4 d0 = *reinterpret_cast<const f32x4 *>(du_s + 32 * s + 4 * g4);
-      const f32x4 d1 = *reinterpret_cast<const f32x4 *>(du_s + 32 * s + 16 + 4 * g4);
-      rec[(RB_TW + f) * 64 + lane] = __builtin_bit_cast(u32x4, pack_hi(-(t0 * c0), -(t1 * c1)));
-      bf16x8 uh, ul;
-      pack_hilo(t0 * d0, t1 * d1, uh, ul);
-      rec[(RB_TUH + f) * 64 + lane] = __builtin_bit_cast(u32x4, uh);
-      rec[(RB_TUL + f) * 64 + lane] = __builtin_bit_cast(u32x4, ul);
-      rec[(RB_A + f) * 64 + lane] = __builtin_bit_cast(u32x4, pack_hi(af[2 * s], af[2 * s + 1]));
-    }
-  }
 }
 
 // ------------------------------------------------------------------ phase B
@@ -1527,540 +1257,6 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_persist_kernel(Chu
   }
 }
 
-// ------------------------------------------------------------------ fused scan
-// One workgroup per (sequence, v-head, 16 state columns): four compute waves
-// and one loader wave.  Compute wave p owns chunk positions 16p..16p+15 and
-// state rows 32p..32p+31, as in chunk_scan_kernel, and runs the state chain
-// of chunk c while it builds, in registers, the operands of chunk c + 1 for
-// its own rows from the raw inputs and the solve record:
-//   A'[i][j] = nq_i q_i . k_j e^(gamma_i - gamma_j)  (j <= i; q.k on MFMA)
-//   W[i]     = nk_i^-1 sum_j T^[i][j] cw_j k_j        (MFMA, T^ split hi + lo)
-//   U[i]     = nk_i^-1 sum_j T^[i][j] du_j v_j         (this tile's 16 columns)
-// (the chunk algorithm of engine/kernels/delta_rule.py:295-349 with
-// T = D^-1 T^ D, see chunk_solve_kernel; the column norm of A is carried by
-// V' instead: O = (e^gamma Q~) S + A' (nk * V')).  Waves 0 and 1 also
-// compute the second half of W's columns for row blocks 2 and 3 (handed over
-// through LDS), so that the four waves do about the same MFMA work.
-// Each chunk's raw K rows (swizzled for the transposing reads), V slice and
-// solve record reach a triple-buffered LDS stage by buffer_load ... lds, the
-// copies split over the four waves and issued two chunks ahead; q rows go
-// straight into the waves' registers two chunks ahead.  No operand of the
-// chain goes through HBM.  One wave per SIMD, so each can hold the two
-// chunks' operand sets (about 400 registers with the accumulation registers).
-//
-// Copy ordering: in every chunk period a wave issues, last of all its vector
-// memory operations, its copies for chunk c + 3 (the buffer chunk c held,
-// read during period c - 1).  Before barrier 1 of chunk c + 1 -- after which
-// chunk c + 2's operands are read -- the wave's most recent vector memory
-// operations are its copies for chunk c + 3 (none are issued in between), so
-// waiting until at most that many remain (vector memory operations complete
-// in order) means everything before them, chunk c + 2's copies included, has
-// landed.
-// ------------------------------------------------------------- fused scan
-// Workgroup = 8 waves for one (sequence, v-head, 16 state columns), serial
-// over the sequence's chunks, reading only q, k, v and the solve records:
-//
-// * chain waves p = 0..3 run the state recurrence alone.  Wave p owns chunk
-//   positions 16p..16p+15 (its rows of V') and state rows 32p..32p+31 (its
-//   accumulators hold them for the whole sequence).  Per chunk:
-//     R1  V' = U - W S (4 MFMAs on -W and U from the hand-over buffer, S from
-//         LDS as bf16); V'' = diag(sk) V' (bf16 hi + lo) and nk V' to LDS;
-//     barrier B1;
-//     R2  S = eL S + K^T V'' (8 MFMAs, K^T read transposed from the stage);
-//         the new state (bf16) to LDS;  barrier B2.
-// * side waves p = 0..3 do everything else, one chunk ahead of the chain:
-//     before B1: Q S for chunk c (4 MFMAs, Q in registers), and the -W
-//       fragments of chunk c + 1 for k-step p of every row block (12 MFMAs,
-//       K^T and T_w from the stage);
-//     after B1: the output rows 16p.. of chunk c = diag(sq) Q S + A' (nk V')
-//       (A' in registers), U rows of chunk c + 1 (T_u hi + lo in registers,
-//       V from the stage), their share of chunk c + 2's stage (loaded into
-//       registers one period earlier) written to LDS, then the loads for
-//       later chunks: their stage share of c + 3, q and A' of c + 2, T_u of c + 3.
-// Every wave runs the same barriers (two per chunk), and every period of a
-// side wave issues the same loads (past the last chunk they repeat the last
-// chunk's and go unused), so that the compiler's wait counts for them are
-// exact: each load has one to two chunk periods to land.
-constexpr int F2_NST = 3;                                               // stage buffers
-constexpr int ST_K = 0, ST_V = 16, ST_SC = 18, ST_TW = 19, ST_N = 25;  // stage blocks (1 KiB) per chunk
-constexpr int HD_W = 0, HD_U = 16, HD_N = 20;                           // hand-over blocks: -W [pb][s], U [pb]
-// side wave w's share of a chunk's stage: blocks [st_lo(w), st_lo(w + 1)) of
-// 0..15 K rows 4d..4d+3, 16..17 V rows, 18 scalars, 19..24 T_w fragments
-__host__ __device__ constexpr int st_lo(int w) { return w == 0 ? 0 : w == 1 ? 7 : w == 2 ? 13 : w == 3 ? 19 : 25; }
-constexpr int ST_SHARE = 7;  // the largest share
-// T_u fragments loaded by side wave w (its U row blocks): wave 0 row block 3,
-// wave 1 row block 2, wave 2 row blocks 1 and 0, wave 3 none
-__host__ __device__ constexpr int tu_count(int w) { return w < 3 ? 4 : 0; }
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t brsrc_of(const void *base, int64_t bytes) {
-  const int n = bytes <= 0 ? 0 : bytes >= 0x7fffffff ? 0x7fffffff : static_cast<int>(bytes);
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, n, BUF_DWORD3);
-}
-__device__ __forceinline__ u32x2 vload8(__amdgpu_buffer_rsrc_t rsrc, int voff) {
-  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rsrc, voff, 0, 0));
-}
-__device__ __forceinline__ u32x4 vload16(__amdgpu_buffer_rsrc_t rsrc, int voff, int soff) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, soff, 0));
-}
-
-// L2 warm-up: 4 bytes per lane from global memory into an LDS pad that
-// nothing reads (buffer_load_dword ... lds).  Inline asm, so the compiler
-// neither waits for it nor counts it; it writes no register, so nothing the
-// compiler tracks can be overwritten when its data returns.  Only the chain
-// waves issue it (they wait for no global load inside the loop) and they
-// drain it with s_waitcnt vmcnt(0) before they finish.
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ i32x4_t touch_rsrc(const void *base, int64_t bytes) {
-  const uint64_t pp = reinterpret_cast<uint64_t>(base);
-  const int n = bytes <= 0 ? 0 : bytes >= 0x7fffffff ? 0x7fffffff : static_cast<int>(bytes);
-  return i32x4_t{__builtin_amdgcn_readfirstlane(static_cast<int>(pp & 0xffffffffu)),
-                 __builtin_amdgcn_readfirstlane(static_cast<int>((pp >> 32) & 0xffff)),
-                 __builtin_amdgcn_readfirstlane(n), BUF_DWORD3};
-}
-__device__ __forceinline__ void touch4(const i32x4_t &rsrc, const void *pad, int voff) {
-  asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc),
-               "{m0}"(static_cast<uint32_t>(
-                   reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char *)pad))));
-}
-constexpr int F2_AHEAD = 4;  // chunks between a warm-up read and the first load of the same data
-
-// V slice [64 rows][16 columns] bf16, rows of 32 bytes: pi fragment of V over
-// the positions of k-step s (as the B operand: B[k][n] = V[pos k][col n]).
-__device__ __forceinline__ bf16x8 frag_tr_v(const uint16_t *tile, int s, int lane) {
-  const int L = lane & 15, g4 = lane >> 4;
-  auto rd = [&](int j0) {
-    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_s16x4 *)(const_cast<uint16_t *>(tile) + (j0 + (L >> 2)) * 16 + 4 * (L & 3)));
-  };
-  const s16x4 lo = rd(32 * s + 4 * g4), hi = rd(32 * s + 16 + 4 * g4);
-  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-}
-
-// "c8" order of the k dimension in the fused scan: lane group g of an MFMA
-// operand over k-step s holds k indices 32 s + 8 g + 0..7 (contiguous, so
-// that a q row fragment is one 16-byte load).  A state tile t of a 32-row
-// block at c0 holds rows c0 + 8 (m / 4) + 4 t + m % 4 (m its D row), and two
-// tiles t = 0, 1 pack into one c8 operand.  The fragment of X^T whose 16 rows
-// are those columns of X (k-step s over the rows of X), read transposed:
-__device__ __forceinline__ bf16x8 frag_tr_c8(const uint16_t *tile, int s, int c0, int lane) {
-  const int L = lane & 15, g4 = lane >> 4;
-  auto rd = [&](int j0) {
-    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_s16x4 *)(const_cast<uint16_t *>(tile) + nsw(j0 + (L >> 2), c0 + 8 * (L & 3))));
-  };
-  const s16x4 lo = rd(32 * s + 4 * g4), hi = rd(32 * s + 16 + 4 * g4);
-  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-}
-
-// Per-workgroup constants of the fused scan.
-struct F2Ctx {
-  int n, h, hk, ct, nch, c0, ratio;
-  int64_t tok0, rem;  // first token of the first chunk; tokens from there to the sequence end
-  __device__ int64_t t0(int c) const { return tok0 + static_cast<int64_t>(c) * CK; }
-  __device__ int len(int c) const { return static_cast<int>(min<int64_t>(CK, rem - static_cast<int64_t>(c) * CK)); }
-  __device__ const u32x4 *rec(const ChunkArgs &a, int c) const {
-    return a.vh + (static_cast<size_t>(c0 + c) * a.Hv + h) * (RB_N * 64);
-  }
-};
-
-struct F2Lds {
-  u32x4 (*stage)[ST_N * 64];
-  u32x4 (*hand)[HD_N * 64];
-  u32x4 (*xs)[64];            // state rows by k-step (bf16), lane order
-  u32x2 (*xv)[2][64][2];      // nk V', V'' hi, V'' lo by k-step, lane, half
-  uint32_t (*pad)[64];        // landing pad of the warm-up reads, per chain wave
-};
-
-// Chain wave p's warm-up of chunk c: p = 0 this workgroup's eighth of the
-// chunk's solve record, p = 1 / 2 its share of the chunk's k / q lines (read
-// by the 8 Hv / Hk workgroups of one k-head), p = 3 the v lines it is the
-// first of four column tiles to read.  Lines past the sequence end read as
-// zero (range-checked offsets).
-__device__ __forceinline__ void f2_touch(const ChunkArgs &a, const F2Ctx &x, const F2Lds &L, int p, int lane, int c) {
-  const int len = x.len(c);
-  if (p == 0) {
-    if (lane < RB_N) touch4(touch_rsrc(x.rec(a, c), RB_N * 1024), L.pad[0], (RB_N * x.ct + lane) * 128);
-  } else if (p <= 2) {
-    const int per = max(1, 128 / (8 * x.ratio));  // 128-byte lines of the chunk's rows per workgroup
-    const int m = (x.h % x.ratio) * 8 + x.ct;
-    const int64_t stride = p == 1 ? a.ks : a.qs;
-    const uint16_t *base = (p == 1 ? a.k : a.q) + x.t0(c) * stride + (int64_t)x.hk * DK;
-    const int li = (m * per + lane) & 127;  // row li / 2, half li % 2
-    if (lane < per)
-      touch4(touch_rsrc(base, (len - 1) * stride * 2 + DK * 2), L.pad[p],
-             static_cast<int>((li >> 1) * stride * 2) + 128 * (li & 1));
-  } else if (lane < 16) {
-    const uint16_t *base = a.v + x.t0(c) * a.vs + (int64_t)x.h * DV + 16 * x.ct;
-    touch4(touch_rsrc(base, (len - 1) * a.vs * 2 + 32), L.pad[3],
-           static_cast<int>((4 * lane + (x.ct & 3)) * a.vs * 2));
-  }
-}
-
-template <bool BF16_OUT>
-__device__ __forceinline__ void f2_chain(const ChunkArgs &a, const F2Ctx &x, const F2Lds &L, int p, int lane,
-                                         const float *src, float *dst) {
-  const int g4 = lane >> 4, row0 = 32 * p, col = 16 * x.ct + (lane & 15);
-  (void)col;
-  f32x4 S[2];  // state rows row0 + 8g + 4t + e of this lane's column (c8 order)
-  if (src) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) S[t][e] = src[(row0 + 8 * g4 + 4 * t + e) * DV];
-  } else {
-#pragma unroll
-    for (int t = 0; t < 2; ++t) S[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  L.xs[p][lane] = __builtin_bit_cast(u32x4, pack_hi(S[0], S[1]));
-  for (int c = 2; c < 2 + F2_AHEAD && c < x.nch; ++c) f2_touch(a, x, L, p, lane, c);
-  lds_barrier();  // prologue 1: initial state in LDS
-  lds_barrier();  // prologue 2: the hand-over of chunk 0
-  for (int c = 0; c < x.nch; ++c) {
-    const u32x4 *st = L.stage[c % F2_NST];
-    const u32x4 *hd = L.hand[c & 1];
-    const uint16_t *kn = reinterpret_cast<const uint16_t *>(st + ST_K * 64);
-    const float *scf = reinterpret_cast<const float *>(st + ST_SC * 64);
-    bf16x8 sb[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) sb[s] = __builtin_bit_cast(bf16x8, L.xs[s][lane]);
-    // ---- R1: V' = U - W S
-    f32x4 vp = __builtin_bit_cast(f32x4, hd[(HD_U + p) * 64 + lane]);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) vp = mfma(as_bf16x8(hd[(HD_W + 4 * p + s) * 64 + lane]), sb[s], vp);
-    bf16x8 kt[4];  // K^T of state tile t (c8 rows of block row0), k-step s: [2t + s]
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) kt[2 * t + s] = frag_tr_c8(kn, s, row0 + 4 * t, lane);
-    const f32x4 sk = *reinterpret_cast<const f32x4 *>(scf + S2_SK * CK + 16 * p + 4 * g4);
-    const f32x4 nk = *reinterpret_cast<const f32x4 *>(scf + S2_NK * CK + 16 * p + 4 * g4);
-    const float eL = scf[S2_EL * CK];
-    {
-      const f32x4 v2 = vp * sk;
-      f32x4 hf;
-      bf16x4 hb, lb;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        hb[i] = static_cast<__bf16>(v2[i]);
-        hf[i] = static_cast<float>(hb[i]);
-        lb[i] = static_cast<__bf16>(v2[i] - hf[i]);
-      }
-      L.xv[0][p >> 1][lane][p & 1] = pack4(vp * nk);
-      L.xv[1][p >> 1][lane][p & 1] = __builtin_bit_cast(u32x2, hb);
-      L.xv[2][p >> 1][lane][p & 1] = __builtin_bit_cast(u32x2, lb);
-    }
-#pragma unroll
-    for (int t = 0; t < 2; ++t) S[t] = S[t] * eL;
-    if (c + 2 + F2_AHEAD < x.nch) f2_touch(a, x, L, p, lane, c + 2 + F2_AHEAD);
-    lds_barrier();  // B1
-    // ---- R2: S += K^T V''
-    bf16x8 vh[2], vl[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      vh[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(&L.xv[1][s][lane][0]));
-      vl[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(&L.xv[2][s][lane][0]));
-    }
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t) S[t] = mfma(kt[2 * t + s], vh[s], S[t]);
-#pragma unroll
-      for (int t = 0; t < 2; ++t) S[t] = mfma(kt[2 * t + s], vl[s], S[t]);
-    }
-    L.xs[p][lane] = __builtin_bit_cast(u32x4, pack_hi(S[0], S[1]));
-    lds_barrier();  // B2
-  }
-  if (dst) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) dst[(row0 + 8 * g4 + 4 * t + e) * DV] = S[t][e];
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the warm-up reads
-}
-
-struct F2Q {        // one chunk's operands of a side wave's output rows
-  bf16x8 qm[4];     // q rows 16p.., k-steps 0..3 in c8 order (B operand of Q S)
-  u32x4 am[2];      // A' rows 16p.., k-steps 0, 1
-};
-struct F2T {        // one chunk's T_u fragments of a side wave's U row blocks
-  u32x4 tu[4];
-};
-
-// the T_u fragments side wave W loads: [i] = (row block, k-step, hi / lo)
-template <int W> __device__ __forceinline__ constexpr int tu_pb(int i) { return W == 0 ? 3 : W == 1 ? 2 : (i < 2 ? 1 : 0); }
-template <int W> __device__ __forceinline__ constexpr int tu_s(int i) { return W < 2 ? (i >> 1) : 0; }
-
-// Side wave of role ROW (W = its output row block: Q S, the output, q and A'
-// loads) or COL (W = its k-step of -W, its U row blocks, its share of the
-// stage copies and the T_u loads).
-enum { F2_ROW = 0, F2_COL = 1 };
-template <int W, int ROLE, bool BF16_OUT>
-__device__ __forceinline__ void f2_side(const ChunkArgs &a, const F2Ctx &x, const F2Lds &L, int lane) {
-  constexpr int P = W;  // output row block
-  constexpr int NA = ksteps(P);
-  const int g4 = lane >> 4, r16 = lane & 15, rl = lane >> 4, ps = lane & 15;
-  const int ks2 = static_cast<int>(a.ks * 2), vs2 = static_cast<int>(a.vs * 2);
-  // K row load offsets, by d % 4 (row 4d + rl; LDS segment ps holds logical segment ps ^ (row & 15))
-  int koff[4];
-#pragma unroll
-  for (int m = 0; m < 4; ++m) koff[m] = rl * ks2 + 16 * (ps ^ ((4 * m + rl) & 15));
-  const int qoff = static_cast<int>((16 * P + r16) * a.qs * 2) + 16 * g4;
-
-  // this wave's share of chunk c's stage, loaded into registers, later written to LDS
-  auto load_stage = [&](u32x4 (&sg)[ST_SHARE], int c) {
-    const int len = x.len(c);
-    const auto rk = brsrc_of(a.k + x.t0(c) * a.ks + (int64_t)x.hk * DK, (len - 1) * a.ks * 2 + DK * 2);
-    const auto rv = brsrc_of(a.v + x.t0(c) * a.vs + (int64_t)x.h * DV + 16 * x.ct, (len - 1) * a.vs * 2 + 32);
-    const auto rr = brsrc_of(x.rec(a, c), RB_N * 1024);
-#pragma unroll
-    for (int d = st_lo(W); d < st_lo(W + 1); ++d) {
-      u32x4 &r = sg[d - st_lo(W)];
-      if (d < 16)  // (the whole row offset in the range-checked vector offset: rows past the end read zero)
-        r = vload16(rk, koff[d & 3] + 4 * d * ks2, 0);
-      else if (d < 18)
-        r = vload16(rv, (32 * (d - 16) + (lane >> 1)) * vs2 + 16 * (lane & 1), 0);
-      else if (d == 18)
-        r = vload16(rr, lane * 16, RB_SC * 1024);
-      else
-        r = vload16(rr, lane * 16, (RB_TW + d - 19) * 1024);
-    }
-  };
-  auto write_stage = [&](const u32x4 (&sg)[ST_SHARE], int c) {
-    u32x4 *st = L.stage[c % F2_NST];
-#pragma unroll
-    for (int d = st_lo(W); d < st_lo(W + 1); ++d) st[d * 64 + lane] = sg[d - st_lo(W)];
-  };
-  auto load_q = [&](F2Q &qa, int c) {
-    const auto rq = brsrc_of(a.q + x.t0(c) * a.qs + (int64_t)x.hk * DK, (x.len(c) - 1) * a.qs * 2 + DK * 2);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) qa.qm[s] = as_bf16x8(vload16(rq, qoff + 64 * s, 0));
-  };
-  auto load_am = [&](F2Q &qa, int c) {
-    const auto rr = brsrc_of(x.rec(a, c), RB_N * 1024);
-#pragma unroll
-    for (int s = 0; s < NA; ++s) qa.am[s] = vload16(rr, lane * 16, (RB_A + tfrag(P, s)) * 1024);
-  };
-  auto load_tu = [&](F2T &tu, int c) {
-    const auto rr = brsrc_of(x.rec(a, c), RB_N * 1024);
-#pragma unroll
-    for (int i = 0; i < tu_count(W); ++i)
-      tu.tu[i] = vload16(rr, lane * 16, ((i & 1 ? RB_TUL : RB_TUH) + tfrag(tu_pb<W>(i), tu_s<W>(i))) * 1024);
-  };
-  // -W fragments of chunk c for k-step W of row blocks [pb0, pb1), from the stage
-  auto w_units = [&](int c, int pb0, int pb1) {
-    const u32x4 *st = L.stage[c % F2_NST];
-    u32x4 *hd = L.hand[c & 1];
-    const uint16_t *kn = reinterpret_cast<const uint16_t *>(st + ST_K * 64);
-    bf16x8 kf[2][2];  // K^T of the c8 state tiles t of k-step W, k-steps (positions) 0, 1
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) kf[t][s] = frag_tr_c8(kn, s, 32 * W + 4 * t, lane);
-#pragma unroll
-    for (int pb = 0; pb < 4; ++pb) {
-      if (pb < pb0 || pb >= pb1) continue;
-      f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < ksteps(pb); ++s) {
-        const bf16x8 tw = as_bf16x8(st[(ST_TW + tfrag(pb, s)) * 64 + lane]);
-        d0 = mfma(kf[0][s], tw, d0);
-        d1 = mfma(kf[1][s], tw, d1);
-      }
-      hd[(HD_W + 4 * pb + W) * 64 + lane] = __builtin_bit_cast(u32x4, pack_hi(d0, d1));
-    }
-  };
-  // U rows of chunk c for this wave's row blocks (T_u hi + lo on V)
-  auto u_units = [&](const F2T &tu, int c) {
-    const u32x4 *st = L.stage[c % F2_NST];
-    u32x4 *hd = L.hand[c & 1];
-    const uint16_t *vt = reinterpret_cast<const uint16_t *>(st + ST_V * 64);
-    if constexpr (W < 2) {  // one row block with two k-steps
-      f32x4 ut = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const bf16x8 vf = frag_tr_v(vt, s, lane);
-        ut = mfma(as_bf16x8(tu.tu[2 * s]), vf, ut);
-        ut = mfma(as_bf16x8(tu.tu[2 * s + 1]), vf, ut);
-      }
-      hd[(HD_U + tu_pb<W>(0)) * 64 + lane] = __builtin_bit_cast(u32x4, ut);
-    } else if constexpr (W == 2) {  // row blocks 1 and 0, one k-step each
-      const bf16x8 vf = frag_tr_v(vt, 0, lane);
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        f32x4 ut = {0.f, 0.f, 0.f, 0.f};
-        ut = mfma(as_bf16x8(tu.tu[2 * b]), vf, ut);
-        ut = mfma(as_bf16x8(tu.tu[2 * b + 1]), vf, ut);
-        hd[(HD_U + tu_pb<W>(2 * b)) * 64 + lane] = __builtin_bit_cast(u32x4, ut);
-      }
-    }
-  };
-
-  typedef typename std::conditional<BF16_OUT, uint16_t, float>::type OT;
-  const int64_t ostep = static_cast<int64_t>(a.Hv) * DV;  // elements per token
-  const int voff = static_cast<int>(((16 * P + r16) * ostep + x.h * DV + 16 * x.ct + 4 * g4) * sizeof(OT));
-  auto store_out = [&](const f32x4 &o, int c) {
-    OT *base = static_cast<OT *>(a.o) + x.t0(c) * ostep;
-    const auto r = __builtin_amdgcn_make_buffer_rsrc(base, 0, static_cast<int>(x.len(c) * ostep * sizeof(OT)),
-                                                     BUF_DWORD3);
-    if constexpr (BF16_OUT)
-      __builtin_amdgcn_raw_buffer_store_b64(pack4(o), r, voff, 0, 0);
-    else
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), r, voff, 0, 0);
-  };
-
-  F2Q qa0, qa1;
-  F2T tu0, tu1;
-  u32x4 sg[ST_SHARE];
-  const int last = x.nch - 1;
-  // ---- prologue: stages 0, 1, T_u of chunks 0, 1, q / A' of chunk 0; then
-  // the hand-over of chunk 0 and the loads of "period -1"
-  if constexpr (ROLE == F2_COL) {
-    load_stage(sg, 0);
-    write_stage(sg, 0);
-    load_stage(sg, min(1, last));
-    write_stage(sg, 1);
-    load_tu(tu0, 0);
-    load_tu(tu1, min(1, last));
-    load_stage(sg, min(2, last));
-  } else {
-    load_q(qa0, 0);
-    load_am(qa0, 0);
-    load_q(qa1, min(1, last));
-  }
-  lds_barrier();  // prologue 1: chunks 0, 1 staged; initial state in LDS
-  if constexpr (ROLE == F2_COL) {
-    w_units(0, 0, 4);
-    u_units(tu0, 0);
-    load_tu(tu0, min(2, last));
-  } else {
-    load_am(qa1, min(1, last));
-  }
-  lds_barrier();  // prologue 2: the hand-over of chunk 0
-
-  auto period = [&](int c, F2Q &qa, F2T &tu) {
-    // qa: q / A' of chunk c; tu: T_u of chunk c + 1; sg: stage share of c + 2
-    if constexpr (ROLE == F2_COL) {
-      // stage c + 2 goes to the buffer chunk c - 1 used (its last readers passed B2 of chunk c - 1)
-      write_stage(sg, c + 2);
-      load_stage(sg, min(c + 3, last));
-      if (c + 1 < x.nch) w_units(c + 1, 2, 4);
-      lds_barrier();  // B1
-      if (c + 1 < x.nch) {
-        w_units(c + 1, 0, 2);
-        u_units(tu, c + 1);
-      }
-      load_tu(tu, min(c + 3, last));
-      lds_barrier();  // B2
-    } else {
-      const float *scf = reinterpret_cast<const float *>(L.stage[c % F2_NST] + ST_SC * 64);
-      bf16x8 sb[4];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) sb[s] = __builtin_bit_cast(bf16x8, L.xs[s][lane]);
-      const float sq = scf[S2_SQ * CK + 16 * P + r16];
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) acc = mfma(sb[s], qa.qm[s], acc);
-      load_q(qa, min(c + 2, last));
-      lds_barrier();  // B1
-      f32x4 o = acc * sq;
-#pragma unroll
-      for (int s = 0; s < NA; ++s)
-        o = mfma(__builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(&L.xv[0][s][lane][0])),
-                 as_bf16x8(qa.am[s]), o);
-      store_out(o, c);
-      load_am(qa, min(c + 2, last));
-      lds_barrier();  // B2
-    }
-  };
-  for (int c = 0; c < x.nch; c += 2) {
-    period(c, qa0, tu1);
-    if (c + 1 >= x.nch) break;
-    period(c + 1, qa1, tu0);
-  }
-}
-
-template <bool BF16_OUT>
-__global__ __launch_bounds__(768) void chunk_fused_kernel(ChunkArgs a) {
-  __shared__ u32x4 stage[F2_NST][ST_N * 64];  // 75 KiB
-  __shared__ u32x4 hand[2][HD_N * 64];        // 40 KiB
-  __shared__ u32x4 xs[4][64];
-  __shared__ u32x2 xv[3][2][64][2];
-  __shared__ uint32_t pad[4][64];
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  F2Ctx x;
-  const int nh = a.n_seqs * a.Hv;
-  x.ratio = a.Hv / a.Hk;
-  int ct = blockIdx.x / nh;    // plain order: the column tiles of one head share bid % 8,
-  int rest = blockIdx.x % nh;  // i.e. one XCD and its L2
-  if ((a.n_seqs * a.Hk) % 8 == 0) {  // also the v-heads of one k-head
-    int g, m;
-    xcd_group_order(blockIdx.x, x.ratio * (DV / SCAN_COLS), &g, &m);
-    ct = m % (DV / SCAN_COLS);
-    rest = (g / a.Hk) * a.Hv + (g % a.Hk) * x.ratio + m / (DV / SCAN_COLS);
-  }
-  x.n = rest / a.Hv;
-  x.h = rest % a.Hv;
-  x.hk = x.h / x.ratio;
-  x.ct = ct;
-  const int g4 = lane >> 4;
-  const int col = 16 * ct + (lane & 15);
-
-  int64_t s0;
-  int slen;
-  seq_bounds(a, x.n, &s0, &slen);
-  s0 = uniform64(s0);
-  slen = __builtin_amdgcn_readfirstlane(slen);
-  const int cs = __builtin_amdgcn_readfirstlane(chunk_start_at(a, x.n));
-  const int ce = __builtin_amdgcn_readfirstlane(max(cs, min(chunk_start_at(a, x.n + 1), a.max_chunks)));
-  const int lo = max(cs, a.seg_begin), hi = min(ce, a.seg_end);
-  const int64_t in_row = a.h0 ? uniform64(pool_row_first(a.h0_idx, x.n, a.h0_rows)) : -1;
-  const int64_t out_row = a.hT ? uniform64(pool_row_first(a.hT_idx, x.n, a.hT_rows)) : -1;
-  const int64_t kv = static_cast<int64_t>(DK) * DV;
-  if (cs == ce) {  // empty sequence: the final state is the initial one (handled once)
-    if (wave < 4 && a.seg_begin == 0 && out_row >= 0) {
-      float *dst = a.hT + (out_row * a.Hv + x.h) * kv + col;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 32 * wave + 16 * t + 4 * g4 + e;
-          dst[r * DV] = in_row >= 0 ? a.h0[(in_row * a.Hv + x.h) * kv + r * DV + col] : 0.f;
-        }
-    }
-    return;
-  }
-  if (lo >= hi) return;  // no chunk of this sequence in this segment
-  x.nch = hi - lo;
-  x.c0 = lo - a.seg_begin;  // first chunk, workspace-local
-  const int64_t seq_off = static_cast<int64_t>(lo - cs) * CK;
-  x.tok0 = s0 + seq_off;
-  x.rem = slen - seq_off;
-  const F2Lds L{stage, hand, xs, xv, pad};
-
-  if (wave < 4) {
-    float *carry = a.carry + (static_cast<int64_t>(x.n) * a.Hv + x.h) * kv + col;
-    const float *src = lo == cs ? (in_row >= 0 ? a.h0 + (in_row * a.Hv + x.h) * kv + col : nullptr) : carry;
-    float *dst = hi == ce ? (out_row >= 0 ? a.hT + (out_row * a.Hv + x.h) * kv + col : nullptr) : carry;
-    f2_chain<BF16_OUT>(a, x, L, wave, lane, src, dst);
-  } else if (wave < 8) {
-    switch (wave) {
-      case 4: f2_side<0, F2_ROW, BF16_OUT>(a, x, L, lane); break;
-      case 5: f2_side<1, F2_ROW, BF16_OUT>(a, x, L, lane); break;
-      case 6: f2_side<2, F2_ROW, BF16_OUT>(a, x, L, lane); break;
-      default: f2_side<3, F2_ROW, BF16_OUT>(a, x, L, lane); break;
-    }
-  } else {
-    switch (wave) {
-      case 8: f2_side<0, F2_COL, BF16_OUT>(a, x, L, lane); break;
-      case 9: f2_side<1, F2_COL, BF16_OUT>(a, x, L, lane); break;
-      case 10: f2_side<2, F2_COL, BF16_OUT>(a, x, L, lane); break;
-      default: f2_side<3, F2_COL, BF16_OUT>(a, x, L, lane); break;
-    }
-  }
-}
-
 // Chunks per prep + scan segment: one prep launch produces a segment's
 // operands (about 2.3 MiB per chunk at 32 v-heads: 146 MiB for 64 chunks,
 // which stay in the 256 MB Infinity Cache until the scan reads them) and one
@@ -2101,37 +1297,6 @@ WsLayout ws_layout(int n_seqs, int64_t seg_chunks, int Hv, bool multi) {
   return l;
 }
 
-// Workspace of the solve + fused scan path: the chunk table, the carried
-// state (several segments), and one solve record (RB_N = 25 KiB) per (chunk,
-// v-head) of a segment of up to SEG_FUSED chunks (200 MiB at 32 v-heads;
-// they are read back right after they are written).
-constexpr int SEG_FUSED = 256;
-
-WsLayout ws_layout_fused(int n_seqs, int64_t seg_chunks, int Hv, bool multi) {
-  WsLayout l;
-  size_t off = 0;
-  l.chunk_start = off;
-  off = align256(off + sizeof(int32_t) * (n_seqs + 2));
-  l.seqrec = off;
-  off = align256(off + sizeof(int64_t) * SEQREC * static_cast<size_t>(n_seqs));
-  l.carry = off;
-  if (multi) off = align256(off + sizeof(float) * static_cast<size_t>(n_seqs) * Hv * DK * DV);
-  l.vh = off;
-  off = align256(off + 1024ull * RB_N * seg_chunks * Hv);
-  l.Ut = off;
-  l.dup = off;
-  l.total = off;
-  return l;
-}
-
-bool fused_path_enabled() {
-  static const bool on = [] {
-    const char *e = std::getenv("GDN_CHUNK_FUSED");
-    return e && e[0] == '1';
-  }();
-  return on;
-}
-
 int64_t max_chunks_of(int n_seqs, int64_t total_tokens, bool varlen, int T) {
   if (!varlen) return static_cast<int64_t>(n_seqs) * ((T + CK - 1) / CK);
   return (total_tokens + CK - 1) / CK + n_seqs;
@@ -2144,12 +1309,9 @@ extern "C" size_t gdn_chunk_workspace_bytes(int32_t n_seqs, int64_t total_tokens
                                             int32_t V) {
   using namespace gdn;
   if (n_seqs <= 0 || total_tokens < 0 || Hv <= 0 || K != DK || V != DV) return 0;
-  // Upper bound valid with or without cu_seqlens and for either kernel path;
-  // k-head blocks counted at Hk = Hv.
+  // Upper bound valid with or without cu_seqlens.
   const int64_t nc = (total_tokens + CK - 1) / CK + n_seqs;
-  const size_t old_path = ws_layout(n_seqs, std::min<int64_t>(nc, SEG_CHUNKS), Hv, nc > SEG_CHUNKS).total;
-  const size_t fused = ws_layout_fused(n_seqs, std::min<int64_t>(nc, SEG_FUSED), Hv, nc > SEG_FUSED).total;
-  return std::max(old_path, fused);
+  return ws_layout(n_seqs, std::min<int64_t>(nc, SEG_CHUNKS), Hv, nc > SEG_CHUNKS).total;
 }
 
 namespace gdn {
@@ -2184,15 +1346,10 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
   const int64_t total = cu_seqlens ? static_cast<int64_t>(T) : static_cast<int64_t>(n_seqs) * T;
   const int64_t nc = max_chunks_of(n_seqs, total, cu_seqlens != nullptr, T);
   // several sequences: the persistent scan once its (v-head, column tile)
-  // workgroups fill the CUs without spreading the sequences over the grid;
-  // otherwise the solve + fused scan path
-  // the fused path (solve + fused scan) is selected with GDN_CHUNK_FUSED=1
-  // while it is slower than prep + scan on every shape measured
-  const bool fused = fused_path_enabled();
-  const bool persist = !fused && n_seqs > 1 && static_cast<int64_t>(Hv) * (DV / SCAN_COLS) >= SCAN_PERSIST_BLOCKS;
-  const int64_t seg = std::min<int64_t>(nc, fused ? SEG_FUSED : SEG_CHUNKS);
-  const WsLayout l = fused ? ws_layout_fused(n_seqs, seg, Hv, nc > SEG_FUSED)
-                           : ws_layout(n_seqs, seg, Hv, nc > SEG_CHUNKS);
+  // workgroups fill the CUs without spreading the sequences over the grid
+  const bool persist = n_seqs > 1 && static_cast<int64_t>(Hv) * (DV / SCAN_COLS) >= SCAN_PERSIST_BLOCKS;
+  const int64_t seg = std::min<int64_t>(nc, SEG_CHUNKS);
+  const WsLayout l = ws_layout(n_seqs, seg, Hv, nc > SEG_CHUNKS);
   if (!workspace || workspace_bytes < l.total)
     return fail(GDN_ERR_WORKSPACE, "%s: workspace %zu bytes < %zu needed", name, workspace_bytes, l.total);
   if (reinterpret_cast<uintptr_t>(workspace) % 256)
@@ -2209,27 +1366,15 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
               reinterpret_cast<float *>(ws + l.carry), reinterpret_cast<int64_t *>(ws + l.seqrec), nullptr};
   // q and k given per v-head (Hk == Hv): the prep checks each chunk's pairs
   // of v-heads for repeated rows and the scan reads one copy of a repeated pair
-  if (!fused && !persist && Hk == Hv && Hv % 2 == 0) a.dup = reinterpret_cast<int32_t *>(ws + l.dup);
+  if (!persist && Hk == Hv && Hv % 2 == 0) a.dup = reinterpret_cast<int32_t *>(ws + l.dup);
   auto set_segment = [&](int64_t segment) {
     a.seg_begin = static_cast<int>(segment * seg);
     a.seg_end = static_cast<int>(std::min<int64_t>((segment + 1) * seg, nc));
   };
   auto launch_prep = [&](hipStream_t st) {
-    if (fused)
-      hipLaunchKernelGGL(chunk_solve_kernel, dim3(Hv, static_cast<unsigned>(seg)), dim3(256), 0, st, a);
-    else
-      hipLaunchKernelGGL(chunk_prep_kernel, dim3(Hv, static_cast<unsigned>(seg)), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(chunk_prep_kernel, dim3(Hv, static_cast<unsigned>(seg)), dim3(256), 0, st, a);
   };
   auto launch_scan = [&](hipStream_t st) {
-    if (fused) {
-      if (o_dtype == GDN_DTYPE_BF16)
-        hipLaunchKernelGGL((chunk_fused_kernel<true>), dim3(static_cast<unsigned>(scan_blocks)), dim3(768),
-                           0, st, a);
-      else
-        hipLaunchKernelGGL((chunk_fused_kernel<false>), dim3(static_cast<unsigned>(scan_blocks)),
-                           dim3(768), 0, st, a);
-      return;
-    }
     if (persist) {
       if (o_dtype == GDN_DTYPE_BF16)
         hipLaunchKernelGGL((chunk_scan_persist_kernel<true>), dim3(static_cast<unsigned>(scan_blocks)),
