@@ -1257,6 +1257,437 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_persist_kernel(Chu
   }
 }
 
+// ------------------------------------------------------------------ local prefill
+// One workgroup of 8 waves per (sequence, v-head) runs the whole chunk loop of
+// that pair on one CU, with no workspace: per chunk, waves 0-3 form the
+// chunk's operands in LDS (the phase-A steps above: K K^T and K Q^T, the
+// solve, W and U), then all 8 waves run the state chain, wave w owning state
+// columns 16w..16w+15 of all 128 rows (eight 16x16 fp32 accumulator tiles):
+//   V' = U - W S                            16 MFMAs  (-W blocks, U tile from LDS)
+//   O^T = (S^T Q^T) diag(sq) + V'^T A^T     22 MFMAs  (q fragments, A blocks from LDS)
+//   S <- e^{gamma_63} S + K^T V''           32 MFMAs  (V'' = diag(sk) V' as bf16 hi + lo)
+// The state is the B operand of V' and the A operand of O^T straight from the
+// accumulators (pi order), V'' the B operand of the state update, so no
+// product needs another wave's registers.  The next chunk's k, v and q rows
+// and gates are requested into registers at the start of each chain step.
+// The chunk operands live in LDS in the layouts their consumers read with
+// one ds_read_b128 per fragment: -W and A blocks as in the workspace layout,
+// q rows as pi fragments (written from the prep waves' own fragments), K^T
+// fragments (written by the wave of the prep that reads all of them), U tiles
+// by (column tile, position tile).  Used when the (sequence, v-head) pairs fill
+// the CUs; the same algorithm and precision as prep + scan.
+constexpr int LOC_WAVES = 4;
+constexpr int LOC_NB_A = 6;  // A blocks (p, s), s <= (p >= 2): those of the lower triangle
+__host__ __device__ constexpr int a_blk(int p, int s) { return p < 2 ? p : 2 * p - 2 + s; }
+enum { SC_SQ = 0, SC_SK = CK, SC_EL = 2 * CK };  // the scalar block: sq[64], sk[64], eL
+
+struct LocIn {  // one chunk's inputs in prep thread tid's registers (tid < 256)
+  u32x4 ku[4], vu[4];
+  bf16x8 qf[4];
+  GateRaw graw;
+};
+
+struct LocLds {
+  uint16_t *kn;     // [64 * 128] K rows (nsw swizzle)
+  f32x4 *s16k;      // [1024]: V rows (nsw) / the solve's exchange buffers
+  u32x4 *ktf;       // [16][64] K^T fragments (row tile nb, position k-step s) at 2 nb + s
+  u32x4 *qp;        // [16][64] q pi fragments (position tile i, k-step s) at 4 i + s
+  u32x4 *wb;        // [16][64] -W blocks (p, s) at 4 p + s
+  f32x4 *ub;        // [32][64] U tiles (column tile nb, position tile p) at 4 nb + p
+  u32x4 *ab;        // [LOC_NB_A][64] A blocks (p, s) at a_blk(p, s)
+  float *sc;        // [256] sq[64], sk[64], eL
+  float *gam_s, *beta_s, *nk_s, *nq_s, *colw_s;  // [64] each
+};
+
+__device__ __forceinline__ void loc_load(const ChunkArgs &a, LocIn &in, int64_t t0, int len, int h, int hk, int tid) {
+  const int lane = tid & 63, p = tid >> 6, g4 = lane >> 4, irow = 16 * p + (lane & 15), seg = tid & 15;
+  // buffer ranges end at the chunk's last row: rows past it read as zero
+  auto rows_rsrc = [&](const uint16_t *base, int64_t stride, int head) {
+    const int64_t bytes = (len - 1) * stride * 2 + DK * 2;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base) + t0 * stride + (int64_t)head * DK, 0,
+                                             static_cast<int>(bytes < 0 ? 0 : bytes), BUF_DWORD3);
+  };
+  const auto rk = rows_rsrc(a.k, a.ks, hk), rv = rows_rsrc(a.v, a.vs, h), rq = rows_rsrc(a.q, a.qs, hk);
+  const int ks2 = static_cast<int>(a.ks * 2), vs2 = static_cast<int>(a.vs * 2), qs2 = static_cast<int>(a.qs * 2);
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int row = (tid >> 4) + 16 * it;
+    in.ku[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, row * ks2 + seg * 16, 0, 0));
+    in.vu[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, row * vs2 + seg * 16, 0, 0));
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int off = irow * qs2 + (32 * s + 4 * g4) * 2;
+    const u32x2 x0 = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rq, off, 0, 0));
+    const u32x2 x1 = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rq, off + 32, 0, 0));
+    in.qf[s] = as_bf16x8(u32x4{x0.x, x0.y, x1.x, x1.y});
+  }
+  in.graw = GateRaw{0u, 0u, 0.f, 0.f};
+  if (p == 0 && lane < len) {
+    const int64_t gi = (t0 + lane) * a.gate.stride + h;
+    in.graw.ga = load_bits(a.gate.g_or_a, gi, a.gate.A_log ? a.gate.dt : GDN_DTYPE_F32);
+    in.graw.gb = load_bits(a.gate.beta_or_b, gi, a.gate.dt);
+  }
+  if (a.gate.A_log) {
+    in.graw.a_log = a.gate.A_log[h];
+    in.graw.dt_bias = a.gate.dt_bias[h];
+  }
+}
+
+// Phase A of one chunk on waves 0-3 (thread tid < 256), from the registers of
+// loc_load into the LDS operands of the chain.
+__device__ __forceinline__ void loc_prep(const ChunkArgs &a, const LocIn &in, const LocLds &L, int len, int tid) {
+  const int lane = tid & 63, p = tid >> 6, g4 = lane >> 4, r16 = lane & 15, seg = tid & 15;
+  const int irow = 16 * p + r16;
+  uint16_t *kn = L.kn;
+  uint16_t *vn = reinterpret_cast<uint16_t *>(L.s16k);
+  f32x4 *lbuf = L.s16k;             // [4 * 64] diagonal blocks of L, row layout by lane
+  f32x4 *dxch = L.s16k + 4 * 64;    // [4 * 64] diagonal blocks of T, D layout by lane
+  f32x4 *txch = L.s16k + 8 * 64;    // [3 * 64] T[1][0], T[2][1], T[2][0], D layout by lane
+  float(*dtr)[16 * 20] = reinterpret_cast<float(*)[16 * 20]>(L.s16k + 11 * 64);  // D -> row layout
+
+  float gv = 0.f, bv = 0.f;
+  if (p == 0 && lane < len) gates_from_raw(a.gate, in.graw, &gv, &bv);
+  // ---- K rows into LDS; K and Q row norms; chunk-local cumsum of g; the q fragments for the chain
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int row = (tid >> 4) + 16 * it;
+    *reinterpret_cast<u32x4 *>(kn + nsw(row, seg * 8)) = in.ku[it];
+    float sk = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t kw = in.ku[it][e];
+      const float k0 = bf16_bits_to_f32(kw & 0xffffu), k1 = bf16_bits_to_f32(kw >> 16);
+      sk += k0 * k0 + k1 * k1;
+    }
+    sk = row16_sum(sk);
+    if (seg == 0) L.nk_s[row] = a.l2norm ? rsqrtf(sk + 1e-6f) : 1.f;
+  }
+  {
+    float sq = 0.f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      L.qp[(4 * p + s) * 64 + lane] = __builtin_bit_cast(u32x4, in.qf[s]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = static_cast<float>(in.qf[s][e]);
+        sq += x * x;
+      }
+    }
+    sq += __shfl_xor(sq, 16, 64);
+    sq += __shfl_xor(sq, 32, 64);
+    if (g4 == 0) L.nq_s[irow] = (a.l2norm ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
+  }
+  if (p == 0) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float x = __shfl_up(gv, off, 64);
+      if (lane >= off) gv += x;
+    }
+    L.gam_s[lane] = gv;
+    L.beta_s[lane] = bv;
+  }
+  __syncthreads();  // (1)
+
+  if (p == 0) {  // per-position scalars of the chain, W's column scale
+    const float gl = L.gam_s[CK - 1], gm = L.gam_s[lane], nkl = L.nk_s[lane];
+    L.sc[SC_SQ + lane] = fast_exp(gm) * L.nq_s[lane];
+    L.sc[SC_SK + lane] = fast_exp(gl - gm) * nkl;
+    if (lane == 0) L.sc[SC_EL] = fast_exp(gl);
+    L.colw_s[lane] = L.beta_s[lane] * fast_exp(gm) * nkl;
+  }
+
+  // ---- tiles (cb, p), cb <= p, of K K^T and K Q^T: L and A in row layout
+  const float gi = L.gam_s[irow], bi = L.beta_s[irow], nki = L.nk_s[irow], nqi = L.nq_s[irow];
+  bf16x8 kown[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) kown[s] = frag_pi(kn, 16 * p, s, lane);
+  f32x4 lf[4], af[4];
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) {
+    lf[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    af[cb] = lf[cb];
+    if (cb <= p) {
+      f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = kk;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const bf16x8 kcb = frag_pi(kn, 16 * cb, s, lane);
+        kk = mfma(kcb, kown[s], kk);
+        qk = mfma(kcb, in.qf[s], qk);
+      }
+      const f32x4 gj = *reinterpret_cast<const f32x4 *>(L.gam_s + 16 * cb + 4 * g4);
+      const f32x4 nj = *reinterpret_cast<const f32x4 *>(L.nk_s + 16 * cb + 4 * g4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int jj = 16 * cb + 4 * g4 + e;
+        const float dec = jj <= irow ? fast_exp(gi - gj[e]) : 0.f;
+        af[cb][e] = nqi * nj[e] * qk[e] * dec;
+        lf[cb][e] = jj < irow ? bi * nki * nj[e] * kk[e] * dec : 0.f;
+      }
+    }
+  }
+  L.ab[a_blk(p, 0) * 64 + lane] = __builtin_bit_cast(u32x4, pack_hi(af[0], af[1]));
+  if (p >= 2) L.ab[a_blk(p, 1) * 64 + lane] = __builtin_bit_cast(u32x4, pack_hi(af[2], af[3]));
+
+  // ---- T = (I + L)^-1 (as in chunk_prep_kernel)
+  f32x4 dl, drow;
+  {
+    f32x4 *lb = lbuf + p * 64;
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+      if (cb == p) lb[lane] = lf[cb];
+    __builtin_amdgcn_wave_barrier();
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float acc = i == r16 ? 1.f : 0.f;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+        if (4 * q4 < i) {
+          const f32x4 lrow = lb[i + 16 * q4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (4 * q4 + e < i) acc -= lrow[e] * x[4 * q4 + e];
+        }
+      x[i] = acc;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      dl[e] = g4 == 0 ? x[e] : g4 == 1 ? x[4 + e] : g4 == 2 ? x[8 + e] : x[12 + e];
+    dxch[p * 64 + lane] = dl;
+    float *tr = dtr[p];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tr[(4 * g4 + e) * 20 + r16] = dl[e];
+    __builtin_amdgcn_wave_barrier();
+    drow = *reinterpret_cast<const f32x4 *>(tr + r16 * 20 + 4 * g4);
+  }
+  __syncthreads();  // (2)
+  f32x4 trow[4];
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int b = 0; b < 4; ++b) trow[b] = b == p ? drow : z4;
+#pragma unroll
+  for (int b = 0; b < 3; ++b)
+    if (b == p - 1) {
+      const f32x4 x = mm16(lf[b], dxch[b * 64 + lane], z4);
+      trow[b] = -mm16(x, drow, z4);
+      if (b <= 1) txch[b * 64 + lane] = -mm16(drow, x, z4);
+    }
+  __syncthreads();  // (3)
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+    if (b == p - 2) {
+      f32x4 x = mm16(lf[b], dxch[b * 64 + lane], z4);
+      x = mm16(lf[b + 1], txch[b * 64 + lane], x);
+      trow[b] = -mm16(x, drow, z4);
+      if (b == 0) txch[2 * 64 + lane] = -mm16(drow, x, z4);
+    }
+  __syncthreads();  // (4)
+  if (p == 3) {
+    f32x4 x = mm16(lf[0], dxch[lane], z4);
+    x = mm16(lf[1], txch[lane], x);
+    x = mm16(lf[2], txch[2 * 64 + lane], x);
+    trow[0] = -mm16(x, drow, z4);
+  }
+  __syncthreads();  // (5) the exchange buffers are free: V rows take their place
+#pragma unroll
+  for (int it = 0; it < 4; ++it)
+    *reinterpret_cast<u32x4 *>(vn + nsw((tid >> 4) + 16 * it, seg * 8)) = in.vu[it];
+  __syncthreads();  // (6)
+
+  // ---- W^T = K^T (T diag(colw))^T and U = T diag(beta) V; wave 3 (which
+  // reads every K^T fragment) also leaves them for the chain
+  f32x4 wt[8], ut[8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) {
+    wt[nb] = z4;
+    ut[nb] = z4;
+  }
+  const int nsteps = p >= 2 ? 2 : 1;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    if (s < nsteps) {
+      const f32x4 cw0 = *reinterpret_cast<const f32x4 *>(L.colw_s + 32 * s + 4 * g4);
+      const f32x4 cw1 = *reinterpret_cast<const f32x4 *>(L.colw_s + 32 * s + 16 + 4 * g4);
+      const f32x4 be0 = *reinterpret_cast<const f32x4 *>(L.beta_s + 32 * s + 4 * g4);
+      const f32x4 be1 = *reinterpret_cast<const f32x4 *>(L.beta_s + 32 * s + 16 + 4 * g4);
+      bf16x8 whi, wlo, uhi, ulo;
+      pack_hilo(trow[2 * s] * cw0, trow[2 * s + 1] * cw1, whi, wlo);
+      pack_hilo(trow[2 * s] * be0, trow[2 * s + 1] * be1, uhi, ulo);
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) {
+        const bf16x8 kt = frag_tr(kn, s, 16 * nb, lane);
+        const bf16x8 vf = frag_tr(vn, s, 16 * nb, lane);
+        if (p == 3) L.ktf[(2 * nb + s) * 64 + lane] = __builtin_bit_cast(u32x4, kt);
+        wt[nb] = mfma(kt, whi, wt[nb]);
+        wt[nb] = mfma(kt, wlo, wt[nb]);
+        ut[nb] = mfma(uhi, vf, ut[nb]);
+        ut[nb] = mfma(ulo, vf, ut[nb]);
+      }
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s) L.wb[(4 * p + s) * 64 + lane] = __builtin_bit_cast(u32x4, pack_hi(-wt[2 * s], -wt[2 * s + 1]));
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) L.ub[(4 * nb + p) * 64 + lane] = ut[nb];
+  __syncthreads();  // (7) the chunk's operands are in LDS
+}
+
+template <bool BF16_OUT>
+__global__ __launch_bounds__(64 * LOC_WAVES) void chunk_local_kernel(ChunkArgs a) {
+  __shared__ __align__(16) uint16_t kn[CK * DK];
+  __shared__ __align__(16) f32x4 s16k[1024];
+  __shared__ u32x4 ktf[16 * 64], qp[16 * 64], wb[16 * 64], ab[LOC_NB_A * 64];
+  __shared__ f32x4 ub[32 * 64];
+  __shared__ __align__(16) float sc[SCAL], gam_s[CK], beta_s[CK], nk_s[CK], nq_s[CK], colw_s[CK];
+  const LocLds L{kn, s16k, ktf, qp, wb, ub, ab, sc, gam_s, beta_s, nk_s, nq_s, colw_s};
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g4 = lane >> 4, r16 = lane & 15;
+  const int ratio = a.Hv / a.Hk;
+  // (sequence, v-head) of this workgroup; the v-heads of one k-head (which
+  // read the same q / k rows) on one XCD when the pairs come in groups of 8
+  int n = blockIdx.x / a.Hv, h = blockIdx.x % a.Hv;
+  if ((a.n_seqs * (a.Hv / ratio)) % 8 == 0) {
+    int g, m;
+    xcd_group_order(blockIdx.x, ratio, &g, &m);
+    n = g / (a.Hv / ratio);
+    h = (g % (a.Hv / ratio)) * ratio + m;
+  }
+  const int hk = h / ratio;
+  int64_t s0;
+  int slen;
+  seq_bounds(a, n, &s0, &slen);
+  s0 = uniform64(s0);
+  slen = __builtin_amdgcn_readfirstlane(slen);
+  const int nch = (slen + CK - 1) / CK;
+  const int64_t kv = static_cast<int64_t>(DK) * DV;
+  const int64_t in_row = a.h0 ? uniform64(pool_row_first(a.h0_idx, n, a.h0_rows)) : -1;
+  const int64_t out_row = a.hT ? uniform64(pool_row_first(a.hT_idx, n, a.hT_rows)) : -1;
+  // wave w: phase A for chunk rows 16w.., then the chain for state columns
+  // 32 w .. + 31 as two 16-column tiles
+  const int cw = wave;
+  float *dst[2];
+  f32x4 S[2][8];  // tile j: state rows 16 t + 4 g + e of column 32 cw + 16 j + r
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int col = 32 * cw + 16 * j + r16;
+    const float *src = in_row >= 0 ? a.h0 + (in_row * a.Hv + h) * kv + col : nullptr;
+    dst[j] = out_row >= 0 ? a.hT + (out_row * a.Hv + h) * kv + col : nullptr;
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) S[j][t][e] = src ? src[(16 * t + 4 * g4 + e) * DV] : 0.f;
+  }
+  auto store_state = [&]() {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      if (dst[j]) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dst[j][(16 * t + 4 * g4 + e) * DV] = S[j][t][e];
+      }
+  };
+  if (nch == 0) {  // empty sequence: the final state is the initial one
+    store_state();
+    return;
+  }
+
+  typedef typename std::conditional<BF16_OUT, uint16_t, float>::type OT;
+  const int64_t ostep = static_cast<int64_t>(a.Hv) * DV;
+  LocIn in;
+  loc_load(a, in, s0, min(CK, slen), h, hk, tid);
+  for (int c = 0; c < nch; ++c) {
+    const int64_t t0 = s0 + static_cast<int64_t>(c) * CK;
+    const int len = min(CK, slen - c * CK);
+    loc_prep(a, in, L, len, tid);  // phase A (ends with a barrier), then the next chunk's inputs requested
+    if (c + 1 < nch) loc_load(a, in, t0 + CK, min(CK, slen - (c + 1) * CK), h, hk, tid);
+
+    // ---- the chain for the wave's two column tiles
+    bf16x8 sb[2][4];  // the state as bf16 B operands (pi order), row k-steps 0..3
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) sb[j][s] = pack_hi(S[j][2 * s], S[j][2 * s + 1]);
+    // V' = U - W S
+    f32x4 vp[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) vp[j][t] = ub[(4 * (2 * cw + j) + t) * 64 + lane];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const bf16x8 w = as_bf16x8(wb[(4 * t + s) * 64 + lane]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) vp[j][t] = mfma(w, sb[j][s], vp[j][t]);
+      }
+    // O^T = (S^T Q^T) diag(sq) + V'^T A^T per position tile i; rows past the chunk dropped
+    bf16x8 vb[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) vb[j][s] = pack_hi(vp[j][2 * s], vp[j][2 * s + 1]);
+    OT *obase = static_cast<OT *>(a.o) + t0 * ostep;
+    const auto ro = __builtin_amdgcn_make_buffer_rsrc(obase, 0, static_cast<int>(len * ostep * sizeof(OT)), BUF_DWORD3);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const bf16x8 qv = as_bf16x8(qp[(4 * i + s) * 64 + lane]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[j] = mfma(sb[j][s], qv, acc[j]);
+      }
+      const float sqi = sc[SC_SQ + 16 * i + r16];
+      const bf16x8 a0 = as_bf16x8(ab[a_blk(i, 0) * 64 + lane]);
+      const bf16x8 a1 = i >= 2 ? as_bf16x8(ab[a_blk(i, 1) * 64 + lane]) : a0;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        f32x4 o = acc[j] * sqi;
+        o = mfma(vb[j][0], a0, o);
+        if (i >= 2) o = mfma(vb[j][1], a1, o);
+        const int voff = static_cast<int>(((16 * i + r16) * ostep + h * DV + 32 * cw + 16 * j + 4 * g4) * sizeof(OT));
+        if constexpr (BF16_OUT)
+          __builtin_amdgcn_raw_buffer_store_b64(pack4(o), ro, voff, 0, 0);
+        else
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), ro, voff, 0, 0);
+      }
+    }
+    // S <- e^{gamma_63} S + K^T V'',  V'' = diag(sk) V' in bf16 hi + lo
+    bf16x8 vh[2][2], vl[2][2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const f32x4 sk0 = *reinterpret_cast<const f32x4 *>(sc + SC_SK + 32 * s + 4 * g4);
+      const f32x4 sk1 = *reinterpret_cast<const f32x4 *>(sc + SC_SK + 32 * s + 16 + 4 * g4);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) pack_hilo(vp[j][2 * s] * sk0, vp[j][2 * s + 1] * sk1, vh[j][s], vl[j][s]);
+    }
+    const float eL = sc[SC_EL];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) S[j][t] = S[j][t] * eL;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const bf16x8 kt = as_bf16x8(ktf[(2 * t + s) * 64 + lane]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          S[j][t] = mfma(kt, vh[j][s], S[j][t]);
+          S[j][t] = mfma(kt, vl[j][s], S[j][t]);
+        }
+      }
+    __syncthreads();  // the chunk's operands are read: the next prep may overwrite them
+  }
+  store_state();
+}
+
 // Chunks per prep + scan segment: one prep launch produces a segment's
 // operands (about 2.3 MiB per chunk at 32 v-heads: 146 MiB for 64 chunks,
 // which stay in the 256 MB Infinity Cache until the scan reads them) and one
@@ -1268,6 +1699,7 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_persist_kernel(Chu
 // kernels cannot share a CU -- the scan holds 138 KiB of LDS -- so the prep
 // takes CUs from the scan's chain).
 constexpr int SEG_CHUNKS = 64;
+constexpr int LOC_MIN_PAIRS = 256;  // (sequence, v-head) pairs from which the local kernel runs
 
 // Workspace: the chunk table, the state carried between segments (when
 // there are several) and the scan operands of one segment.
@@ -1347,6 +1779,8 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
   const int64_t nc = max_chunks_of(n_seqs, total, cu_seqlens != nullptr, T);
   // several sequences: the persistent scan once its (v-head, column tile)
   // workgroups fill the CUs without spreading the sequences over the grid
+  // (sequence, v-head) pairs that fill the CUs: the local kernel, one workgroup per pair
+  const bool local = static_cast<int64_t>(n_seqs) * Hv >= LOC_MIN_PAIRS;
   const bool persist = n_seqs > 1 && static_cast<int64_t>(Hv) * (DV / SCAN_COLS) >= SCAN_PERSIST_BLOCKS;
   const int64_t seg = std::min<int64_t>(nc, SEG_CHUNKS);
   const WsLayout l = ws_layout(n_seqs, seg, Hv, nc > SEG_CHUNKS);
@@ -1392,6 +1826,14 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
                          dim3(64 * SCAN_WAVES), 0, st, a);
   };
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (local) {  // one workgroup per (sequence, v-head), no workspace
+    const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(n_seqs) * Hv)), block(64 * LOC_WAVES);
+    if (o_dtype == GDN_DTYPE_BF16)
+      hipLaunchKernelGGL((chunk_local_kernel<true>), grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL((chunk_local_kernel<false>), grid, block, 0, s, a);
+    return check_launch(name);
+  }
   // the chunk table: chunk starts for varlen, per-sequence records for the persistent scan
   // (which computes them itself for a dense batch without slot ids)
   if (cu_seqlens || (persist && (h0_idx || hT_idx)))
