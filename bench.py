@@ -45,6 +45,7 @@ import argparse
 import concurrent.futures as cf
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -198,7 +199,7 @@ def bench_decode(torch, steps, warmup, n_pools):
     return dict(tokens=b, steps=steps, kernel_s=kernel_s, eager_wall=eager_wall, graph_wall=graph_wall)
 
 
-def bench_decode_batches(torch, batches=(1, 4, 16, 64), reps=50):
+def bench_decode_batches(torch, batches=(1, 4, 16, 64), reps=100):
     """The decode step of configuration 1 at smaller batches (the first B
     rows of its inputs and slots; pool of 128 slots, 4 pools rotating so that
     the touched states come from HBM): time per step from a HIP graph of 20
@@ -233,13 +234,13 @@ def bench_decode_batches(torch, batches=(1, 4, 16, 64), reps=50):
         with torch.cuda.graph(gph):
             for _ in range(20):
                 step()
-        t = _time(torch, gph.replay, max(1, reps // 10)) / 20
+        t = _time(torch, gph.replay, reps) / 20
         byts = 2 * b * 32 * 128 * 128 * 4
         out[f"B{b}"] = {"us": t * 1e6, "tok_per_s": b / t, "frac": byts / t / HBM_PEAK, "eager_us": t_eager * 1e6}
     return out
 
 
-def bench_prefill(torch, reps=24, warmup=3, repeat_qk=False, n_sets=3):
+def bench_prefill(torch, reps=120, warmup=3, repeat_qk=False, n_sets=3):
     """Configuration 2.  With repeat_qk, q and k arrive repeated to the 32 v-heads
     (HF's repeat_interleave before the call), the layout the reference's boundary
     actually receives; otherwise they keep their 16 heads (native GQA).  Calls
@@ -263,27 +264,23 @@ def bench_prefill(torch, reps=24, warmup=3, repeat_qk=False, n_sets=3):
     def run(i):
         return chunk_gated_delta_rule(*sets[i % n_sets], output_final_state=True, use_qk_l2norm_in_kernel=True)
 
-    for i in range(warmup):
-        run(i)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for i in range(reps):
-        run(i)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    per = e0.elapsed_time(e1) * 1e-3 / reps
+    i = [0]
+
+    def call():
+        run(i[0])
+        i[0] += 1
+
+    per = _time(torch, call, reps, warmup)
     flop = PREFILL_FLOP_PER_CHUNK_HEAD * ((t + 63) // 64) * 32
     set_mb = sum(x.numel() * x.element_size() for x in sets[0]) / 1e6
     return {"config": f"prefill B=1 T=4096 Hk={sets[0][0].shape[2]} Hv=32 d=128 bf16, chunk 64, zero h0, "
                       f"final state out; {n_sets} input sets of {set_mb:.0f} MB rotated call by call",
-            "tok_per_s": t / per, "ms": per * 1e3,
+            "tok_per_s": t / per, "ms": per * 1e3, "reps": reps, "timing": "median of per-call events",
             "mfma": {"achieved": flop / per / 1e12, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
                      "frac": flop / per / MFMA_BF16_PEAK, "flop_per_call": flop}}
 
 
-def bench_prefill_b16(torch, reps=10, repeat_qk=False):
+def bench_prefill_b16(torch, reps=100, repeat_qk=False):
     """The reference's own profiled prefill shape (its profile of fla's chunk
     kernel: 1.659 ms per layer on H200): a dense batch of 16 sequences of 1038
     tokens (17 chunks each), q/k at 16 heads (with repeat_qk: repeated to the
@@ -311,7 +308,7 @@ def bench_prefill_b16(torch, reps=10, repeat_qk=False):
             "reference_h200_us": 1659.0}
 
 
-def bench_varlen(torch, reps=10):
+def bench_varlen(torch, reps=100):
     """Configuration 3: 16 packed sequences (lengths U{128..2048}, seeded) as
     HF's layer runs them after the input projections: the causal conv + SiLU
     over the packed [sum L, 8192] projection with cu_seqlens (windows from
@@ -355,7 +352,7 @@ def bench_varlen(torch, reps=10):
             "gdn_bytes": gdn_bytes}
 
 
-def bench_spec_verify(torch, reps=20):
+def bench_spec_verify(torch, reps=100):
     """Configuration 4: a speculative verify step of B=32 sequences x T=4
     tokens on a 64-slot fp32 pool (the recurrence reading each slot's state
     and writing all four per-token states as snapshots, the pool untouched),
@@ -392,20 +389,24 @@ def bench_spec_verify(torch, reps=20):
 
 
 def _time(torch, fn, reps, warmup=3):
+    """Median, over ``reps`` calls, of the time between two events recorded
+    on the current stream just before and just after each call (seconds).
+    A call that the host launches more slowly than the GPU runs it (a small
+    eager step) is timed with its launch gap, as the caller would see it."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(reps):
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for e0, e1 in ev:
+        e0.record(stream)
         fn()
-    e1.record(stream)
+        e1.record(stream)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e-3 / reps
+    return statistics.median(e0.elapsed_time(e1) for e0, e1 in ev) * 1e-3
 
 
-def bench_conv_prefill(torch, reps=40):
+def bench_conv_prefill(torch, reps=100):
     """Row a-6's prefill conv (``causal_conv1d_fn`` + SiLU, width 4) over the
     qkv projection rows as the layer feeds it (token-major [T, 8192] bf16,
     transformers modeling_qwen3_5_moe.py:443-444, 468-474), for one 4096-token and one 16384-token
@@ -435,7 +436,7 @@ def bench_conv_prefill(torch, reps=40):
     return out
 
 
-def bench_layer_glue(torch, reps=20):
+def bench_layer_glue(torch, reps=100):
     """Configuration 2's shape through the GDN layer glue (row f-1): the glue as
     HF's layer forward runs it in torch around the core (gates,
     modeling_qwen3_5_moe.py:495-497; q/k repeat_interleave, :498-500;
@@ -631,12 +632,13 @@ def cpu_baseline(budget_s=6.0):
     return out
 
 
-def bench_in_proj(torch, sets=6, reps=4):
+def bench_in_proj(torch, sets=6, reps=100):
     """Row f-4 at the decode batch (64 rows, hidden 2048, Qwen3.5-MoE GDN
     shapes): the fused input-projection kernel against the unfused path HF's
     layer takes (four nn.Linear on hipBLASLt, then causal_conv1d_update on
     the slot pool).  Each path is captured once per weight set into one
-    HIP graph; the graph is replayed ``reps`` times between two events."""
+    HIP graph; the graph is replayed ``reps`` times, each replay between two
+    events, and the median replay is reported."""
     import torch.nn.functional as F
     from engine.kernels import causal_conv1d_update, gdn_in_proj_decode
 
@@ -670,7 +672,7 @@ def bench_in_proj(torch, sets=6, reps=4):
         return _time(torch, g.replay, reps, warmup=2) / sets * 1e6
 
     t_fused, t_unfused = graph_us(fused), graph_us(unfused)
-    t_eager = _time(torch, lambda: fused(wsets[0]), 50) * 1e6
+    t_eager = _time(torch, lambda: fused(wsets[0]), reps) * 1e6
     wbytes = sum(c for c in n) * k * 2
     byts = wbytes + m * k * 2 + m * sum(n) * 2 + 2 * m * n[0] * 8  # weights, x, outputs, windows read + written
     return {"config": "B=64 rows, hidden 2048 -> qkv 8192 (conv width 4, 128-slot bf16 pool) / z 4096 / b 32 / a 32, bf16",
@@ -681,7 +683,7 @@ def bench_in_proj(torch, sets=6, reps=4):
                          "kernel": "gdn::in_proj_xs_kernel<16, 4>"}}
 
 
-def bench_out_proj(torch, sets=16, reps=4):
+def bench_out_proj(torch, sets=16, reps=100):
     """Row f-4's output side at the decode batch: ``out_proj`` (4096 -> 2048,
     bf16) for 64 rows, the split-K kernel pair against hipBLASLt (torch
     F.linear), each captured once per weight set into one HIP graph (16 sets:
@@ -719,7 +721,7 @@ def bench_out_proj(torch, sets=16, reps=4):
                                     "partials written and read besides)"}}
 
 
-def bench_layer_decode(torch, layers=4, reps=5, batch=64):
+def bench_layer_decode(torch, layers=4, reps=100, batch=64):
     """One GDN layer decode step at B=64 with Qwen3.5-MoE layer shapes (hidden
     2048, 16 k-heads, 32 v-heads of 128, conv width 4; random bf16 weights):
     HF's ``Qwen3_5MoeGatedDeltaNet`` with ``gated_delta_net_forward`` on

@@ -13,8 +13,11 @@
  *     allocates device memory or synchronises the device or the stream:
  *     every kernel is enqueued on `stream` (a hipStream_t passed as void*;
  *     NULL is the null stream), so calls are safe to record into a HIP graph.
- *     The library keeps no state between calls and creates no streams or
- *     events (apart from the thread-local error string).
+ *     The library creates no streams or events.  Between calls it keeps
+ *     the thread-local error string and, for gdn_out_proj_decode_noalloc
+ *     only, a fixed per-GPU scratch array (GDN_OUT_PROJ_NOALLOC_MAX_BYTES)
+ *     whose address is looked up once per device; every other entry point
+ *     works only on the buffers its caller passes.
  *   - The return value is a gdn_status_t.  On failure nothing was launched
  *     and gdn_last_error_string() (thread-local) says why.
  *   - Token-major activations: element (token t, head h, dim d) of q/k/v lives
@@ -139,7 +142,8 @@ int gdn_recurrent_fwd_gated(const void *q, const void *k, const void *v, int qkv
  *   hT  fp32 final states (hT_rows rows, selected by hT_idx) or NULL; hT may
  *       equal h0.  Ids as for gdn_recurrent_fwd.
  *   o   [tokens, Hv, V] o_dtype, contiguous
- *   workspace  device scratch of at least gdn_chunk_workspace_bytes(...)
+ *   workspace  device scratch of at least gdn_chunk_workspace_bytes(...),
+ *              256-byte aligned (unused, may be NULL, when that is 0)
  * Requires K == V == 128 and q/k/v in bf16.
  */
 int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
@@ -171,7 +175,10 @@ int gdn_chunk_fwd_gated(const void *q, const void *k, const void *v, int qkv_dty
                         void *workspace, size_t workspace_bytes, void *stream);
 
 /* Workspace bytes gdn_chunk_fwd(_gated) needs for `total_tokens` tokens in
- * `n_seqs` sequences (an upper bound that needs no knowledge of the lengths). */
+ * `n_seqs` sequences (an upper bound that needs no knowledge of the lengths).
+ * 0 when n_seqs * Hv >= 256: such a batch runs one workgroup per (sequence,
+ * v-head) that keeps every chunk operand in LDS, and the workspace pointer
+ * may then be NULL. */
 size_t gdn_chunk_workspace_bytes(int32_t n_seqs, int64_t total_tokens,
                                  int32_t Hv, int32_t K, int32_t V);
 

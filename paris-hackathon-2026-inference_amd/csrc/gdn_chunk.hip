@@ -1741,6 +1741,7 @@ extern "C" size_t gdn_chunk_workspace_bytes(int32_t n_seqs, int64_t total_tokens
                                             int32_t V) {
   using namespace gdn;
   if (n_seqs <= 0 || total_tokens < 0 || Hv <= 0 || K != DK || V != DV) return 0;
+  if (static_cast<int64_t>(n_seqs) * Hv >= LOC_MIN_PAIRS) return 0;  // the local kernel keeps all in LDS
   // Upper bound valid with or without cu_seqlens.
   const int64_t nc = (total_tokens + CK - 1) / CK + n_seqs;
   return ws_layout(n_seqs, std::min<int64_t>(nc, SEG_CHUNKS), Hv, nc > SEG_CHUNKS).total;
@@ -1784,6 +1785,19 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
   const bool persist = n_seqs > 1 && static_cast<int64_t>(Hv) * (DV / SCAN_COLS) >= SCAN_PERSIST_BLOCKS;
   const int64_t seg = std::min<int64_t>(nc, SEG_CHUNKS);
   const WsLayout l = ws_layout(n_seqs, seg, Hv, nc > SEG_CHUNKS);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (local) {  // one workgroup per (sequence, v-head); no workspace
+    ChunkArgs a{static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
+                q_stride_t, k_stride_t, v_stride_t, gate, h0, h0_idx, h0_rows, hT, hT_idx, hT_rows, o, o_dtype,
+                cu_seqlens, n_seqs, T, Hk, Hv, total, scale, l2norm_qk, static_cast<int>(std::min<int64_t>(nc, 0x7fffffff)),
+                0, 0, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(n_seqs) * Hv)), block(64 * LOC_WAVES);
+    if (o_dtype == GDN_DTYPE_BF16)
+      hipLaunchKernelGGL((chunk_local_kernel<true>), grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL((chunk_local_kernel<false>), grid, block, 0, s, a);
+    return check_launch(name);
+  }
   if (!workspace || workspace_bytes < l.total)
     return fail(GDN_ERR_WORKSPACE, "%s: workspace %zu bytes < %zu needed", name, workspace_bytes, l.total);
   if (reinterpret_cast<uintptr_t>(workspace) % 256)
@@ -1825,15 +1839,6 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
       hipLaunchKernelGGL((chunk_scan_kernel<false>), dim3(static_cast<unsigned>(scan_blocks)),
                          dim3(64 * SCAN_WAVES), 0, st, a);
   };
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (local) {  // one workgroup per (sequence, v-head), no workspace
-    const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(n_seqs) * Hv)), block(64 * LOC_WAVES);
-    if (o_dtype == GDN_DTYPE_BF16)
-      hipLaunchKernelGGL((chunk_local_kernel<true>), grid, block, 0, s, a);
-    else
-      hipLaunchKernelGGL((chunk_local_kernel<false>), grid, block, 0, s, a);
-    return check_launch(name);
-  }
   // the chunk table: chunk starts for varlen, per-sequence records for the persistent scan
   // (which computes them itself for a dense batch without slot ids)
   if (cu_seqlens || (persist && (h0_idx || hT_idx)))

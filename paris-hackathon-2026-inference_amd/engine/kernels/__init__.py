@@ -10,7 +10,7 @@ third-party packages (fla, causal-conv1d) via HF:
 - ``fused_recurrent_gated_delta_rule``  decode / spec-verify recurrence
 - ``recurrent_gated_delta_rule``        HF-signature adapter of the above
 - ``causal_conv1d_fn``, ``causal_conv1d_update``
-- ``gdn_state_commit``, ``gdn_conv_state_commit``, ``LinearAttentionSlotPool``
+- ``gdn_state_commit``, ``gdn_conv_state_commit``
 - ``chunk_gated_delta_rule_from_projections``,
   ``fused_recurrent_gated_delta_rule_from_projections``  gates computed in
   the kernels from the layer's raw a / b projections
@@ -36,7 +36,7 @@ from .fused_recurrent import (fused_recurrent_gated_delta_rule, fused_recurrent_
                               recurrent_gated_delta_rule)
 from .gdn_layer import gated_delta_net_forward, install_gdn_layer_patch, rms_norm_gated
 from .in_proj import gdn_in_proj_decode, gdn_out_proj_decode
-from .state_pool import LinearAttentionSlotPool, gdn_conv_state_commit, gdn_state_commit
+from .state_pool import gdn_conv_state_commit, gdn_state_commit
 
 __all__ = [
     "chunk_gated_delta_rule",
@@ -47,7 +47,6 @@ __all__ = [
     "causal_conv1d_update",
     "gdn_state_commit",
     "gdn_conv_state_commit",
-    "LinearAttentionSlotPool",
     "chunk_gated_delta_rule_from_projections",
     "fused_recurrent_gated_delta_rule_from_projections",
     "rms_norm_gated",

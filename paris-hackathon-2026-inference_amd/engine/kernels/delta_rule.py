@@ -188,6 +188,13 @@ def _chunk(query, key, value, gates, chunk_size, initial_state, output_final_sta
         if has.numel() != n_seqs:
             raise ValueError(f"has_initial_state has {has.numel()} entries for {n_seqs} sequences")
         rows = idx if idx is not None else torch.arange(n_seqs, device=dev, dtype=torch.int64)
+        if idx is not None:
+            # a row repeating an earlier row's slot id is "no slot" for both the
+            # read and the write: decide the repeats on the unmasked ids, so the
+            # masked read ids cannot turn a later repeat into the slot's reader
+            # while the first row writes it
+            rep = (rows[:, None] == rows[None, :]).tril(-1).any(dim=1)
+            has = has & ~rep
         h0_idx = torch.where(has, rows, torch.full_like(rows, -1))
     if output_final_state and not inplace_final_state:
         final = hT = torch.empty((n_seqs, hv, dk, dv), dtype=torch.float32, device=dev)

@@ -5,12 +5,11 @@ The reference keeps one GDN layer's state as two slot pools
 recurrent ``[slots, Hv, K, V]`` fp32 and conv ``[slots, conv_dim, 4]`` bf16,
 gathered with ``index_select(...).clone()`` before each forward and
 scattered back with ``index_copy_`` after it (:189-208).  Here the kernels
-address the pools by slot id, so :class:`LinearAttentionSlotPool` only owns
-the tensors; decode, prefill and the spec-verify commit update them in place.
+address the pools by slot id (engine/runtime/slot_pools.py owns the tensors);
+decode, prefill and the spec-verify commits of both the recurrent state and
+the conv window update them in place.
 """
 from __future__ import annotations
-
-from typing import Optional
 
 import torch
 
@@ -73,29 +72,3 @@ def gdn_conv_state_commit(pool: torch.Tensor, slot_ids: torch.Tensor, hist: torc
                                            n, c, s, length, _lib.GDN_DTYPE[pool.dtype], _lib.stream_of(pool))
     _lib.check(st, "gdn_conv_state_commit")
     return pool
-
-
-class LinearAttentionSlotPool:
-    """One GDN layer's pooled state, addressed by slot id (no gather/scatter).
-
-    Mirrors the reference's ``_LinearAttentionSlotLayer`` pools and
-    ``reset_slot`` (kv_cache.py:160-212) with the same shapes and dtypes.
-    """
-
-    def __init__(self, num_slots: int, conv_dim: int = 8192, conv_kernel: int = 4,
-                 num_v_heads: int = 32, head_k_dim: int = 128, head_v_dim: int = 128,
-                 device: Optional[torch.device] = None, conv_dtype: torch.dtype = torch.bfloat16):
-        device = device or torch.device("cuda")
-        self.num_slots = num_slots
-        self.conv_states = torch.zeros(num_slots, conv_dim, conv_kernel, dtype=conv_dtype, device=device)
-        self.recurrent_states = torch.zeros(num_slots, num_v_heads, head_k_dim, head_v_dim,
-                                            dtype=torch.float32, device=device)
-
-    def reset_slot(self, slot_id: int) -> None:
-        self.conv_states[slot_id].zero_()
-        self.recurrent_states[slot_id].zero_()
-
-    def commit_spec(self, slot_ids: torch.Tensor, snapshots: torch.Tensor,
-                    accepted_len: torch.Tensor) -> None:
-        """Keep the recurrent state after each sequence's last accepted draft token."""
-        gdn_state_commit(self.recurrent_states, slot_ids, snapshots, accepted_len)

@@ -27,7 +27,10 @@ with its own torch GDN paths and ``DynamicCache``) on the seeded layers of
 side (each through its own cache, as the reference engine's slot cache
 gathers them), a slot reset and reused, and speculative verify of T = 1, 4
 and 17 tokens followed by the decode of only the accepted tokens.  The GPU
-tests rebuild the same weights and compare; they never run HF's forward.
+tests rebuild the same weights and compare.  The expected values always come
+from HF's forward on its own torch paths, here; on the GPU box HF's forward
+runs only as the caller of the installed GPU kernels (test_gpu_binding.py),
+never as the source of expected values.
 
 Usage:  HF_HUB_OFFLINE=1 python tests/golden/make_golden.py
 """

@@ -103,8 +103,12 @@ def test_commit_rejects_bad_sizes(lib):
 
 def test_chunk_workspace_is_host_arithmetic(lib):
     a = lib.gdn_chunk_workspace_bytes(1, 4096, 32, 128, 128)
-    b = lib.gdn_chunk_workspace_bytes(16, 4096, 32, 128, 128)
-    assert a >= 0 and b >= a
+    b = lib.gdn_chunk_workspace_bytes(4, 4096, 32, 128, 128)
+    assert a > 0 and b >= a
+    # a batch of 256+ (sequence, v-head) pairs runs one workgroup per pair
+    # with all its operands in LDS: no workspace
+    assert lib.gdn_chunk_workspace_bytes(8, 4096, 32, 128, 128) == 0
+    assert lib.gdn_chunk_workspace_bytes(16, 16 * 1038, 32, 128, 128) == 0
 
 
 def test_wrappers_refuse_cpu_tensors():

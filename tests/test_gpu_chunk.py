@@ -357,3 +357,28 @@ def test_repeated_slot_ids_advance_a_slot_once():
         assert gdn.state_rel_err(np64(pd[4])[None], s_ref_rows[1][None]) < S_TOL, fn
         assert torch.equal(pd[[0, 1, 3]].cpu(), pool[[0, 1, 3]]), fn
         assert np.abs(np64(o[1]) - o0_pad[0]).max() < O_TOL, fn  # the repeated row: zero initial state
+
+
+@pytest.mark.parametrize("has_first", [False, True])
+def test_repeated_slot_id_with_mismatched_has_initial_state(has_first):
+    """ids [5, 5] with has_initial_state [has_first, not has_first], in place,
+    varlen: the repeat is decided on the slot ids themselves, so row 0 alone
+    reads (when its flag is set) and writes slot 5, and row 1 runs from a zero
+    state and writes nothing -- the read of one row never races the write of
+    the other."""
+    c = configs.config2(seed=68, t=2 * 90)
+    cu = torch.tensor([0, 90, 180], dtype=torch.int32)
+    pool = torch.randn(6, 32, 128, 128, generator=torch.Generator().manual_seed(69)) * 0.1
+    ids = torch.tensor([5, 5])
+    has = torch.tensor([has_first, not has_first])
+    pd = pool.to(DEV)
+    o, _ = chunk_gated_delta_rule(*(c[x].to(DEV) for x in ("q", "k", "v", "g", "beta")), initial_state=pd,
+                                  ssm_state_indices=ids.to(DEV), has_initial_state=has.to(DEV),
+                                  inplace_final_state=True, use_qk_l2norm_in_kernel=True, cu_seqlens=cu.to(DEV))
+    zero = np.zeros((32, 128, 128), np.float32)
+    h0 = np.stack([pool[5].numpy() if has_first else zero, zero])
+    o_ref, s_ref = gdn.chunk_gated_delta_rule_varlen(*(c[x].float().numpy() for x in ("q", "k", "v", "g", "beta")),
+                                                     cu.numpy(), h0)
+    assert np.abs(np64(o) - o_ref).max() < O_TOL
+    assert gdn.state_rel_err(np64(pd[5])[None], s_ref[0:1]) < S_TOL
+    assert torch.equal(pd[:5].cpu(), pool[:5])
