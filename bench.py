@@ -280,6 +280,29 @@ def bench_prefill(torch, reps=120, warmup=3, repeat_qk=False, n_sets=3):
                      "frac": flop / per / MFMA_BF16_PEAK, "flop_per_call": flop}}
 
 
+def bench_prefill_non_bf16(torch, dtype, reps=5):
+    """Configuration 2 (B=1, T=4096) with q/k/v given in fp32 or fp16 instead
+    of bf16: the chunk entry then runs the token recurrence in fp32 on the
+    inputs as given (the MFMA chunk path takes bf16 operands only).  Few
+    reps: one call is milliseconds."""
+    from engine import configs
+    from engine.kernels import chunk_gated_delta_rule
+
+    dev = torch.device("cuda", 0)
+    c = configs.config2(seed=2)
+    q, k, v = (c[x].to(dev, dtype) for x in ("q", "k", "v"))
+    g, beta = c["g"].to(dev), c["beta"].to(dev)
+    t = q.shape[1]
+
+    def run():
+        return chunk_gated_delta_rule(q, k, v, g, beta, output_final_state=True, use_qk_l2norm_in_kernel=True)
+
+    per = _time(torch, run, reps, warmup=1)
+    return {"config": f"prefill B=1 T={t} Hk=16 Hv=32 d=128, q/k/v {str(dtype).replace('torch.', '')}, "
+                      "zero h0, final state out (token recurrence)",
+            "ms": per * 1e3, "tok_per_s": t / per, "reps": reps}
+
+
 def bench_prefill_b16(torch, reps=100, repeat_qk=False):
     """The reference's own profiled prefill shape (its profile of fla's chunk
     kernel: 1.659 ms per layer on H200): a dense batch of 16 sequences of 1038
@@ -850,6 +873,9 @@ def main():
         out["prefill"] = bench_prefill(torch)
         if not args.no_prefill_repeated:
             out["prefill_qk_repeated"] = bench_prefill(torch, repeat_qk=True)
+        for dt, key in ((torch.float32, "prefill_f32_qkv"), (torch.float16, "prefill_f16_qkv")):
+            out[key] = bench_prefill_non_bf16(torch, dt)
+            out[key]["x_bf16_call"] = out[key]["ms"] / out["prefill"]["ms"]
         if not args.no_layer_glue:
             out["layer_glue"] = bench_layer_glue(torch)
         out["varlen"] = bench_varlen(torch)

@@ -207,6 +207,8 @@ int gdn_rmsnorm_gated_fwd(const void *x, int x_dtype, int64_t x_stride_t,
  * layout engine/runtime/kv_cache.py:142-156), including the cache update HF
  * does before it (cache_utils.py:1032-1068).
  *
+ *   dtype  bf16, fp16 or fp32 storage of x, w, bias, y and the windows
+ *          (fp32 arithmetic, one rounding per stored value)
  *   x      [tokens, C] (dtype, token stride x_stride_t, channels contiguous)
  *   w      [C, width] (dtype);  bias [C] (dtype) or NULL
  *   y      [tokens, C] (dtype, token stride y_stride_t)
@@ -235,7 +237,8 @@ int causal_conv1d_fwd(const void *x, int64_t x_stride_t, const void *w, const vo
  * reference's slot pool [slots, C, state_len] (engine/runtime/kv_cache.py:
  * 142-146) addressed by slot index instead of gathered.
  *
- *   x [n_seqs*T, C] (token stride x_stride_t), y likewise (y_stride_t)
+ *   x [n_seqs*T, C] (token stride x_stride_t), y likewise (y_stride_t);
+ *   x, w, bias, y and conv_state share dtype: bf16, fp16 or fp32
  *   conv_state [state_rows, C, state_len], rows by state_idx (NULL: row n);
  *   updated in place.  Ids outside [0, state_rows): zero window, nothing
  *   written.
@@ -337,7 +340,7 @@ int gdn_state_commit(float *pool, const int64_t *slot_ids, int64_t pool_rows, co
  * [a, a + S) are the window after the first a tokens.  accepted_len[b] <= 0
  * or slot_ids[b] outside [0, pool_rows) leaves the slot untouched.  Rolls back the conv state
  * that engine/runtime/spec_decode.py:81-87 leaves without a rollback.
- *   pool [pool_rows, C, S] and hist [n_seqs, C, L] of dtype (bf16 or fp32)
+ *   pool [pool_rows, C, S] and hist [n_seqs, C, L] of dtype (bf16, fp16 or fp32)
  *   slot_ids int64 [n_seqs];  accepted_len int32 [n_seqs]
  */
 int gdn_conv_state_commit(void *pool, const int64_t *slot_ids, int64_t pool_rows, const void *hist,

@@ -10,6 +10,8 @@
 // Update: one thread per (sequence, channel) shifts the cached window by
 // the T new tokens in place.
 //
+// Storage bf16, fp16 or fp32 (x, weight, bias, windows and y share it);
+// arithmetic in fp32, one rounding on the store.
 // Semantics: transformers modeling_qwen3_5_moe.py:200-240 (causal_conv1d_fn
 // and causal_conv1d_update) and cache_utils.py:1032-1068 (cached window).
 #include "gdn_common.h"
@@ -64,12 +66,37 @@ template <> struct Vec8<float> {
   }
 };
 
+template <> struct Vec8<_Float16> {
+  struct Raw { uint4 u; };
+  static constexpr int PF = 4;
+  static __device__ __forceinline__ Raw load_raw(const _Float16 *p) { return Raw{*reinterpret_cast<const uint4 *>(p)}; }
+  static __device__ __forceinline__ void cvt(const Raw &r, float *o) {
+    const uint32_t w[4] = {r.u.x, r.u.y, r.u.z, r.u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] & 0xffffu)));
+      o[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] >> 16)));
+    }
+  }
+  static __device__ __forceinline__ void load(const _Float16 *p, float *o) { cvt(load_raw(p), o); }
+  static __device__ __forceinline__ void store(_Float16 *p, const float *x) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)  // round to nearest even, as torch's fp16 cast
+      w[i] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(x[2 * i]))) |
+             (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(x[2 * i + 1]))) << 16);
+    *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+
 template <typename T> __device__ __forceinline__ float ld1(const T *p);
 template <> __device__ __forceinline__ float ld1<uint16_t>(const uint16_t *p) { return bf16_bits_to_f32(*p); }
 template <> __device__ __forceinline__ float ld1<float>(const float *p) { return *p; }
+template <> __device__ __forceinline__ float ld1<_Float16>(const _Float16 *p) { return static_cast<float>(*p); }
 template <typename T> __device__ __forceinline__ void st1(T *p, float x);
 template <> __device__ __forceinline__ void st1<uint16_t>(uint16_t *p, float x) { *p = f32_to_bf16_bits(x); }
 template <> __device__ __forceinline__ void st1<float>(float *p, float x) { *p = x; }
+template <> __device__ __forceinline__ void st1<_Float16>(_Float16 *p, float x) { *p = static_cast<_Float16>(x); }
 
 __device__ __forceinline__ float silu(float x) { return x / (1.f + expf(-x)); }
 // SiLU with the hardware exp2 and reciprocal (a few ulp; the prefill kernel's
@@ -374,8 +401,8 @@ extern "C" int causal_conv1d_fwd(const void *x, int64_t x_stride_t, const void *
                                  int32_t C, int32_t width, int32_t state_len,
                                  int silu, int dtype, void *stream) {
   using namespace gdn;
-  if (dtype != GDN_DTYPE_BF16 && dtype != GDN_DTYPE_F32)
-    return fail(GDN_ERR_UNSUPPORTED, "causal_conv1d_fwd: dtype must be bf16 or fp32");
+  if (!valid_dtype(dtype))
+    return fail(GDN_ERR_UNSUPPORTED, "causal_conv1d_fwd: dtype must be bf16, fp16 or fp32");
   if (width < 1 || width > 4 || (state_len != 3 && state_len != 4))
     return fail(GDN_ERR_UNSUPPORTED, "causal_conv1d_fwd: width=%d state_len=%d (need width<=4, state_len in {3,4})",
                 width, state_len);
@@ -397,6 +424,8 @@ extern "C" int causal_conv1d_fwd(const void *x, int64_t x_stride_t, const void *
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == GDN_DTYPE_BF16)
     return state_len == 4 ? launch_fwd<uint16_t, 4>(a, s) : launch_fwd<uint16_t, 3>(a, s);
+  if (dtype == GDN_DTYPE_F16)
+    return state_len == 4 ? launch_fwd<_Float16, 4>(a, s) : launch_fwd<_Float16, 3>(a, s);
   return state_len == 4 ? launch_fwd<float, 4>(a, s) : launch_fwd<float, 3>(a, s);
 }
 
@@ -406,8 +435,8 @@ extern "C" int causal_conv1d_update(const void *x, int64_t x_stride_t, void *con
                                     int32_t C, int32_t width, int32_t state_len,
                                     int silu, int dtype, void *stream) {
   using namespace gdn;
-  if (dtype != GDN_DTYPE_BF16 && dtype != GDN_DTYPE_F32)
-    return fail(GDN_ERR_UNSUPPORTED, "causal_conv1d_update: dtype must be bf16 or fp32");
+  if (!valid_dtype(dtype))
+    return fail(GDN_ERR_UNSUPPORTED, "causal_conv1d_update: dtype must be bf16, fp16 or fp32");
   if (width < 1 || width > 4 || (state_len != 3 && state_len != 4) || width > state_len + 1)
     return fail(GDN_ERR_UNSUPPORTED, "causal_conv1d_update: width=%d state_len=%d (need width<=min(4,state_len+1))",
                 width, state_len);
@@ -423,5 +452,7 @@ extern "C" int causal_conv1d_update(const void *x, int64_t x_stride_t, void *con
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == GDN_DTYPE_BF16)
     return state_len == 4 ? launch_upd<uint16_t, 4>(a, s) : launch_upd<uint16_t, 3>(a, s);
+  if (dtype == GDN_DTYPE_F16)
+    return state_len == 4 ? launch_upd<_Float16, 4>(a, s) : launch_upd<_Float16, 3>(a, s);
   return state_len == 4 ? launch_upd<float, 4>(a, s) : launch_upd<float, 3>(a, s);
 }

@@ -54,14 +54,14 @@ extern "C" int gdn_conv_state_commit(void *pool, const int64_t *slot_ids, int64_
   if (n_seqs < 0 || C <= 0 || S <= 0 || L <= S || n_seqs > 65535)
     return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_conv_state_commit: bad sizes n_seqs=%d C=%d S=%d L=%d", n_seqs, C,
                 S, L);
-  if (dtype != GDN_DTYPE_BF16 && dtype != GDN_DTYPE_F32)
-    return fail(GDN_ERR_UNSUPPORTED, "gdn_conv_state_commit: dtype %d (bf16 or fp32)", dtype);
+  if (!valid_dtype(dtype))
+    return fail(GDN_ERR_UNSUPPORTED, "gdn_conv_state_commit: dtype %d (bf16, fp16 or fp32)", dtype);
   if (n_seqs == 0) return ok();
   if (!pool || !slot_ids || !hist || !accepted_len || pool_rows < 0)
     return fail(GDN_ERR_INVALID_ARGUMENT, "gdn_conv_state_commit: null pointer or negative pool_rows");
   const dim3 grid((C + COMMIT_NT - 1) / COMMIT_NT, n_seqs);
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == GDN_DTYPE_BF16)
+  if (dtype != GDN_DTYPE_F32)  // a 2-byte copy: bf16 and fp16 alike
     hipLaunchKernelGGL(conv_commit_kernel<uint16_t>, grid, dim3(COMMIT_NT), 0, st, static_cast<uint16_t *>(pool),
                        slot_ids, static_cast<int64_t>(pool_rows), static_cast<const uint16_t *>(hist), accepted_len,
                        C, S, L, L - S);

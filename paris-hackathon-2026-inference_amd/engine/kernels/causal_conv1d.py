@@ -81,8 +81,8 @@ def causal_conv1d_fn(
     """
     dev = _lib.require_gpu(x, weight, bias, initial_states, conv_states, final_states_out)
     dt = x.dtype
-    if dt not in (torch.bfloat16, torch.float32):
-        raise TypeError(f"causal_conv1d_fn: dtype {dt} unsupported (bf16 or fp32)")
+    if dt not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError(f"causal_conv1d_fn: dtype {dt} unsupported (bf16, fp16 or fp32)")
     w = weight.to(dt).contiguous()
     bb = None if bias is None else bias.to(dt).contiguous()
     xt, xs, b, t, was_bct = _stream_view(x)
@@ -109,7 +109,10 @@ def causal_conv1d_fn(
         in_idx = idx
         if has_initial_state is not None:
             base = idx if idx is not None else torch.arange(n_seqs, device=dev)
-            in_idx = torch.where(has_initial_state.to(dev).bool(), base, torch.full_like(base, -1))
+            has = has_initial_state.to(dev).bool().reshape(-1)
+            if idx is not None:  # a repeated slot id neither reads nor writes: decide it on the unmasked ids
+                has = has & ~(base[:, None] == base[None, :]).tril(-1).any(dim=1)
+            in_idx = torch.where(has, base, torch.full_like(base, -1))
     if initial_states is not None:
         if initial_states.shape[:2] != (n_seqs, c):
             raise ValueError(f"initial_states must be [{n_seqs}, {c}, S]")
@@ -157,8 +160,8 @@ def causal_conv1d_update(
     x3 = x.unsqueeze(-1) if squeeze else x
     b, c, t = x3.shape
     dt = x.dtype
-    if dt not in (torch.bfloat16, torch.float32):
-        raise TypeError(f"causal_conv1d_update: dtype {dt} unsupported (bf16 or fp32)")
+    if dt not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError(f"causal_conv1d_update: dtype {dt} unsupported (bf16, fp16 or fp32)")
     if conv_state.dtype != dt or not conv_state.is_contiguous() or conv_state.shape[1] != c:
         raise ValueError("conv_state must be a contiguous [*, C, S] tensor of x's dtype")
     idx = _lib.as_index(conv_state_indices, dev)

@@ -56,8 +56,8 @@ def gdn_conv_state_commit(pool: torch.Tensor, slot_ids: torch.Tensor, hist: torc
     engine/runtime/spec_decode.py:81-87 leaves unimplemented.
     """
     dev = _lib.require_gpu(pool, hist)
-    if pool.dtype != hist.dtype or pool.dtype not in (torch.bfloat16, torch.float32):
-        raise TypeError("pool and hist must share a dtype, bf16 or fp32")
+    if pool.dtype != hist.dtype or pool.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError("pool and hist must share a dtype, bf16, fp16 or fp32")
     if not pool.is_contiguous() or not hist.is_contiguous():
         raise ValueError("pool and hist must be contiguous")
     n, c, length = hist.shape

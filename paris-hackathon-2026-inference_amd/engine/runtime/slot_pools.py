@@ -41,7 +41,7 @@ GDN_PAD_SLOT = -1
 class GDNSlotPools:
     """The GDN half of a slot-pool cache.
 
-    ``conv_pools[layer]`` ``[slots, C, S]`` (bf16 or fp32) and
+    ``conv_pools[layer]`` ``[slots, C, S]`` (bf16, fp16 or fp32) and
     ``rec_pools[layer]`` ``[slots, Hv, K, V]`` fp32 are the pools of each GDN
     layer (the cache's own tensors, not copies).  ``max_batch`` bounds the
     rows of one forward (graph buckets included).
@@ -60,8 +60,8 @@ class GDNSlotPools:
             r, c = self.rec[i], self.conv[i]
             if r.dtype != torch.float32 or r.dim() != 4 or not r.is_contiguous():
                 raise ValueError(f"layer {i}: recurrent pool must be contiguous fp32 [slots, Hv, K, V]")
-            if c.dim() != 3 or not c.is_contiguous() or c.dtype not in (torch.bfloat16, torch.float32):
-                raise ValueError(f"layer {i}: conv pool must be contiguous [slots, C, S] bf16 or fp32")
+            if c.dim() != 3 or not c.is_contiguous() or c.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+                raise ValueError(f"layer {i}: conv pool must be contiguous [slots, C, S] bf16, fp16 or fp32")
             if r.shape[0] != self.num_slots or c.shape[0] != self.num_slots:
                 raise ValueError(f"layer {i}: pools hold different slot counts")
             if r.device != self.device or c.device != self.device:

@@ -87,7 +87,7 @@ def test_conv_rejects_bad_shapes(lib):
     assert call(width=5) == 2
     assert call(sl=5) == 2
     assert call(x=8) == 1                          # misaligned
-    assert call(dt=2) == 2                         # fp16 not built
+    assert call(dt=3) == 2                         # no such dtype (0 fp32, 1 bf16, 2 fp16)
     assert call(so=256, sor=0) == 1                # final-state rows do not cover the sequence
 
 

@@ -4,7 +4,9 @@ with the CPU oracle and with HF's golden vectors, through the C ABI.
 fp32 cases are checked to 1e-5.  bf16 outputs are checked to
 |y - y_ref| <= 2e-2 * max(1, |y_ref|): the north star's 2e-2 abs bound, widened
 to one bf16 ulp (2^-7 relative) for the |y| > 1 values SiLU produces here.
-Window/state tensors are copies of inputs, so they are checked bit-exactly."""
+fp16 outputs (one rounding of an fp32 result, 2^-11 relative) are checked to
+|y - y_ref| <= 1e-3 * max(1, |y_ref|).  Window/state tensors are copies of
+inputs, so they are checked bit-exactly."""
 import numpy as np
 import pytest
 import torch
@@ -28,11 +30,23 @@ def bf16_close(y, y_ref):
     return err.max() <= 2e-2
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def f16_close(y, y_ref):
+    err = np.abs(np64(y) - y_ref) / np.maximum(1.0, np.abs(y_ref))
+    return err.max() <= 1e-3
+
+
+def close_for(dtype):
+    return f16_close if dtype == torch.float16 else bf16_close
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_fn_matches_hf_golden(golden, dtype):
     x = torch.from_numpy(golden["conv_fn.x"]).to(DEV, dtype)
     w = torch.from_numpy(golden["conv_fn.w"]).to(DEV, dtype)
     close = (lambda a, b: np.abs(np64(a) - b).max() < 1e-5) if dtype == torch.float32 else bf16_close
+    # (the golden input is fp32: rounding it to fp16 moves y by more than
+    # fp16's own output bound, so fp16 is held to the bf16 bound here and to
+    # its own bound on fp16 inputs below)
     y = causal_conv1d_fn(x, w, None, activation="silu")
     assert y.shape == x.shape and y.dtype == dtype
     assert close(y, golden["conv_fn.y"])
@@ -50,26 +64,27 @@ def test_update_matches_hf_golden(golden):
     assert np.array_equal(st.cpu().numpy(), golden["conv_upd.state_after"])
 
 
-def test_config3_varlen_conv_with_history_and_pool():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_config3_varlen_conv_with_history_and_pool(dtype):
     c = configs.config3()
     cu = c["cu_seqlens"]
     n = cu.numel() - 1
     gen = torch.Generator().manual_seed(33)
-    hist = torch.randn(n, configs.CONV_DIM, 4, generator=gen).to(torch.bfloat16)
+    hist = torch.randn(n, configs.CONV_DIM, 4, generator=gen).to(dtype)
     num_slots = 24
     slots = torch.randperm(num_slots, generator=gen)[:n]
-    pool0 = torch.randn(num_slots, configs.CONV_DIM, 4, generator=gen).to(torch.bfloat16)
+    pool0 = torch.randn(num_slots, configs.CONV_DIM, 4, generator=gen).to(dtype)
     pool0[slots] = hist
-    x = c["x"]
-    y_ref, fin_ref = conv.causal_conv1d_varlen(x.float().numpy(), c["conv_w"].float().numpy(), cu.numpy(),
+    x, cw = c["x"].to(dtype), c["conv_w"].to(dtype)
+    y_ref, fin_ref = conv.causal_conv1d_varlen(x.float().numpy(), cw.float().numpy(), cu.numpy(),
                                                activation="silu", initial_states=hist.float().numpy(),
                                                dtype=np.float32)
     pool = pool0.to(DEV)
-    y = causal_conv1d_fn(x.to(DEV), c["conv_w"].to(DEV), None, activation="silu", cu_seqlens=cu.to(DEV),
+    y = causal_conv1d_fn(x.to(DEV), cw.to(DEV), None, activation="silu", cu_seqlens=cu.to(DEV),
                          conv_states=pool, cache_indices=slots.to(DEV))
-    assert y.shape == x.shape
-    assert bf16_close(y, y_ref)
-    assert np.abs(np64(y) - y_ref).mean() < 2e-3
+    assert y.shape == x.shape and y.dtype == dtype and pool.dtype == dtype
+    assert close_for(dtype)(y, y_ref)
+    assert np.abs(np64(y) - y_ref).mean() < (2e-3 if dtype == torch.bfloat16 else 2e-4)
     assert np.array_equal(np64(pool[slots.to(DEV)]), fin_ref)
     keep = torch.ones(num_slots, dtype=torch.bool)
     keep[slots] = False
@@ -106,13 +121,14 @@ def test_has_initial_state_false_starts_from_zeros():
     assert np.array_equal(np64(pool[0]), f0[0]) and np.array_equal(np64(pool[1]), f1[0])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("t", [1, 2, 4])
-def test_update_pool_indices_and_negative_slot(t):
+def test_update_pool_indices_and_negative_slot(t, dtype):
     gen = torch.Generator().manual_seed(10 + t)
     b, c = 4, configs.CONV_DIM
-    x = torch.randn(b, c, t, generator=gen).to(torch.bfloat16)
-    w = torch.randn(c, 4, generator=gen).to(torch.bfloat16)
-    pool0 = torch.randn(6, c, 4, generator=gen).to(torch.bfloat16)
+    x = torch.randn(b, c, t, generator=gen).to(dtype)
+    w = torch.randn(c, 4, generator=gen).to(dtype)
+    pool0 = torch.randn(6, c, 4, generator=gen).to(dtype)
     idx = torch.tensor([4, -1, 0, 2])
     states = torch.zeros(b, c, 4)
     states[[0, 2, 3]] = pool0[[4, 0, 2]].float()
@@ -120,7 +136,7 @@ def test_update_pool_indices_and_negative_slot(t):
                                               activation="silu")
     pool = pool0.to(DEV)
     y = causal_conv1d_update(x.to(DEV), pool, w.to(DEV), None, "silu", conv_state_indices=idx.to(DEV))
-    assert bf16_close(y, y_ref)
+    assert y.dtype == dtype and close_for(dtype)(y, y_ref)
     assert np.array_equal(np64(pool[[4, 0, 2]]), st_ref[[0, 2, 3]])
     assert torch.equal(pool[[1, 3, 5]].cpu(), pool0[[1, 3, 5]])
 
@@ -184,20 +200,42 @@ def test_conv_state_commit_matches_update_over_the_accepted_prefix():
     assert torch.equal(pool[[1, 2, 4, 5]].cpu(), pool0[[1, 2, 4, 5]])  # a = 0 (row 4), unused slots
 
 
-def test_update_with_repeated_slot_ids_advances_a_slot_once():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_update_with_repeated_slot_ids_advances_a_slot_once(dtype):
     """ids [s, s, t] with identical rows 0 and 1: slot s's window moves by one
     token, row 1 runs as a padding row (zero window, nothing written)."""
     gen = torch.Generator().manual_seed(72)
     c = 512
-    pool0 = torch.randn(4, c, 4, generator=gen).to(torch.bfloat16)
-    x = torch.randn(2, c, 1, generator=gen).to(torch.bfloat16)
+    pool0 = torch.randn(4, c, 4, generator=gen).to(dtype)
+    x = torch.randn(2, c, 1, generator=gen).to(dtype)
     x = torch.cat([x[:1], x[:1], x[1:]])  # rows 0 and 1 identical
-    w = torch.randn(c, 4, generator=gen).to(torch.bfloat16)
+    w = torch.randn(c, 4, generator=gen).to(dtype)
+    close = close_for(dtype)
     pool = pool0.to(DEV)
     y = causal_conv1d_update(x.to(DEV), pool, w.to(DEV), None, "silu", conv_state_indices=torch.tensor([2, 2, 0]).to(DEV))
     y0, st0 = conv.causal_conv1d_update(np64(x[:1]), np64(pool0[2:3]), np64(w))
     y1, _ = conv.causal_conv1d_update(np64(x[1:2]), np.zeros((1, c, 4)), np64(w))
     y2, st2 = conv.causal_conv1d_update(np64(x[2:3]), np64(pool0[0:1]), np64(w))
-    assert bf16_close(y[0:1], y0) and bf16_close(y[1:2], y1) and bf16_close(y[2:3], y2)
+    assert close(y[0:1], y0) and close(y[1:2], y1) and close(y[2:3], y2)
     assert np.array_equal(np64(pool[2])[None], st0) and np.array_equal(np64(pool[0])[None], st2)
     assert torch.equal(pool[[1, 3]].cpu(), pool0[[1, 3]])
+
+
+def test_fn_repeated_slot_id_with_mismatched_has_initial_state():
+    """Prefill conv on a pool with ids [3, 3] and has_initial_state [False,
+    True]: row 0 alone owns slot 3 (zero history, its final window written),
+    row 1 runs from a zero window and writes nothing."""
+    gen = torch.Generator().manual_seed(74)
+    c = 256
+    x = torch.randn(2, c, 6, generator=gen).to(torch.bfloat16)
+    w = torch.randn(c, 4, generator=gen).to(torch.bfloat16)
+    pool0 = torch.randn(4, c, 4, generator=gen).to(torch.bfloat16)
+    pool = pool0.to(DEV)
+    y = causal_conv1d_fn(x.to(DEV), w.to(DEV), activation="silu", conv_states=pool,
+                         cache_indices=torch.tensor([3, 3], device=DEV),
+                         has_initial_state=torch.tensor([False, True], device=DEV))
+    y0, f0 = conv.causal_conv1d_fn(np64(x[:1]), np64(w))
+    y1, _ = conv.causal_conv1d_fn(np64(x[1:]), np64(w))
+    assert bf16_close(y[:1], y0) and bf16_close(y[1:], y1)
+    assert np.array_equal(np64(pool[3]), f0[0])
+    assert torch.equal(pool[:3].cpu(), pool0[:3])
