@@ -740,8 +740,8 @@ def bench_out_proj(torch, sets=16, reps=100):
             "us": t_ours, "hipblaslt_us": t_lt, "speedup": t_lt / t_ours,
             "roofline": {"bound": "hbm", "achieved": byts / t_ours / 1e3, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                          "frac": byts / (t_ours * 1e-6) / HBM_PEAK, "bytes_per_call": byts,
-                         "kernels": "gdn::out_proj_partial_kernel + gdn::out_proj_sum_kernel<8> (4 MiB of fp32 "
-                                    "partials written and read besides)"}}
+                         "kernels": "gdn::out_proj_partial_kernel (4 splits of 1024) + gdn::out_proj_sum_kernel<4> "
+                                    "(2 MiB of fp32 partials written and read besides)"}}
 
 
 def bench_layer_decode(torch, layers=4, reps=100, batch=64):

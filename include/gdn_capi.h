@@ -280,7 +280,8 @@ int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w_qkv, const
 
 /*
  * Decode-step output projection of the GDN layer:  y = x W^T  (bf16, fp32
- * sums), with K split over workgroups (512 of K each); a second kernel adds
+ * sums), with K split over workgroups (1024 of K each when K is a multiple of
+ * 1024, else 512); a second kernel adds
  * the fp32 partial sums in split order, so results do not depend on
  * scheduling.  One row with K / 512 in {1, 2, 4, 8} runs as a single GEMV
  * kernel (the workspace is then not touched).
@@ -309,7 +310,7 @@ int gdn_out_proj_decode(const void *x, int64_t x_stride, const void *w, int32_t 
  * GPU, held from the library's first use on that GPU until the process
  * ends), so the caller passes only x, w and y.  Calls that need more partial
  * sums than that (gdn_out_proj_workspace_bytes(M, K, N) > the maximum; 64
- * rows at K = 4096, N = 2048 need 4 MiB) fail with GDN_ERR_UNSUPPORTED.  All
+ * rows at K = 4096, N = 2048 need 2 MiB) fail with GDN_ERR_UNSUPPORTED.  All
  * calls on one GPU share the scratch: calls that overlap on one GPU (on two
  * streams) race.  The stream must belong to the current device.  Results are
  * bit-identical to gdn_out_proj_decode's.

@@ -76,8 +76,15 @@ struct ProjShape {
   static_assert(CG * KQ == IP_WAVES && KS % NPH == 0 && 64 % CH == 0 && (KQ * CH) % IP_WAVES == 0, "shape");
   static_assert(LDS_BLOCKS * 16 <= 128 * 1024 && KQ * CG * 4 * 64 <= LDS_BLOCKS, "LDS");
 };
-using OutProjShape = ProjShape<4, 4, 4, 1>;      // out_proj: 64 columns x 512 of K per workgroup
-constexpr int OP_KSPAN = 4 * OutProjShape::KPART;  // K per workgroup (512)
+// out_proj workgroups: 64 columns x 512 of K, or, when K is a multiple of
+// 1024, 32 columns x 1024 of K -- half the splits, so half the fp32
+// partial sums written and read back (2 MiB each way instead of 4 for the
+// Qwen3.5-MoE layer at 64 rows), for twice the staged rows per workgroup
+using OutProjShape = ProjShape<4, 4, 4, 1>;
+using OutProjShapeWide = ProjShape<2, 8, 4, 1>;
+constexpr int OP_KSPAN = OutProjShape::KQ * OutProjShape::KPART;            // 512
+constexpr int OP_KSPAN_WIDE = OutProjShapeWide::KQ * OutProjShapeWide::KPART;  // 1024
+inline int op_kspan(int K) { return K % OP_KSPAN_WIDE == 0 ? OP_KSPAN_WIDE : OP_KSPAN; }
 constexpr int OP_MAX_SPLIT = 16;                  // workgroups per column block (K <= 8192)
 constexpr int OP_RED_NT = 256;                    // threads per workgroup of the partials' sum
 
@@ -238,10 +245,17 @@ __device__ __forceinline__ void conv_epilogue(const InProjArgs &a, const f32x4_t
 // ---------------------------------------------------------------------------
 // Input projections, rows held in registers ("x-stationary").
 //
-// The four matrices are cut into tiles of 16 output columns (qkv, z, b, a in
-// that order: 772 tiles for the Qwen3.5-MoE layer); workgroup b of G takes
-// tiles b, b + G, ... (G = max(256, tiles / 4), so every CU works and a
-// workgroup has at most XS_MAX_TILES).  Its 16 waves split K: wave w holds
+// The qkv and z matrices are cut into tiles of 16 output columns (768 tiles
+// for the Qwen3.5-MoE layer); workgroup b of G takes tiles b, b + G, ...
+// (G = max(256, tiles / 4), so every CU works and a workgroup has at most
+// XS_MAX_TILES).  The b and a projections (64 columns there) are not tiled:
+// as 4 more tiles they gave 4 workgroups a fourth tile that set the
+// kernel's end.  Workgroup b instead computes columns b, b + G, ... of
+// [b | a] as one-column products (an MFMA A operand whose other 15 rows
+// are zero) from the hidden rows already in its registers and the column's
+// weight row fetched into LDS at the start, in the time waves 4-15 wait for
+// the first tile's epilogue; wave 4 adds the waves' partial sums in wave
+// order -- the tile path's arithmetic, so the values are the same.  Its 16 waves split K: wave w holds
 // K / 16 columns of all 64 hidden rows as MFMA B operands in registers
 // (64 VGPRs at K = 2048), loaded once, and streams the matching K / 16 of
 // each tile's 16 weight rows, the next tile's requested as soon as the
@@ -254,6 +268,8 @@ __device__ __forceinline__ void conv_epilogue(const InProjArgs &a, const f32x4_t
 constexpr int XS_WAVES = 16;
 constexpr int XS_MAX_TILES = 4;
 constexpr int XS_MIN_WGS = 256;  // MI355X CUs
+constexpr int XS_BA_MAX = 2;     // b / a columns per workgroup (G >= 32 for the 64 of Qwen3.5-MoE)
+constexpr int XS_K_MAX = 2048;   // the largest K built
 
 struct XsTile {
   int mat, col, live;  // matrix (0 qkv, 1 z, 2 b, 3 a), first column, columns in the matrix (<= 16)
@@ -274,6 +290,44 @@ __device__ __forceinline__ XsTile xs_tile(const InProjArgs &a, const int (&tiles
   return t;
 }
 
+// The b / a columns: this wave's K slice of each column's dot products with
+// the 64 rows (lane (c, 0) of row tile t ends with row 16 t + c in element 0),
+// into bared; then wave 4 adds the waves' partials per row, in wave order.
+template <int NW, int KSW>
+__device__ __forceinline__ void xs_ba_partials(const u32x4_t (*baw)[XS_K_MAX / 8], float (*bared)[NW][64],
+                                               const u32x4_t (&xr)[4][KSW], int nbc, int kw, int wave, int lane) {
+  const int c = lane & 15, g = lane >> 4;
+  for (int ci = 0; ci < nbc; ++ci) {
+    f32x4_t acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KSW; ++s) {
+      const u32x4_t wf = c == 0 ? baw[ci][kw / 8 + 4 * s + g] : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[t] = mfma16(wf, xr[t][s], acc[t]);
+    }
+    if (g == 0) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) bared[ci][wave][16 * t + c] = acc[t][0];
+    }
+  }
+}
+
+template <int NW>
+__device__ __forceinline__ void xs_ba_finish(const InProjArgs &a, const float (*bared)[NW][64], int nbc, int G, int m0,
+                                             int lane) {  // wave 4, lane = row
+  for (int ci = 0; ci < nbc; ++ci) {
+    float o = bared[ci][0][lane];
+    for (int q = 1; q < NW; ++q) o += bared[ci][q][lane];
+    const int jj = static_cast<int>(blockIdx.x) + G * ci;
+    const bool is_b = jj < a.n[2];
+    const int nmat = is_b ? a.n[2] : a.n[3];
+    if (m0 + lane < a.M)
+      (is_b ? a.y[2] : a.y[3])[static_cast<int64_t>(m0 + lane) * nmat + (is_b ? jj : jj - a.n[2])] = f32_to_bf16_bits(o);
+  }
+}
+
 // NW waves, KSW k-steps (of 32) per wave: K = NW * 32 * KSW.
 template <int NW, int KSW>
 __global__ __launch_bounds__(64 * NW) void in_proj_xs_kernel(InProjArgs a) {
@@ -282,16 +336,24 @@ __global__ __launch_bounds__(64 * NW) void in_proj_xs_kernel(InProjArgs a) {
   __shared__ f32x4_t red[NW][4][64];                       // partial products of one tile
   __shared__ u32x4_t win[XS_MAX_TILES][4][2][64];          // conv windows by tile, row tile, half, lane: 32 KiB
   __shared__ u32x4_t tap[XS_MAX_TILES][64];                // lanes 0-7 taps (2 channels each), 8-9 bias
+  // (a fixed bound: with the bound K / 8 on this LDS-DMA target, hipcc emitted
+  // no host launch stub for the kernel and the library failed to load)
+  static_assert(K <= XS_K_MAX, "K");
+  __shared__ u32x4_t baw[XS_BA_MAX][XS_K_MAX / 8];         // weight rows of this workgroup's b / a columns
+  __shared__ float bared[XS_BA_MAX][NW][64];               // their partial sums by wave and row
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15, g = lane >> 4;
   const int m0 = blockIdx.y * IP_ROWS;
   const int mb = min(IP_ROWS, a.M - m0);
-  const int tiles[4] = {(a.n[0] + 15) / 16, (a.n[1] + 15) / 16, (a.n[2] + 15) / 16, (a.n[3] + 15) / 16};
-  const int ntiles = tiles[0] + tiles[1] + tiles[2] + tiles[3];
+  const int tiles[4] = {(a.n[0] + 15) / 16, (a.n[1] + 15) / 16, 0, 0};  // b and a: columns, below
+  const int ntiles = tiles[0] + tiles[1];
   const int G = gridDim.x;
   const int nt = __builtin_amdgcn_readfirstlane((ntiles - static_cast<int>(blockIdx.x) + G - 1) / G);  // <= XS_MAX_TILES
+  // this workgroup's columns of [b | a]: blockIdx.x + G ci, ci < nbc (<= XS_BA_MAX: checked on the host)
+  const int nba = a.n[2] + a.n[3];
+  const int nbc = __builtin_amdgcn_readfirstlane(min(XS_BA_MAX, (nba - static_cast<int>(blockIdx.x) + G - 1) / G));
   const int kw = wave * 32 * KSW;  // this wave's columns of K
 
   // slot id of the row this lane finishes (waves 0-3: row tile = wave)
@@ -357,8 +419,19 @@ __global__ __launch_bounds__(64 * NW) void in_proj_xs_kernel(InProjArgs a) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, &tap[i][0], 16, lane < 10 ? (t.col + 8 * (lane - 8)) * 2 : IP_OOB, 0,
                                                  0, 0);
     }
+    for (int ci = 0; ci < nbc; ++ci) {  // the b / a weight rows, 1 KiB per instruction
+      const int jj = static_cast<int>(blockIdx.x) + G * ci;
+      const uint16_t *wrow = jj < a.n[2] ? a.w[2] + static_cast<int64_t>(jj) * K : a.w[3] + static_cast<int64_t>(jj - a.n[2]) * K;
+      const auto rr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(wrow), 0, K * 2, BUF_DWORD3);
+#pragma unroll
+      for (int p = 0; p < K / 512; ++p)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, &baw[ci][64 * p], 16, (512 * p + 8 * lane) * 2, 0, 0, 0);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
+
+  auto ba_partials = [&]() { xs_ba_partials<NW, KSW>(baw, bared, xr, nbc, kw, wave, lane); };
+  auto ba_finish = [&]() { xs_ba_finish<NW>(a, bared, nbc, G, m0, lane); };
 
   for (int i = 0; i < nt; ++i) {
     f32x4_t acc[4];
@@ -381,6 +454,8 @@ __global__ __launch_bounds__(64 * NW) void in_proj_xs_kernel(InProjArgs a) {
         __builtin_amdgcn_s_waitcnt(ip_vmcnt(0));
     }
     __syncthreads();
+    if (i == 0 && wave >= 4) ba_partials();  // (waves 0-3 after their epilogue)
+    if (i == 1 && wave == 4) ba_finish();
     if (wave < 4) {
       // row tile `wave`: lane (c, g) holds row me, columns col + 4 g .. + 3; the
       // partials in wave order, four read at a time (the registers hold x)
@@ -414,8 +489,16 @@ __global__ __launch_bounds__(64 * NW) void in_proj_xs_kernel(InProjArgs a) {
         }
       }
     }
+    if (i == 0 && wave < 4) ba_partials();
     __syncthreads();  // the partials are consumed: the next tile's may go in
   }
+  if (nt == 0 && nbc > 0) {  // no tile: the b / a columns alone
+    __builtin_amdgcn_s_waitcnt(ip_vmcnt(0));
+    __syncthreads();
+    ba_partials();
+    __syncthreads();
+  }
+  if (nt <= 1 && wave == 4) ba_finish();
 }
 
 // One or two rows (the smallest decode batches): the projection is a GEMV stream.
@@ -531,18 +614,19 @@ struct OutProjArgs {
   int64_t xs;
   const uint16_t *w;  // [N, K] bf16, rows contiguous
   int M, K, N;
-  int split, ncb;     // workgroups per column block (K / 512), column blocks (N / 64)
+  int split, ncb;     // workgroups per column block (K / 512 or K / 1024), column blocks (N / 64 or N / 32)
   float *part;        // [split][row blocks][64][N] fp32 partial sums
   uint16_t *y;        // [M, N] bf16, row stride ys elements
   int64_t ys;
 };
 
-// Partial block (64 rows x 64 columns, 512 of K) of workgroup (column block
-// cb, split sp, row block blockIdx.y).  A column block's split workgroups
-// are bid = cb + ncb sp.
+// Partial block (64 rows x S::COLS columns, S::KQ S::KPART of K) of
+// workgroup (column block cb, split sp, row block blockIdx.y).  A column
+// block's split workgroups are bid = cb + ncb sp.
+template <class S>
 __global__ __launch_bounds__(64 * IP_WAVES) void out_proj_partial_kernel(OutProjArgs a) {
-  using S = OutProjShape;
-  __shared__ u32x4_t xl[S::LDS_BLOCKS];  // the rows' 512 columns of K: 64 KiB
+  constexpr int KSPAN = S::KQ * S::KPART;
+  __shared__ u32x4_t xl[S::LDS_BLOCKS];  // the rows' KSPAN columns of K: 64 or 128 KiB
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -552,7 +636,7 @@ __global__ __launch_bounds__(64 * IP_WAVES) void out_proj_partial_kernel(OutProj
   const int m0 = mblk * IP_ROWS;
   const int mb = min(IP_ROWS, a.M - m0);
   const int col = cb * S::COLS + 16 * cg;
-  const int k0 = sp * OP_KSPAN;
+  const int k0 = sp * KSPAN;
   const auto rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.w) + static_cast<int64_t>(col) * a.K, 0,
                                                     16 * a.K * 2, BUF_DWORD3);
   const uint16_t *xbase = a.x + static_cast<int64_t>(m0) * a.xs + k0;
@@ -565,7 +649,10 @@ __global__ __launch_bounds__(64 * IP_WAVES) void out_proj_partial_kernel(OutProj
   __builtin_amdgcn_sched_barrier(0);
   const f32x4_t o = proj_phases<S, 0>(xl, wr, [](int) {}, wave, lane);
 
-  // lane (c, g) of wave (cg, kq): row 16 kq + c, columns col + 4 g .. + 3
+  // lane (c, g) of wave (cg, kq), kq < 4: row 16 kq + c, columns col + 4 g .. + 3
+  // (waves of the further K parts hold no row tile: with KQ = 8 they would
+  // address rows 64-127, the next block's)
+  if (kq >= 4) return;
   const int c = lane & 15, g = lane >> 4;
   const int64_t prow = static_cast<int64_t>(sp * nmb + mblk) * IP_ROWS + 16 * kq + c;
   *reinterpret_cast<f32x4_t *>(a.part + prow * a.N + col + 4 * g) = o;
@@ -649,7 +736,7 @@ extern "C" size_t gdn_out_proj_workspace_bytes(int32_t M, int32_t K, int32_t N) 
   using namespace gdn;
   if (M <= 0 || K <= 0 || N <= 0) return 0;
   const int64_t nmb = (M + IP_ROWS - 1) / IP_ROWS;
-  const int64_t split = (K + OP_KSPAN - 1) / OP_KSPAN;
+  const int64_t split = (K + op_kspan(K) - 1) / op_kspan(K);
   return static_cast<size_t>(split * nmb * IP_ROWS * N * 4);
 }
 
@@ -685,8 +772,9 @@ extern "C" int gdn_out_proj_decode(const void *x, int64_t x_stride, const void *
   args.M = M;
   args.K = K;
   args.N = N;
-  args.split = K / OP_KSPAN;
-  args.ncb = N / OutProjShape::COLS;
+  const bool wide = op_kspan(K) == OP_KSPAN_WIDE;
+  args.split = K / op_kspan(K);
+  args.ncb = N / (wide ? OutProjShapeWide::COLS : OutProjShape::COLS);
   args.part = static_cast<float *>(workspace);
   args.y = static_cast<uint16_t *>(y);
   args.ys = y_stride;
@@ -702,7 +790,10 @@ extern "C" int gdn_out_proj_decode(const void *x, int64_t x_stride, const void *
     return check_launch("gdn_out_proj_decode");
   }
   const dim3 grid(static_cast<unsigned>(args.ncb * args.split), static_cast<unsigned>((M + IP_ROWS - 1) / IP_ROWS));
-  hipLaunchKernelGGL(out_proj_partial_kernel, grid, dim3(64 * IP_WAVES), 0, s, args);
+  if (wide)
+    hipLaunchKernelGGL(out_proj_partial_kernel<OutProjShapeWide>, grid, dim3(64 * IP_WAVES), 0, s, args);
+  else
+    hipLaunchKernelGGL(out_proj_partial_kernel<OutProjShape>, grid, dim3(64 * IP_WAVES), 0, s, args);
   const int64_t quads = static_cast<int64_t>(M) * (N / 4);
   const dim3 rgrid(static_cast<unsigned>((quads + OP_RED_NT - 1) / OP_RED_NT));
   switch (args.split) {
@@ -843,8 +934,9 @@ extern "C" int gdn_in_proj_decode(const void *x, int64_t x_stride, const void *w
       launch_gemv<2>(args, grid.x, K / 512, s);
     return check_launch("gdn_in_proj_decode");
   }
-  const int ntiles = (n_qkv + 15) / 16 + (n_z + 15) / 16 + (n_b + 15) / 16 + (n_a + 15) / 16;
-  const int gx = std::min(ntiles, std::max(XS_MIN_WGS, (ntiles + XS_MAX_TILES - 1) / XS_MAX_TILES));
+  const int ntiles = (n_qkv + 15) / 16 + (n_z + 15) / 16;  // b and a go by columns, XS_BA_MAX per workgroup
+  const int gx = std::max(std::min(ntiles, std::max(XS_MIN_WGS, (ntiles + XS_MAX_TILES - 1) / XS_MAX_TILES)),
+                          (n_b + n_a + XS_BA_MAX - 1) / XS_BA_MAX);
   const dim3 xgrid(static_cast<unsigned>(gx), grid.y);
   switch (K) {
     case 1024: hipLaunchKernelGGL((in_proj_xs_kernel<XS_WAVES, 2>), xgrid, dim3(64 * XS_WAVES), 0, s, args); break;

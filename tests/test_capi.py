@@ -222,10 +222,13 @@ def _outproj_call(lib, **over):
 
 
 def test_out_proj_workspace_is_host_arithmetic(lib):
-    # the partial sums: [K/512 splits][row blocks][64 rows][N] fp32
-    assert lib.gdn_out_proj_workspace_bytes(64, 4096, 2048) == 8 * 64 * 2048 * 4
-    assert lib.gdn_out_proj_workspace_bytes(65, 4096, 2048) == 8 * 2 * 64 * 2048 * 4
-    assert lib.gdn_out_proj_workspace_bytes(1, 2048, 64 * 70) == 4 * 64 * 64 * 70 * 4
+    # the partial sums [splits][row blocks][64 rows][N] fp32, one split per
+    # 1024 of K when K is a multiple of 1024, else per 512
+    assert lib.gdn_out_proj_workspace_bytes(64, 4096, 2048) == 4 * 64 * 2048 * 4
+    assert lib.gdn_out_proj_workspace_bytes(64, 2048, 1024) == 2 * 64 * 1024 * 4
+    assert lib.gdn_out_proj_workspace_bytes(64, 3072, 2048) == 3 * 64 * 2048 * 4
+    assert lib.gdn_out_proj_workspace_bytes(65, 8192, 2048) == 8 * 2 * 64 * 2048 * 4
+    assert lib.gdn_out_proj_workspace_bytes(7, 1536, 128) == 3 * 64 * 128 * 4
     assert lib.gdn_out_proj_workspace_bytes(0, 4096, 2048) == 0
 
 
@@ -239,7 +242,7 @@ def test_out_proj_decode_rejects_bad_arguments(lib):
     assert _outproj_call(lib, x=24) == 1                   # misaligned
     assert _outproj_call(lib, ws=24) == 1                  # workspace not 16-byte aligned
     assert _outproj_call(lib, ws=None) == 1
-    assert _outproj_call(lib, ws_bytes=1 << 20) == 1       # too small for 64 rows
+    assert _outproj_call(lib, k=3072, xs=3072, ws_bytes=1 << 20) == 1  # too small for 64 rows' partials
     assert "workspace" in lib.gdn_last_error_string().decode()
     assert _outproj_call(lib, m=0) == 0                    # nothing to do, nothing launched
 
@@ -252,8 +255,8 @@ def test_out_proj_python_gate():
 
 
 def test_out_proj_noalloc_rejects_sizes_beyond_its_scratch(lib):
-    """Host-side check, no launch: 256 rows at K = 4096, N = 2048 need 16 MiB
+    """Host-side check, no launch: 512 rows at K = 3072, N = 2048 need 12 MiB
     of partial sums, past the 8 MiB built-in scratch."""
-    st = lib.gdn_out_proj_decode_noalloc(16, 4096, 16, 256, 4096, 2048, 16, 2048, None)
+    st = lib.gdn_out_proj_decode_noalloc(16, 3072, 16, 512, 3072, 2048, 16, 2048, None)
     assert st == 2  # GDN_ERR_UNSUPPORTED
     assert b"scratch" in lib.gdn_last_error_string()

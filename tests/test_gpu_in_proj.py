@@ -270,7 +270,8 @@ def run_out(x, w):
 
 
 @pytest.mark.parametrize("m,k,n", [(64, 4096, 2048), (1, 4096, 2048), (5, 4096, 2048), (100, 4096, 2048),
-                                   (256, 4096, 2048), (3, 2048, 1024), (7, 512, 64), (9, 1536, 128),
+                                   (256, 4096, 2048), (3, 2048, 1024), (40, 1024, 192), (7, 512, 64),
+                                   (9, 1536, 128), (6, 3072, 256), (70, 8192, 128),
                                    (1, 2048, 1024), (1, 512, 64), (1, 1536, 128)])
 def test_out_proj_matches_oracle(m, k, n):
     """Against the exact sum: one bf16 ulp plus the fp32 summation error (one

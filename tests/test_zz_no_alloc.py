@@ -15,12 +15,16 @@ pytestmark = [pytest.mark.gpu,
 DEV = "cuda"
 
 
-def test_noalloc_out_proj_matches_the_workspace_entry_point():
+@pytest.mark.parametrize("k", [3072, 4096])
+def test_noalloc_out_proj_matches_the_workspace_entry_point(k):
+    """K = 3072 and 4096 (3 and 4 splits of 1024): the partial sums in the
+    built-in scratch."""
     from engine.kernels import _lib
     from engine.kernels.in_proj import gdn_out_proj_decode
     lib = _lib.load()
     gen = torch.Generator().manual_seed(101)
-    k, n = 4096, 2048
+    n = 2048
+    assert lib.gdn_out_proj_workspace_bytes(64, k, n) == (k // 1024) * 64 * n * 4
     w = (0.02 * torch.randn(n, k, generator=gen)).to(torch.bfloat16).to(DEV)
     for m in (64, 5, 1, 33):  # each call after a larger one: no stale partials may leak in
         print(f"noalloc out_proj M={m} K={k} N={n}", flush=True)
