@@ -80,7 +80,8 @@ def parse():
     ap.add_argument("--no-layer-decode", action="store_true", help="skip the whole-layer decode measurement")
     ap.add_argument("--pools", type=int, default=4, help="rotating decode state pools")
     ap.add_argument("--prefill-only", action="store_true",
-                    help="time only the configuration 2 prefill (for counter profiles; prints no headline value)")
+                    help="time only the configuration 2 prefill and the B=16 x T=1038 batch (for counter "
+                         "profiles; prints no headline value)")
     ap.add_argument("--layer-only", action="store_true",
                     help="time only the decode projections and the whole-layer decode steps (for counter "
                          "profiles; prints no headline value)")
@@ -836,7 +837,8 @@ def main():
         copy_probe(torch)
         return
     if args.prefill_only:  # the prefill kernels alone (for counter profiles); no headline value
-        print(json.dumps({"prefill": bench_prefill(torch)}), flush=True)
+        print(json.dumps({"prefill": bench_prefill(torch), "prefill_b16_t1038": bench_prefill_b16(torch)}),
+              flush=True)
         return
     if args.layer_only:  # the decode projections and layer steps alone (for counter profiles)
         print(json.dumps({"decode_in_proj": bench_in_proj(torch), "decode_out_proj": bench_out_proj(torch),
