@@ -382,3 +382,53 @@ def test_repeated_slot_id_with_mismatched_has_initial_state(has_first):
     assert np.abs(np64(o) - o_ref).max() < O_TOL
     assert gdn.state_rel_err(np64(pd[5])[None], s_ref[0:1]) < S_TOL
     assert torch.equal(pd[:5].cpu(), pool[:5])
+
+
+@pytest.mark.parametrize("b,t,seed", [(8, 130, 5), (16, 64, 6)])
+def test_per_pair_kernel_batches_match_the_oracle(b, t, seed):
+    """A batch of 256 or more (sequence, v-head) pairs runs one workgroup per
+    pair (chunk_local_kernel, no workspace): B = 8 x T = 130 (a partial last
+    chunk) and B = 16 x T = 64 (one chunk each), zero h0, final states out,
+    against the oracle sequence by sequence."""
+    from engine.kernels import _lib
+    assert _lib.load().gdn_chunk_workspace_bytes(b, b * t, 32, 128, 128) == 0  # the per-pair kernel's batch
+    c = configs.config2(t=b * t, seed=seed)
+    x = {k: c[k].reshape(b, t, *c[k].shape[2:]) for k in ("q", "k", "v", "g", "beta")}
+    print(f"per-pair kernel B={b} T={t}", flush=True)
+    o, s = chunk_gated_delta_rule(*(x[k].to(DEV) for k in ("q", "k", "v", "g", "beta")), output_final_state=True,
+                                  use_qk_l2norm_in_kernel=True)
+    for i in range(b):
+        o_ref, s_ref = gdn.chunk_gated_delta_rule(*(x[k][i:i + 1].float().numpy() for k in ("q", "k", "v", "g", "beta")))
+        assert np.abs(np64(o[i:i + 1]) - o_ref).max() < O_TOL, i
+        assert gdn.state_rel_err(np64(s[i:i + 1]), s_ref) < S_TOL, i
+
+
+def test_per_pair_kernel_varlen_on_a_slot_pool():
+    """8 packed sequences (256 pairs: the per-pair kernel) of 4,500 (71 chunks,
+    past the two-kernel path's 64-chunk segment), 0, 1, 130, 64, 700, 65 and 17
+    tokens on a 12-slot pool, in place, with slot ids [7, 2, 9, 2, -1, 0, 11, 5]
+    (row 3 repeats row 1's slot, row 4 has none) and has_initial_state False
+    for row 5: rows 3 and 4 start from zero and write nothing, row 5 starts
+    from zero and writes slot 0, the empty row 1 passes slot 2 through."""
+    lens = [4500, 0, 1, 130, 64, 700, 65, 17]
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32)
+    c = configs.config2(seed=77, t=int(cu[-1]))
+    pool0 = torch.randn(12, 32, 128, 128, generator=torch.Generator().manual_seed(78)) * 0.1
+    ids = torch.tensor([7, 2, 9, 2, -1, 0, 11, 5])
+    has = torch.tensor([True, True, True, True, True, False, True, True])
+    h0 = torch.zeros(len(lens), 32, 128, 128)
+    for r in (0, 1, 2, 6, 7):
+        h0[r] = pool0[ids[r]]
+    print("per-pair kernel varlen on a pool", flush=True)
+    pool = pool0.to(DEV)
+    o, _ = chunk_gated_delta_rule(*(c[x].to(DEV) for x in ("q", "k", "v", "g", "beta")), initial_state=pool,
+                                  ssm_state_indices=ids.to(DEV), has_initial_state=has.to(DEV),
+                                  inplace_final_state=True, use_qk_l2norm_in_kernel=True, cu_seqlens=cu.to(DEV))
+    o_ref, s_ref = gdn.chunk_gated_delta_rule_varlen(*(c[x].float().numpy() for x in ("q", "k", "v", "g", "beta")),
+                                                     cu.numpy(), h0.numpy())
+    assert np.abs(np64(o) - o_ref).max() < O_TOL
+    for r in (0, 1, 2, 5, 6, 7):  # the rows that own their slot
+        assert gdn.state_rel_err(np64(pool[int(ids[r])])[None], s_ref[r:r + 1]) < S_TOL, r
+    assert torch.equal(pool[2].cpu(), pool0[2])  # the empty row passed its state through
+    untouched = [i for i in range(12) if i not in (7, 2, 9, 0, 11, 5)]
+    assert torch.equal(pool[untouched].cpu(), pool0[untouched])
