@@ -1258,25 +1258,22 @@ __global__ __launch_bounds__(64 * SCAN_WAVES) void chunk_scan_persist_kernel(Chu
 }
 
 // ------------------------------------------------------------------ local prefill
-// One workgroup of 8 waves per (sequence, v-head) runs the whole chunk loop of
-// that pair on one CU, with no workspace: per chunk, waves 0-3 form the
-// chunk's operands in LDS (the phase-A steps above: K K^T and K Q^T, the
-// solve, W and U), then all 8 waves run the state chain, wave w owning state
-// columns 16w..16w+15 of all 128 rows (eight 16x16 fp32 accumulator tiles):
-//   V' = U - W S                            16 MFMAs  (-W blocks, U tile from LDS)
-//   O^T = (S^T Q^T) diag(sq) + V'^T A^T     22 MFMAs  (q fragments, A blocks from LDS)
-//   S <- e^{gamma_63} S + K^T V''           32 MFMAs  (V'' = diag(sk) V' as bf16 hi + lo)
+// Batches of (sequence, v-head) pairs that fill the CUs run one workgroup per
+// pair over the pair's whole chunk loop, with no workspace: the chunk's
+// operands are formed in LDS by loc_prep (the phase-A steps of
+// chunk_prep_kernel: K K^T and K Q^T, the solve, W and U) and consumed there
+// by the state's chain, the state held in registers for the whole sequence:
+//   V' = U - W S                            (-W blocks, U tiles from LDS)
+//   O^T = (S^T Q^T) diag(sq) + V'^T A^T     (q fragments, A blocks from LDS)
+//   S <- e^{gamma_63} S + K^T V''           (V'' = diag(sk) V' as bf16 hi + lo)
 // The state is the B operand of V' and the A operand of O^T straight from the
 // accumulators (pi order), V'' the B operand of the state update, so no
-// product needs another wave's registers.  The next chunk's k, v and q rows
-// and gates are requested into registers at the start of each chain step.
-// The chunk operands live in LDS in the layouts their consumers read with
-// one ds_read_b128 per fragment: -W and A blocks as in the workspace layout,
-// q rows as pi fragments (written from the prep waves' own fragments), K^T
-// fragments (written by the wave of the prep that reads all of them), U tiles
-// by (column tile, position tile).  Used when the (sequence, v-head) pairs fill
-// the CUs; the same algorithm and precision as prep + scan.
-constexpr int LOC_WAVES = 4;
+// product needs another wave's registers.  The chunk operands live in LDS in
+// the layouts their consumers read with one ds_read_b128 per fragment: -W
+// and A blocks as in the workspace layout, q rows as pi fragments (written
+// from the prep waves' own fragments), K^T fragments (written by the wave of
+// the prep that reads all of them), U tiles by (column tile, position tile).
+// Same algorithm and precision as prep + scan.
 constexpr int LOC_NB_A = 6;  // A blocks (p, s), s <= (p >= 2): those of the lower triangle
 __host__ __device__ constexpr int a_blk(int p, int s) { return p < 2 ? p : 2 * p - 2 + s; }
 enum { SC_SQ = 0, SC_SK = CK, SC_EL = 2 * CK };  // the scalar block: sq[64], sk[64], eL
@@ -1336,7 +1333,11 @@ __device__ __forceinline__ void loc_load(const ChunkArgs &a, LocIn &in, int64_t 
 
 // Phase A of one chunk on waves 0-3 (thread tid < 256), from the registers of
 // loc_load into the LDS operands of the chain.
-__device__ __forceinline__ void loc_prep(const ChunkArgs &a, const LocIn &in, const LocLds &L, int len, int tid) {
+// after_v() runs once the chunk's inputs in `in` are consumed (after barrier
+// 6): the caller may request the next chunk's into it there.
+template <class AfterV>
+__device__ __forceinline__ void loc_prep(const ChunkArgs &a, const LocIn &in, const LocLds &L, int len, int tid,
+                                         const AfterV &after_v) {
   const int lane = tid & 63, p = tid >> 6, g4 = lane >> 4, r16 = lane & 15, seg = tid & 15;
   const int irow = 16 * p + r16;
   uint16_t *kn = L.kn;
@@ -1387,7 +1388,7 @@ __device__ __forceinline__ void loc_prep(const ChunkArgs &a, const LocIn &in, co
     L.gam_s[lane] = gv;
     L.beta_s[lane] = bv;
   }
-  __syncthreads();  // (1)
+  lds_barrier();  // (1)
 
   if (p == 0) {  // per-position scalars of the chain, W's column scale
     const float gl = L.gam_s[CK - 1], gm = L.gam_s[lane], nkl = L.nk_s[lane];
@@ -1461,7 +1462,7 @@ __device__ __forceinline__ void loc_prep(const ChunkArgs &a, const LocIn &in, co
     __builtin_amdgcn_wave_barrier();
     drow = *reinterpret_cast<const f32x4 *>(tr + r16 * 20 + 4 * g4);
   }
-  __syncthreads();  // (2)
+  lds_barrier();  // (2)
   f32x4 trow[4];
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1473,7 +1474,7 @@ __device__ __forceinline__ void loc_prep(const ChunkArgs &a, const LocIn &in, co
       trow[b] = -mm16(x, drow, z4);
       if (b <= 1) txch[b * 64 + lane] = -mm16(drow, x, z4);
     }
-  __syncthreads();  // (3)
+  lds_barrier();  // (3)
 #pragma unroll
   for (int b = 0; b < 2; ++b)
     if (b == p - 2) {
@@ -1482,73 +1483,93 @@ __device__ __forceinline__ void loc_prep(const ChunkArgs &a, const LocIn &in, co
       trow[b] = -mm16(x, drow, z4);
       if (b == 0) txch[2 * 64 + lane] = -mm16(drow, x, z4);
     }
-  __syncthreads();  // (4)
+  lds_barrier();  // (4)
   if (p == 3) {
     f32x4 x = mm16(lf[0], dxch[lane], z4);
     x = mm16(lf[1], txch[lane], x);
     x = mm16(lf[2], txch[2 * 64 + lane], x);
     trow[0] = -mm16(x, drow, z4);
   }
-  __syncthreads();  // (5) the exchange buffers are free: V rows take their place
+  lds_barrier();  // (5) the exchange buffers are free: V rows take their place
 #pragma unroll
   for (int it = 0; it < 4; ++it)
     *reinterpret_cast<u32x4 *>(vn + nsw((tid >> 4) + 16 * it, seg * 8)) = in.vu[it];
-  __syncthreads();  // (6)
+  lds_barrier();  // (6)
+  after_v();
 
   // ---- W^T = K^T (T diag(colw))^T and U = T diag(beta) V; wave 3 (which
   // reads every K^T fragment) also leaves them for the chain
-  f32x4 wt[8], ut[8];
-#pragma unroll
-  for (int nb = 0; nb < 8; ++nb) {
-    wt[nb] = z4;
-    ut[nb] = z4;
-  }
+  // (in two halves of 4 column tiles: 32 accumulator registers instead of 64)
   const int nsteps = p >= 2 ? 2 : 1;
+  bf16x8 whi[2], wlo[2], uhi[2], ulo[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
-    if (s < nsteps) {
-      const f32x4 cw0 = *reinterpret_cast<const f32x4 *>(L.colw_s + 32 * s + 4 * g4);
-      const f32x4 cw1 = *reinterpret_cast<const f32x4 *>(L.colw_s + 32 * s + 16 + 4 * g4);
-      const f32x4 be0 = *reinterpret_cast<const f32x4 *>(L.beta_s + 32 * s + 4 * g4);
-      const f32x4 be1 = *reinterpret_cast<const f32x4 *>(L.beta_s + 32 * s + 16 + 4 * g4);
-      bf16x8 whi, wlo, uhi, ulo;
-      pack_hilo(trow[2 * s] * cw0, trow[2 * s + 1] * cw1, whi, wlo);
-      pack_hilo(trow[2 * s] * be0, trow[2 * s + 1] * be1, uhi, ulo);
-#pragma unroll
-      for (int nb = 0; nb < 8; ++nb) {
-        const bf16x8 kt = frag_tr(kn, s, 16 * nb, lane);
-        const bf16x8 vf = frag_tr(vn, s, 16 * nb, lane);
-        if (p == 3) L.ktf[(2 * nb + s) * 64 + lane] = __builtin_bit_cast(u32x4, kt);
-        wt[nb] = mfma(kt, whi, wt[nb]);
-        wt[nb] = mfma(kt, wlo, wt[nb]);
-        ut[nb] = mfma(uhi, vf, ut[nb]);
-        ut[nb] = mfma(ulo, vf, ut[nb]);
-      }
-    }
+    const f32x4 cw0 = *reinterpret_cast<const f32x4 *>(L.colw_s + 32 * s + 4 * g4);
+    const f32x4 cw1 = *reinterpret_cast<const f32x4 *>(L.colw_s + 32 * s + 16 + 4 * g4);
+    const f32x4 be0 = *reinterpret_cast<const f32x4 *>(L.beta_s + 32 * s + 4 * g4);
+    const f32x4 be1 = *reinterpret_cast<const f32x4 *>(L.beta_s + 32 * s + 16 + 4 * g4);
+    pack_hilo(trow[2 * s] * cw0, trow[2 * s + 1] * cw1, whi[s], wlo[s]);
+    pack_hilo(trow[2 * s] * be0, trow[2 * s + 1] * be1, uhi[s], ulo[s]);
   }
 #pragma unroll
-  for (int s = 0; s < 4; ++s) L.wb[(4 * p + s) * 64 + lane] = __builtin_bit_cast(u32x4, pack_hi(-wt[2 * s], -wt[2 * s + 1]));
+  for (int half = 0; half < 2; ++half) {
+    f32x4 wt[4], ut[4];
 #pragma unroll
-  for (int nb = 0; nb < 8; ++nb) L.ub[(4 * nb + p) * 64 + lane] = ut[nb];
-  __syncthreads();  // (7) the chunk's operands are in LDS
+    for (int q = 0; q < 4; ++q) {
+      wt[q] = z4;
+      ut[q] = z4;
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (s < nsteps) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int nb = 4 * half + q;
+          const bf16x8 kt = frag_tr(kn, s, 16 * nb, lane);
+          const bf16x8 vf = frag_tr(vn, s, 16 * nb, lane);
+          if (p == 3) L.ktf[(2 * nb + s) * 64 + lane] = __builtin_bit_cast(u32x4, kt);
+          wt[q] = mfma(kt, whi[s], wt[q]);
+          wt[q] = mfma(kt, wlo[s], wt[q]);
+          ut[q] = mfma(uhi[s], vf, ut[q]);
+          ut[q] = mfma(ulo[s], vf, ut[q]);
+        }
+      }
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+      L.wb[(4 * p + 2 * half + s2) * 64 + lane] = __builtin_bit_cast(u32x4, pack_hi(-wt[2 * s2], -wt[2 * s2 + 1]));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) L.ub[(4 * (4 * half + q) + p) * 64 + lane] = ut[q];
+  }
+  lds_barrier();  // (7) the chunk's operands are in LDS
 }
+
+
+// The per-pair prefill, the chunk's preparation and the state's chain
+// overlapped: one workgroup of 8 waves per (sequence, v-head).  Waves 0-3
+// prepare chunk k (loc_prep, 7 barriers) while waves 4-7 run chunk k - 1's
+// chain, fitted between the same barriers: V' = U - W S before barrier 1,
+// the output and the state update between barriers 1 and 2 (the solve's
+// interval, the longest).  The operands the preparation writes before
+// barrier 2 (q fragments, A blocks, scalars) are double-buffered; -W, U and
+// K^T are written after barrier 6, when the chain has read them.  The next
+// chunk's rows are requested after barrier 6, when the current ones are in
+// LDS.  143 KiB of LDS: one workgroup per CU.
+constexpr int LOC_WAVES = 8;
 
 template <bool BF16_OUT>
 __global__ __launch_bounds__(64 * LOC_WAVES) void chunk_local_kernel(ChunkArgs a) {
   __shared__ __align__(16) uint16_t kn[CK * DK];
   __shared__ __align__(16) f32x4 s16k[1024];
-  __shared__ u32x4 ktf[16 * 64], qp[16 * 64], wb[16 * 64], ab[LOC_NB_A * 64];
+  __shared__ u32x4 ktf[16 * 64], wb[16 * 64], qp2[2][16 * 64], ab2[2][LOC_NB_A * 64];
   __shared__ f32x4 ub[32 * 64];
-  __shared__ __align__(16) float sc[SCAL], gam_s[CK], beta_s[CK], nk_s[CK], nq_s[CK], colw_s[CK];
-  const LocLds L{kn, s16k, ktf, qp, wb, ub, ab, sc, gam_s, beta_s, nk_s, nq_s, colw_s};
+  __shared__ __align__(16) float sc2[2][SCAL], gam_s[CK], beta_s[CK], nk_s[CK], nq_s[CK], colw_s[CK];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, r16 = lane & 15;
   const int ratio = a.Hv / a.Hk;
-  // (sequence, v-head) of this workgroup; the v-heads of one k-head (which
-  // read the same q / k rows) on one XCD when the pairs come in groups of 8
   int n = blockIdx.x / a.Hv, h = blockIdx.x % a.Hv;
   if ((a.n_seqs * (a.Hv / ratio)) % 8 == 0) {
     int g, m;
@@ -1563,12 +1584,32 @@ __global__ __launch_bounds__(64 * LOC_WAVES) void chunk_local_kernel(ChunkArgs a
   s0 = uniform64(s0);
   slen = __builtin_amdgcn_readfirstlane(slen);
   const int nch = (slen + CK - 1) / CK;
+  auto chunk_len = [&](int k) { return min(CK, slen - k * CK); };
+
+  if (wave < 4) {  // ---------------- preparation of chunk k at step k
+    LocIn in;
+    if (nch > 0) loc_load(a, in, s0, chunk_len(0), h, hk, tid);
+    for (int k = 0; k < nch; ++k) {
+      // the thread index made opaque per chunk: the LDS addresses derived from
+      // it are recomputed in the loop instead of hoisted out of it and spilled
+      int tk = tid;
+      asm volatile("" : "+v"(tk));
+      const LocLds L{kn, s16k, ktf, qp2[k & 1], wb, ub, ab2[k & 1], sc2[k & 1], gam_s, beta_s, nk_s, nq_s, colw_s};
+      loc_prep(a, in, L, chunk_len(k), tk, [&] {
+        if (k + 1 < nch) loc_load(a, in, s0 + static_cast<int64_t>(k + 1) * CK, chunk_len(k + 1), h, hk, tk);
+      });
+    }
+    if (nch > 0)  // step nch: the chain's last chunk
+#pragma unroll 1
+      for (int b = 0; b < 7; ++b) lds_barrier();
+    return;
+  }
+
+  // ---------------- the chain of chunk k - 1 at step k (waves 4-7)
+  const int cw = wave - 4;
   const int64_t kv = static_cast<int64_t>(DK) * DV;
   const int64_t in_row = a.h0 ? uniform64(pool_row_first(a.h0_idx, n, a.h0_rows)) : -1;
   const int64_t out_row = a.hT ? uniform64(pool_row_first(a.hT_idx, n, a.hT_rows)) : -1;
-  // wave w: phase A for chunk rows 16w.., then the chain for state columns
-  // 32 w .. + 31 as two 16-column tiles
-  const int cw = wave;
   float *dst[2];
   f32x4 S[2][8];  // tile j: state rows 16 t + 4 g + e of column 32 cw + 16 j + r
 #pragma unroll
@@ -1581,38 +1622,24 @@ __global__ __launch_bounds__(64 * LOC_WAVES) void chunk_local_kernel(ChunkArgs a
 #pragma unroll
       for (int e = 0; e < 4; ++e) S[j][t][e] = src ? src[(16 * t + 4 * g4 + e) * DV] : 0.f;
   }
-  auto store_state = [&]() {
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      if (dst[j]) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) dst[j][(16 * t + 4 * g4 + e) * DV] = S[j][t][e];
-      }
-  };
-  if (nch == 0) {  // empty sequence: the final state is the initial one
-    store_state();
-    return;
-  }
-
   typedef typename std::conditional<BF16_OUT, uint16_t, float>::type OT;
   const int64_t ostep = static_cast<int64_t>(a.Hv) * DV;
-  LocIn in;
-  loc_load(a, in, s0, min(CK, slen), h, hk, tid);
-  for (int c = 0; c < nch; ++c) {
+  // step 0: the preparation of chunk 0 alone
+  if (nch > 0)
+#pragma unroll 1
+    for (int b = 0; b < 7; ++b) lds_barrier();
+  for (int k = 1; k <= nch; ++k) {
+    const int c = k - 1;
+    const u32x4 *qp = qp2[c & 1], *ab = ab2[c & 1];
+    const float *sc = sc2[c & 1];
     const int64_t t0 = s0 + static_cast<int64_t>(c) * CK;
-    const int len = min(CK, slen - c * CK);
-    loc_prep(a, in, L, len, tid);  // phase A (ends with a barrier), then the next chunk's inputs requested
-    if (c + 1 < nch) loc_load(a, in, t0 + CK, min(CK, slen - (c + 1) * CK), h, hk, tid);
-
-    // ---- the chain for the wave's two column tiles
-    bf16x8 sb[2][4];  // the state as bf16 B operands (pi order), row k-steps 0..3
+    const int len = chunk_len(c);
+    // interval 0: V' = U - W S
+    bf16x8 sb[2][4];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int s = 0; s < 4; ++s) sb[j][s] = pack_hi(S[j][2 * s], S[j][2 * s + 1]);
-    // V' = U - W S
     f32x4 vp[2][4];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -1626,7 +1653,8 @@ __global__ __launch_bounds__(64 * LOC_WAVES) void chunk_local_kernel(ChunkArgs a
 #pragma unroll
         for (int j = 0; j < 2; ++j) vp[j][t] = mfma(w, sb[j][s], vp[j][t]);
       }
-    // O^T = (S^T Q^T) diag(sq) + V'^T A^T per position tile i; rows past the chunk dropped
+    lds_barrier();  // (1)
+    // interval 1: O^T = (S^T Q^T) diag(sq) + V'^T A^T, then S <- e^{gamma_63} S + K^T V''
     bf16x8 vb[2][2];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -1658,7 +1686,6 @@ __global__ __launch_bounds__(64 * LOC_WAVES) void chunk_local_kernel(ChunkArgs a
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), ro, voff, 0, 0);
       }
     }
-    // S <- e^{gamma_63} S + K^T V'',  V'' = diag(sk) V' in bf16 hi + lo
     bf16x8 vh[2][2], vl[2][2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -1683,10 +1710,19 @@ __global__ __launch_bounds__(64 * LOC_WAVES) void chunk_local_kernel(ChunkArgs a
           S[j][t] = mfma(kt, vl[j][s], S[j][t]);
         }
       }
-    __syncthreads();  // the chunk's operands are read: the next prep may overwrite them
+#pragma unroll 1
+    for (int b = 1; b < 7; ++b) lds_barrier();  // (2) .. (7)
   }
-  store_state();
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    if (dst[j]) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[j][(16 * t + 4 * g4 + e) * DV] = S[j][t][e];
+    }
 }
+
 
 // Chunks per prep + scan segment: one prep launch produces a segment's
 // operands (about 2.3 MiB per chunk at 32 v-heads: 146 MiB for 64 chunks,
@@ -1791,11 +1827,11 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
                 q_stride_t, k_stride_t, v_stride_t, gate, h0, h0_idx, h0_rows, hT, hT_idx, hT_rows, o, o_dtype,
                 cu_seqlens, n_seqs, T, Hk, Hv, total, scale, l2norm_qk, static_cast<int>(std::min<int64_t>(nc, 0x7fffffff)),
                 0, 0, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
-    const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(n_seqs) * Hv)), block(64 * LOC_WAVES);
+    const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(n_seqs) * Hv));
     if (o_dtype == GDN_DTYPE_BF16)
-      hipLaunchKernelGGL((chunk_local_kernel<true>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((chunk_local_kernel<true>), grid, dim3(64 * LOC_WAVES), 0, s, a);
     else
-      hipLaunchKernelGGL((chunk_local_kernel<false>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((chunk_local_kernel<false>), grid, dim3(64 * LOC_WAVES), 0, s, a);
     return check_launch(name);
   }
   if (!workspace || workspace_bytes < l.total)
