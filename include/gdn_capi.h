@@ -176,7 +176,7 @@ int gdn_chunk_fwd_gated(const void *q, const void *k, const void *v, int qkv_dty
 
 /* Workspace bytes gdn_chunk_fwd(_gated) needs for `total_tokens` tokens in
  * `n_seqs` sequences (an upper bound that needs no knowledge of the lengths).
- * 0 when n_seqs * Hv >= 256: such a batch runs one workgroup per (sequence,
+ * 0 when n_seqs * Hv >= 160: such a batch runs one workgroup per (sequence,
  * v-head) that keeps every chunk operand in LDS, and the workspace pointer
  * may then be NULL. */
 size_t gdn_chunk_workspace_bytes(int32_t n_seqs, int64_t total_tokens,

@@ -1735,7 +1735,14 @@ __global__ __launch_bounds__(64 * LOC_WAVES) void chunk_local_kernel(ChunkArgs a
 // kernels cannot share a CU -- the scan holds 138 KiB of LDS -- so the prep
 // takes CUs from the scan's chain).
 constexpr int SEG_CHUNKS = 64;
-constexpr int LOC_MIN_PAIRS = 256;  // (sequence, v-head) pairs from which the local kernel runs
+// (sequence, v-head) pairs from which the local kernel runs.  Its time is the
+// longest sequence's chunk count times a chunk step, whatever the batch (up
+// to one workgroup per CU); prep + scan grows with the total chunks.
+// Measured (q/k at 16 heads, Hv = 32): B = 4 x T = 1038 132 (prep + scan)
+// against 139 us, B = 6 x T = 1038 193 against 142, B = 4 x T = 4096 459
+// against 495, B = 2 x T = 4096 242 against 477: the local kernel from 5
+// sequences of 32 v-heads.
+constexpr int LOC_MIN_PAIRS = 160;
 
 // Workspace: the chunk table, the state carried between segments (when
 // there are several) and the scan operands of one segment.

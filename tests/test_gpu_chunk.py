@@ -384,12 +384,13 @@ def test_repeated_slot_id_with_mismatched_has_initial_state(has_first):
     assert torch.equal(pd[:5].cpu(), pool[:5])
 
 
-@pytest.mark.parametrize("b,t,seed", [(8, 130, 5), (16, 64, 6)])
+@pytest.mark.parametrize("b,t,seed", [(8, 130, 5), (16, 64, 6), (5, 200, 7)])
 def test_per_pair_kernel_batches_match_the_oracle(b, t, seed):
-    """A batch of 256 or more (sequence, v-head) pairs runs one workgroup per
+    """A batch of 160 or more (sequence, v-head) pairs runs one workgroup per
     pair (chunk_local_kernel, no workspace): B = 8 x T = 130 (a partial last
-    chunk) and B = 16 x T = 64 (one chunk each), zero h0, final states out,
-    against the oracle sequence by sequence."""
+    chunk), B = 16 x T = 64 (one chunk each) and B = 5 x T = 200 (160 pairs,
+    fewer workgroups than CUs), zero h0, final states out, against the oracle
+    sequence by sequence."""
     from engine.kernels import _lib
     assert _lib.load().gdn_chunk_workspace_bytes(b, b * t, 32, 128, 128) == 0  # the per-pair kernel's batch
     c = configs.config2(t=b * t, seed=seed)
