@@ -163,6 +163,16 @@ __device__ __forceinline__ void phase_mfma(f32x4_t (&acc)[4], const u32x4_t (&wr
 // s_waitcnt operand: vmcnt <= n, lgkmcnt and expcnt unconstrained
 constexpr int ip_vmcnt(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 
+// A workgroup barrier that orders LDS only: __syncthreads' fence would also
+// wait for every outstanding global load and store (the next tile's weights,
+// the epilogue's stores), which no other wave reads.  Waits for LDS DMA are
+// explicit (ip_vmcnt) where they are needed.
+__device__ __forceinline__ void ip_lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // After phase 0's copies and the weights were issued (and POST more loads
 // after them): the phases, then the parts' partial sums added in LDS in part
 // order.  Returns, for waves of part kq < 4, row tile kq of their column
@@ -354,7 +364,10 @@ __global__ __launch_bounds__(64 * NW) void in_proj_xs_kernel(InProjArgs a) {
   // this workgroup's columns of [b | a]: blockIdx.x + G ci, ci < nbc (<= XS_BA_MAX: checked on the host)
   const int nba = a.n[2] + a.n[3];
   const int nbc = __builtin_amdgcn_readfirstlane(min(XS_BA_MAX, (nba - static_cast<int>(blockIdx.x) + G - 1) / G));
-  const int kw = wave * 32 * KSW;  // this wave's columns of K
+  // this wave's columns of K: part (wave + blockIdx.x) % NW, so that the CUs
+  // (all reading the same rows of x from L2) do not all request the same
+  // addresses at the same moment
+  const int kw = ((wave + static_cast<int>(blockIdx.x)) % NW) * 32 * KSW;
 
   // slot id of the row this lane finishes (waves 0-3: row tile = wave)
   const int me = m0 + 16 * wave + c;
@@ -363,16 +376,25 @@ __global__ __launch_bounds__(64 * NW) void in_proj_xs_kernel(InProjArgs a) {
   if (wave < 4) id_raw = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(ri, min(me, a.M - 1) * 8, 0, 0));
   __builtin_amdgcn_sched_barrier(0);
 
-  // the hidden rows: B operand of row tile t, k-step s at lane (c, g) = row 16 t + c, k = kw + 32 s + 8 g
+  // the hidden rows: B operand of row tile t, k-step s at lane (c, g) = row 16 t + c, k = kw + 32 s + 8 g.
+  // Every CU reads the same rows from L2, where a load of 16 rows x 64 bytes
+  // (the fragment layout) streams at about half the rate of a contiguous
+  // 1 KiB: so they are read contiguously -- instruction q of row tile t holds
+  // rows 16 t + RPI q .., lane l row-in-tile RPI q + l / CPR, 16-byte chunk
+  // l % CPR of the wave's 64 KSW bytes of the row -- and put in the fragment
+  // layout through a wave-private LDS scratch (the tile partials' region,
+  // unused until the first tile is multiplied), chunk ch of row r at slot
+  // r CPR + (ch ^ r % CPR) so that neither side conflicts on banks.
+  constexpr int CPR = 4 * KSW, RPI = 64 / CPR;  // 16-byte chunks per row slice, rows per instruction (KSW of them per tile)
   const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a.x) + static_cast<int64_t>(m0) * a.xs, 0,
                                                     static_cast<int>(((mb - 1) * a.xs + K) * 2), BUF_DWORD3);
   u32x4_t xr[4][KSW];
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int s = 0; s < KSW; ++s)
-      xr[t][s] = __builtin_amdgcn_raw_buffer_load_b128(rx, static_cast<int>(((16 * t + c) * a.xs + kw + 32 * s + 8 * g) * 2),
-                                                       0, 0);
+    for (int q = 0; q < KSW; ++q)
+      xr[t][q] = __builtin_amdgcn_raw_buffer_load_b128(
+          rx, static_cast<int>(((16 * t + RPI * q + lane / CPR) * a.xs + kw + 8 * (lane % CPR)) * 2), 0, 0);
   // a tile's weights: lane (r, g) of k-step s holds W[col + r][kw + 32 s + 8 g .. + 8] (rows past the matrix: 0)
   auto load_tile = [&](u32x4_t (&w)[KSW], int i) {
     const XsTile t = xs_tile(a, tiles, static_cast<int>(blockIdx.x) + G * i);
@@ -392,10 +414,22 @@ __global__ __launch_bounds__(64 * NW) void in_proj_xs_kernel(InProjArgs a) {
   int wbase = -1;  // byte offset of this lane's row in the pool, -1: no window (waves 0-3)
   if (wave < 4) {
     // a row whose slot id repeats an earlier row's selects no window
+    // (the ids read 64 at a time, one per lane, then broadcast lane by lane:
+    // one id per iteration from memory was a dependent load per earlier row)
     bool rep = false;
     if (a.idx) {
-      const int mlast = min(m0 + 16 * wave + 15, a.M - 1);
-      for (int m = 0; m < mlast; ++m) rep |= m < me && a.idx[m] == id;
+      const int mlast = min(m0 + 16 * wave + 15, a.M - 1);  // the wave's last row
+      for (int base = 0; base < mlast; base += 64) {
+        const int64_t v = __builtin_bit_cast(int64_t, __builtin_amdgcn_raw_buffer_load_b64(
+                              ri, min(base + lane, a.M - 1) * 8, 0, 0));
+        const int jn = min(64, mlast - base);
+        for (int j = 0; j < jn; ++j) {
+          const int64_t vj = static_cast<int64_t>(
+              (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v >> 32), j))) << 32) |
+              static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), j)));
+          rep |= base + j < me && vj == id;
+        }
+      }
     }
     const bool has = me < a.M && !rep && id >= 0 && id < a.rows;
     wbase = has ? static_cast<int>(id * a.n[0] * 8) : -1;  // (< IP_OOB: checked on the host)
@@ -430,6 +464,21 @@ __global__ __launch_bounds__(64 * NW) void in_proj_xs_kernel(InProjArgs a) {
   }
   __builtin_amdgcn_sched_barrier(0);
 
+  {  // the rows into the fragment layout, one row tile at a time, in place
+    u32x4_t *scr = reinterpret_cast<u32x4_t *>(&red[wave][0][0]);  // 16 CPR slots of this wave
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int q = 0; q < KSW; ++q) {
+        const int r = RPI * q + lane / CPR, ch = lane % CPR;
+        scr[r * CPR + (ch ^ (r % CPR))] = xr[t][q];
+      }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int s2 = 0; s2 < KSW; ++s2) xr[t][s2] = scr[c * CPR + ((4 * s2 + g) ^ (c % CPR))];
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
   auto ba_partials = [&]() { xs_ba_partials<NW, KSW>(baw, bared, xr, nbc, kw, wave, lane); };
   auto ba_finish = [&]() { xs_ba_finish<NW>(a, bared, nbc, G, m0, lane); };
 
@@ -453,7 +502,7 @@ __global__ __launch_bounds__(64 * NW) void in_proj_xs_kernel(InProjArgs a) {
       else
         __builtin_amdgcn_s_waitcnt(ip_vmcnt(0));
     }
-    __syncthreads();
+    ip_lds_barrier();
     if (i == 0 && wave >= 4) ba_partials();  // (waves 0-3 after their epilogue)
     if (i == 1 && wave == 4) ba_finish();
     if (wave < 4) {
@@ -490,13 +539,13 @@ __global__ __launch_bounds__(64 * NW) void in_proj_xs_kernel(InProjArgs a) {
       }
     }
     if (i == 0 && wave < 4) ba_partials();
-    __syncthreads();  // the partials are consumed: the next tile's may go in
+    ip_lds_barrier();  // the partials are consumed: the next tile's may go in
   }
   if (nt == 0 && nbc > 0) {  // no tile: the b / a columns alone
     __builtin_amdgcn_s_waitcnt(ip_vmcnt(0));
-    __syncthreads();
+    ip_lds_barrier();
     ba_partials();
-    __syncthreads();
+    ip_lds_barrier();
   }
   if (nt <= 1 && wave == 4) ba_finish();
 }
