@@ -268,6 +268,43 @@ __device__ __forceinline__ f32x4 mm16(f32x4 a, f32x4 b, f32x4 acc) {
 
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
+// T[p][p] = (I + L[p][p])^-1 in D layout: each lane solves for column r16 by
+// forward substitution, x[i] = [i == r16] - sum_{j < i} L[i][j] x[j], with
+// L[p][p]'s entries (row layout: row i, columns 4q .. 4q + 3 in lane
+// i + 16 q) broadcast from the lanes that hold them by v_readlane, so the
+// 16 dependent rows wait on no memory.
+__device__ __forceinline__ f32x4 diag_inverse(const f32x4 lf[4], int p, int lane) {
+  const int r16 = lane & 15, g4 = lane >> 4, pu = __builtin_amdgcn_readfirstlane(p);
+  // (the entries are read as ints of the whole vector's bit cast: a bit cast
+  // of one vector element was lowered as a read of element 0, and the builtin
+  // takes ints, so a float argument would be converted by value)
+  const u32x4 lpp = __builtin_bit_cast(u32x4, pu == 0 ? lf[0] : pu == 1 ? lf[1] : pu == 2 ? lf[2] : lf[3]);
+  float x[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float acc = i == r16 ? 1.f : 0.f;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (4 * q4 + e < i) {
+          const float lij = __builtin_bit_cast(float, __builtin_amdgcn_readlane(static_cast<int>(lpp[e]), i + 16 * q4));
+          acc = __builtin_fmaf(-lij, x[4 * q4 + e], acc);
+        }
+    x[i] = acc;
+  }
+  f32x4 d;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {  // x[4 g4 + e]
+    // (the candidates are pinned in registers first: LLVM turns a select
+    // between elements of x into an indexed load, which puts x in scratch)
+    float c0 = x[e], c1 = x[4 + e], c2 = x[8 + e], c3 = x[12 + e];
+    asm volatile("" : "+v"(c0), "+v"(c1), "+v"(c2), "+v"(c3));
+    d[e] = g4 == 0 ? c0 : g4 == 1 ? c1 : g4 == 2 ? c2 : c3;
+  }
+  return d;
+}
+
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void chunk_prep_kernel(ChunkArgs a) {
   __shared__ __align__(16) uint16_t kn[CK * DK];  // K rows (swizzled)
   // V rows (swizzled) share 16 KiB with the solve's exchange buffers: V is
@@ -1294,6 +1331,7 @@ struct LocLds {
   u32x4 *ab;        // [LOC_NB_A][64] A blocks (p, s) at a_blk(p, s)
   float *sc;        // [256] sq[64], sk[64], eL
   float *gam_s, *beta_s, *nk_s, *nq_s, *colw_s;  // [64] each
+  f32x4 *tx;        // [4][4][64] T's rows by position tile (row layout), for the W and U products
 };
 
 __device__ __forceinline__ void loc_load(const ChunkArgs &a, LocIn &in, int64_t t0, int len, int h, int hk, int tid) {
@@ -1342,7 +1380,7 @@ __device__ __forceinline__ void loc_prep(const ChunkArgs &a, const LocIn &in, co
   const int irow = 16 * p + r16;
   uint16_t *kn = L.kn;
   uint16_t *vn = reinterpret_cast<uint16_t *>(L.s16k);
-  f32x4 *lbuf = L.s16k;             // [4 * 64] diagonal blocks of L, row layout by lane
+  // L.s16k[0 .. 4 * 64): unused by the solve
   f32x4 *dxch = L.s16k + 4 * 64;    // [4 * 64] diagonal blocks of T, D layout by lane
   f32x4 *txch = L.s16k + 8 * 64;    // [3 * 64] T[1][0], T[2][1], T[2][0], D layout by lane
   float(*dtr)[16 * 20] = reinterpret_cast<float(*)[16 * 20]>(L.s16k + 11 * 64);  // D -> row layout
@@ -1398,63 +1436,63 @@ __device__ __forceinline__ void loc_prep(const ChunkArgs &a, const LocIn &in, co
     L.colw_s[lane] = L.beta_s[lane] * fast_exp(gm) * nkl;
   }
 
-  // ---- tiles (cb, p), cb <= p, of K K^T and K Q^T: L and A in row layout
-  const float gi = L.gam_s[irow], bi = L.beta_s[irow], nki = L.nk_s[irow], nqi = L.nq_s[irow];
+  // ---- tiles (cb, pa), cb <= pa = 3 - p, of K Q^T (A), then tiles (cb, p),
+  // cb <= p, of K K^T (L, in row layout, for this wave's solve): 5 tile
+  // products per wave instead of 2, 4, 6, 8 (q fragments of other rows from LDS)
+  const f32x4 z4a = {0.f, 0.f, 0.f, 0.f};
+  {
+    const int pa = 3 - p, irow_a = 16 * pa + r16;
+    const float gia = L.gam_s[irow_a], nqa = L.nq_s[irow_a];
+    bf16x8 qa[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qa[s] = as_bf16x8(L.qp[(4 * pa + s) * 64 + lane]);
+    f32x4 af[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+      af[cb] = z4a;
+      if (cb <= pa) {
+        f32x4 qk = z4a;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) qk = mfma(frag_pi(kn, 16 * cb, s, lane), qa[s], qk);
+        const f32x4 gj = *reinterpret_cast<const f32x4 *>(L.gam_s + 16 * cb + 4 * g4);
+        const f32x4 nj = *reinterpret_cast<const f32x4 *>(L.nk_s + 16 * cb + 4 * g4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int jj = 16 * cb + 4 * g4 + e;
+          af[cb][e] = jj <= irow_a ? nqa * nj[e] * qk[e] * fast_exp(gia - gj[e]) : 0.f;
+        }
+      }
+    }
+    L.ab[a_blk(pa, 0) * 64 + lane] = __builtin_bit_cast(u32x4, pack_hi(af[0], af[1]));
+    if (pa >= 2) L.ab[a_blk(pa, 1) * 64 + lane] = __builtin_bit_cast(u32x4, pack_hi(af[2], af[3]));
+  }
+  const float gi = L.gam_s[irow], bi = L.beta_s[irow], nki = L.nk_s[irow];
   bf16x8 kown[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) kown[s] = frag_pi(kn, 16 * p, s, lane);
-  f32x4 lf[4], af[4];
+  f32x4 lf[4];
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb) {
-    lf[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    af[cb] = lf[cb];
+    lf[cb] = z4a;
     if (cb <= p) {
-      f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = kk;
+      f32x4 kk = z4a;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const bf16x8 kcb = frag_pi(kn, 16 * cb, s, lane);
-        kk = mfma(kcb, kown[s], kk);
-        qk = mfma(kcb, in.qf[s], qk);
-      }
+      for (int s = 0; s < 4; ++s) kk = mfma(frag_pi(kn, 16 * cb, s, lane), kown[s], kk);
       const f32x4 gj = *reinterpret_cast<const f32x4 *>(L.gam_s + 16 * cb + 4 * g4);
       const f32x4 nj = *reinterpret_cast<const f32x4 *>(L.nk_s + 16 * cb + 4 * g4);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int jj = 16 * cb + 4 * g4 + e;
-        const float dec = jj <= irow ? fast_exp(gi - gj[e]) : 0.f;
-        af[cb][e] = nqi * nj[e] * qk[e] * dec;
-        lf[cb][e] = jj < irow ? bi * nki * nj[e] * kk[e] * dec : 0.f;
+        lf[cb][e] = jj < irow ? bi * nki * nj[e] * kk[e] * fast_exp(gi - gj[e]) : 0.f;
       }
     }
   }
-  L.ab[a_blk(p, 0) * 64 + lane] = __builtin_bit_cast(u32x4, pack_hi(af[0], af[1]));
-  if (p >= 2) L.ab[a_blk(p, 1) * 64 + lane] = __builtin_bit_cast(u32x4, pack_hi(af[2], af[3]));
 
-  // ---- T = (I + L)^-1 (as in chunk_prep_kernel)
+  // ---- T = (I + L)^-1: diagonal blocks by diag_inverse (no LDS round trip on the
+  // preparation's longest interval), the blocks below them as in chunk_prep_kernel
   f32x4 dl, drow;
   {
-    f32x4 *lb = lbuf + p * 64;
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
-      if (cb == p) lb[lane] = lf[cb];
-    __builtin_amdgcn_wave_barrier();
-    float x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float acc = i == r16 ? 1.f : 0.f;
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4)
-        if (4 * q4 < i) {
-          const f32x4 lrow = lb[i + 16 * q4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (4 * q4 + e < i) acc -= lrow[e] * x[4 * q4 + e];
-        }
-      x[i] = acc;
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      dl[e] = g4 == 0 ? x[e] : g4 == 1 ? x[4 + e] : g4 == 2 ? x[8 + e] : x[12 + e];
+    dl = diag_inverse(lf, p, lane);
     dxch[p * 64 + lane] = dl;
     float *tr = dtr[p];
 #pragma unroll
@@ -1490,6 +1528,8 @@ __device__ __forceinline__ void loc_prep(const ChunkArgs &a, const LocIn &in, co
     x = mm16(lf[2], txch[2 * 64 + lane], x);
     trow[0] = -mm16(x, drow, z4);
   }
+#pragma unroll
+  for (int b = 0; b < 4; ++b) L.tx[(4 * p + b) * 64 + lane] = trow[b];  // for the W and U products
   lds_barrier();  // (5) the exchange buffers are free: V rows take their place
 #pragma unroll
   for (int it = 0; it < 4; ++it)
@@ -1497,51 +1537,67 @@ __device__ __forceinline__ void loc_prep(const ChunkArgs &a, const LocIn &in, co
   lds_barrier();  // (6)
   after_v();
 
-  // ---- W^T = K^T (T diag(colw))^T and U = T diag(beta) V; wave 3 (which
-  // reads every K^T fragment) also leaves them for the chain
-  // (in two halves of 4 column tiles: 32 accumulator registers instead of 64)
-  const int nsteps = p >= 2 ? 2 : 1;
-  bf16x8 whi[2], wlo[2], uhi[2], ulo[2];
+  // ---- -W = -(T diag(colw) K), as W^T tiles K^T (T diag(colw))^T, for the
+  // column tiles 2p and 2p + 1 over every position tile (T's rows from L.tx):
+  // 24 products on every wave; the K^T fragments it reads are also left for
+  // the chain.  U = T diag(beta) V is formed by the chain waves in the same
+  // interval (loc_u).
+  bf16x8 kt[2][2];
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const f32x4 cw0 = *reinterpret_cast<const f32x4 *>(L.colw_s + 32 * s + 4 * g4);
-    const f32x4 cw1 = *reinterpret_cast<const f32x4 *>(L.colw_s + 32 * s + 16 + 4 * g4);
-    const f32x4 be0 = *reinterpret_cast<const f32x4 *>(L.beta_s + 32 * s + 4 * g4);
-    const f32x4 be1 = *reinterpret_cast<const f32x4 *>(L.beta_s + 32 * s + 16 + 4 * g4);
-    pack_hilo(trow[2 * s] * cw0, trow[2 * s + 1] * cw1, whi[s], wlo[s]);
-    pack_hilo(trow[2 * s] * be0, trow[2 * s + 1] * be1, uhi[s], ulo[s]);
-  }
-#pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    f32x4 wt[4], ut[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      wt[q] = z4;
-      ut[q] = z4;
-    }
+  for (int jn = 0; jn < 2; ++jn)
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      if (s < nsteps) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int nb = 4 * half + q;
-          const bf16x8 kt = frag_tr(kn, s, 16 * nb, lane);
-          const bf16x8 vf = frag_tr(vn, s, 16 * nb, lane);
-          if (p == 3) L.ktf[(2 * nb + s) * 64 + lane] = __builtin_bit_cast(u32x4, kt);
-          wt[q] = mfma(kt, whi[s], wt[q]);
-          wt[q] = mfma(kt, wlo[s], wt[q]);
-          ut[q] = mfma(uhi[s], vf, ut[q]);
-          ut[q] = mfma(ulo[s], vf, ut[q]);
-        }
-      }
+      kt[jn][s] = frag_tr(kn, s, 16 * (2 * p + jn), lane);
+      L.ktf[(2 * (2 * p + jn) + s) * 64 + lane] = __builtin_bit_cast(u32x4, kt[jn][s]);
     }
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-      L.wb[(4 * p + 2 * half + s2) * 64 + lane] = __builtin_bit_cast(u32x4, pack_hi(-wt[2 * s2], -wt[2 * s2 + 1]));
+  for (int pt = 0; pt < 4; ++pt) {
+    f32x4 w0 = z4, w1 = z4;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) L.ub[(4 * (4 * half + q) + p) * 64 + lane] = ut[q];
+    for (int s = 0; s < (pt >= 2 ? 2 : 1); ++s) {  // T's rows 0..31 end at column 31
+      const f32x4 cw0 = *reinterpret_cast<const f32x4 *>(L.colw_s + 32 * s + 4 * g4);
+      const f32x4 cw1 = *reinterpret_cast<const f32x4 *>(L.colw_s + 32 * s + 16 + 4 * g4);
+      bf16x8 whi, wlo;
+      pack_hilo(L.tx[(4 * pt + 2 * s) * 64 + lane] * cw0, L.tx[(4 * pt + 2 * s + 1) * 64 + lane] * cw1, whi, wlo);
+      w0 = mfma(kt[0][s], whi, w0);
+      w0 = mfma(kt[0][s], wlo, w0);
+      w1 = mfma(kt[1][s], whi, w1);
+      w1 = mfma(kt[1][s], wlo, w1);
+    }
+    L.wb[(4 * pt + p) * 64 + lane] = __builtin_bit_cast(u32x4, pack_hi(-w0, -w1));
   }
   lds_barrier();  // (7) the chunk's operands are in LDS
+}
+
+// U = T diag(beta) V for the column tiles 2q and 2q + 1 over every position
+// tile, by chain wave 4 + q between barriers 6 and 7 of the chunk's
+// preparation: T's rows from L.tx, V's rows from LDS (written before barrier 6).
+__device__ __forceinline__ void loc_u(const LocLds &L, int q, int lane) {
+  const int g4 = lane >> 4;
+  const uint16_t *vn = reinterpret_cast<const uint16_t *>(L.s16k);
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+  bf16x8 vf[2][2];
+#pragma unroll
+  for (int jn = 0; jn < 2; ++jn)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) vf[jn][s] = frag_tr(vn, s, 16 * (2 * q + jn), lane);
+#pragma unroll
+  for (int pt = 0; pt < 4; ++pt) {
+    f32x4 u0 = z4, u1 = z4;
+#pragma unroll
+    for (int s = 0; s < (pt >= 2 ? 2 : 1); ++s) {
+      const f32x4 be0 = *reinterpret_cast<const f32x4 *>(L.beta_s + 32 * s + 4 * g4);
+      const f32x4 be1 = *reinterpret_cast<const f32x4 *>(L.beta_s + 32 * s + 16 + 4 * g4);
+      bf16x8 uhi, ulo;
+      pack_hilo(L.tx[(4 * pt + 2 * s) * 64 + lane] * be0, L.tx[(4 * pt + 2 * s + 1) * 64 + lane] * be1, uhi, ulo);
+      u0 = mfma(uhi, vf[0][s], u0);
+      u0 = mfma(ulo, vf[0][s], u0);
+      u1 = mfma(uhi, vf[1][s], u1);
+      u1 = mfma(ulo, vf[1][s], u1);
+    }
+    L.ub[(4 * (2 * q) + pt) * 64 + lane] = u0;
+    L.ub[(4 * (2 * q + 1) + pt) * 64 + lane] = u1;
+  }
 }
 
 
@@ -1564,6 +1620,7 @@ __global__ __launch_bounds__(64 * LOC_WAVES) void chunk_local_kernel(ChunkArgs a
   __shared__ u32x4 ktf[16 * 64], wb[16 * 64], qp2[2][16 * 64], ab2[2][LOC_NB_A * 64];
   __shared__ f32x4 ub[32 * 64];
   __shared__ __align__(16) float sc2[2][SCAL], gam_s[CK], beta_s[CK], nk_s[CK], nq_s[CK], colw_s[CK];
+  __shared__ f32x4 tx[16 * 64];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1594,7 +1651,7 @@ __global__ __launch_bounds__(64 * LOC_WAVES) void chunk_local_kernel(ChunkArgs a
       // it are recomputed in the loop instead of hoisted out of it and spilled
       int tk = tid;
       asm volatile("" : "+v"(tk));
-      const LocLds L{kn, s16k, ktf, qp2[k & 1], wb, ub, ab2[k & 1], sc2[k & 1], gam_s, beta_s, nk_s, nq_s, colw_s};
+      const LocLds L{kn, s16k, ktf, qp2[k & 1], wb, ub, ab2[k & 1], sc2[k & 1], gam_s, beta_s, nk_s, nq_s, colw_s, tx};
       loc_prep(a, in, L, chunk_len(k), tk, [&] {
         if (k + 1 < nch) loc_load(a, in, s0 + static_cast<int64_t>(k + 1) * CK, chunk_len(k + 1), h, hk, tk);
       });
@@ -1624,10 +1681,20 @@ __global__ __launch_bounds__(64 * LOC_WAVES) void chunk_local_kernel(ChunkArgs a
   }
   typedef typename std::conditional<BF16_OUT, uint16_t, float>::type OT;
   const int64_t ostep = static_cast<int64_t>(a.Hv) * DV;
+  // the chain waves' share of the preparation of chunk k: U, between barriers 6 and 7
+  const LocLds Lu{kn, s16k, ktf, nullptr, wb, ub, nullptr, nullptr, gam_s, beta_s, nk_s, nq_s, colw_s, tx};
+  auto prep_share = [&](int k) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));  // per call: keeps LLVM from hoisting loc_u's LDS addresses into the loop
+    if (k < nch) loc_u(Lu, cw, ln);
+  };
   // step 0: the preparation of chunk 0 alone
-  if (nch > 0)
+  if (nch > 0) {
 #pragma unroll 1
-    for (int b = 0; b < 7; ++b) lds_barrier();
+    for (int b = 0; b < 6; ++b) lds_barrier();  // (1) .. (6)
+    prep_share(0);
+    lds_barrier();  // (7)
+  }
   for (int k = 1; k <= nch; ++k) {
     const int c = k - 1;
     const u32x4 *qp = qp2[c & 1], *ab = ab2[c & 1];
@@ -1711,7 +1778,9 @@ __global__ __launch_bounds__(64 * LOC_WAVES) void chunk_local_kernel(ChunkArgs a
         }
       }
 #pragma unroll 1
-    for (int b = 1; b < 7; ++b) lds_barrier();  // (2) .. (7)
+    for (int b = 1; b < 6; ++b) lds_barrier();  // (2) .. (6)
+    prep_share(k);
+    lds_barrier();  // (7)
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j)
