@@ -94,7 +94,8 @@ const char *gdn_last_error_string(void);
  *             token t (requires cu_seqlens == NULL)
  *   cu_seqlens int32 [n_seqs + 1] (device) or NULL for n_seqs x T tokens
  *   scale     multiplier of q after the optional l2norm (K^-1/2 by default)
- * Requires K == V == 128.
+ * Requires K in {64, 128, 256} and V a positive multiple of 32 (K == V == 128
+ * is the build the decode figures are measured on).
  */
 int gdn_recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
                       int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,
@@ -144,7 +145,9 @@ int gdn_recurrent_fwd_gated(const void *q, const void *k, const void *v, int qkv
  *   o   [tokens, Hv, V] o_dtype, contiguous
  *   workspace  device scratch of at least gdn_chunk_workspace_bytes(...),
  *              256-byte aligned (unused, may be NULL, when that is 0)
- * Requires K == V == 128 and q/k/v in bf16.
+ * Requires K == V == 128 and q/k/v in bf16 (other head dims and fp16 / fp32
+ * q/k/v: gdn_recurrent_fwd, the token recurrence, which the Python entry
+ * chunk_gated_delta_rule calls for them).
  */
 int gdn_chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
                   int64_t q_stride_t, int64_t k_stride_t, int64_t v_stride_t,

@@ -1,11 +1,13 @@
 // Token recurrence of the gated delta rule (decode / spec-verify / small-T).
 //
-// One workgroup owns a [128 x VT] column slice of one (sequence, v-head)
-// state and keeps it in registers for all of the sequence's tokens: the
+// One workgroup owns a [KD x VT] column slice of one (sequence, v-head)
+// state (KD = 128 by default; 64 and 256 are also built, and any v head dim
+// that is a multiple of VT) and keeps it in registers for all of the
+// sequence's tokens: the
 // state is read from HBM once and written once, so decode is a pure stream
 // of the fp32 state (the HBM roofline).  Thread mapping (NT = 2*VT threads):
 //   columns: 4 per thread (float4), TPR = VT/4 threads span the slice;
-//   rows:    8 row groups, thread row group rg owns rows rg + 8r, r < 16.
+//   rows:    8 row groups, thread row group rg owns rows rg + 8r, r < KD / 8.
 // Per token the two K-reductions k~^T S and q~^T S are done together: in
 // registers over 16 rows, xor-shuffles across the row groups of a wave, and
 // LDS across waves when VT > 32.  The output uses
@@ -22,8 +24,8 @@ namespace {
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
 
-constexpr int KD = 128;  // head dim of k (rows of the state)
-constexpr int VD = 128;  // head dim of v (columns of the state)
+constexpr int KD_DEFAULT = 128;  // head dim of k (rows of the state) of the tuned build
+constexpr int VD_DEFAULT = 128;  // head dim of v (columns of the state)
 
 struct RecArgs {
   const void *q, *k, *v;
@@ -39,6 +41,7 @@ struct RecArgs {
   float *snap;
   const int32_t *cu;
   int n_seqs, T, Hk, Hv;
+  int V;  // v head dim (a multiple of the workgroup's columns)
   int64_t total;
   float scale;
   int l2norm;
@@ -84,13 +87,17 @@ constexpr int64_t REC_CAP_MIN_BLOCKS = 2304;   // 1.5 rounds of 6 per CU on 256 
 constexpr unsigned REC_CAP_LDS = 24 * 1024;    // + 1 KiB static: 6 per CU in 160 KiB
 constexpr unsigned REC_SNAP_CAP_LDS = 36 * 1024;  // + 1 KiB static: 4 per CU
 
-template <int VT, int NT>
+// KD: k head dim (64, 128 or 256); VDC: v head dim, or 0 for a.V
+template <int VT, int NT, int KD, int VDC>
 __global__ __launch_bounds__(NT) void recurrent_kernel(RecArgs a) {
   constexpr int NW = NT / 64;
   constexpr int TPR = VT / 4;     // threads per state row
   constexpr int NRG = NT / TPR;   // row groups
   constexpr int RPT = KD / NRG;   // rows per thread
-  constexpr int NSPLIT = VD / VT;
+  constexpr int QE = KD / 64;     // q and k elements per lane
+  static_assert(KD % 64 == 0 && KD % NRG == 0, "k head dim");
+  const int VD = VDC ? VDC : a.V;
+  const int NSPLIT = VD / VT;
 
   __shared__ float qs_l[KD];
   __shared__ float ks_l[KD];
@@ -128,16 +135,16 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(RecArgs a) {
   // A token's inputs as raw bits: this lane's two elements of q and k, its
   // four columns of v, and the gates.
   struct TokIn {
-    uint32_t q[2], k[2], v[4];
+    uint32_t q[QE], k[QE], v[4];
     GateRaw gate;
   };
   auto tok_load = [&](int64_t tok) {
     TokIn r;
-    const int64_t qoff = tok * a.qs + (int64_t)hk * KD + 2 * lane;
-    const int64_t koff = tok * a.ks + (int64_t)hk * KD + 2 * lane;
+    const int64_t qoff = tok * a.qs + (int64_t)hk * KD + QE * lane;
+    const int64_t koff = tok * a.ks + (int64_t)hk * KD + QE * lane;
     const int64_t vo = tok * a.vs + (int64_t)h * VD + col0;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < QE; ++i) {
       r.q[i] = load_bits(a.q, qoff + i, a.qkv_dt);
       r.k[i] = load_bits(a.k, koff + i, a.qkv_dt);
     }
@@ -163,7 +170,7 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(RecArgs a) {
   // rg + 8r sit 4 KiB apart, an offset carried in a scalar register, so the
   // 16 accesses share one vector offset.
   const int voff = (rg * VD + col0) * 4;
-  constexpr int ROW8 = NRG * VD * 4;  // bytes between a thread's rows
+  const int ROW8 = NRG * VD * 4;  // bytes between a thread's rows
   // (a row with no slot gets an empty range: its loads read zeros without
   // touching memory, so the loads are issued on one path whatever the row)
   auto state_rsrc = [&](const float *pool, int64_t row) {
@@ -186,20 +193,28 @@ __global__ __launch_bounds__(NT) void recurrent_kernel(RecArgs a) {
 
   for (int t = 0; t < len; ++t) {
     const int64_t tok = t0 + t;
-    // ---- q/k prologue: every wave reduces the full 128-vectors itself
-    const float q0 = bits_to_f32(cur.q[0], a.qkv_dt), q1 = bits_to_f32(cur.q[1], a.qkv_dt);
-    const float k0 = bits_to_f32(cur.k[0], a.qkv_dt), k1 = bits_to_f32(cur.k[1], a.qkv_dt);
-    const float sqq = wave_sum(q0 * q0 + q1 * q1);
-    const float skk = wave_sum(k0 * k0 + k1 * k1);
-    const float sqk = wave_sum(q0 * k0 + q1 * k1);
+    // ---- q/k prologue: every wave reduces the full KD-vectors itself
+    float qv[QE], kv[QE], pqq = 0.f, pkk = 0.f, pqk = 0.f;
+#pragma unroll
+    for (int i = 0; i < QE; ++i) {
+      qv[i] = bits_to_f32(cur.q[i], a.qkv_dt);
+      kv[i] = bits_to_f32(cur.k[i], a.qkv_dt);
+      pqq += qv[i] * qv[i];
+      pkk += kv[i] * kv[i];
+      pqk += qv[i] * kv[i];
+    }
+    const float sqq = wave_sum(pqq);
+    const float skk = wave_sum(pkk);
+    const float sqk = wave_sum(pqk);
     const float rq = a.l2norm ? rsqrtf(sqq + 1e-6f) : 1.f;
     const float rk = a.l2norm ? rsqrtf(skk + 1e-6f) : 1.f;
     const float qsc = rq * a.scale;
     if (wave == 0) {
-      qs_l[2 * lane] = q0 * qsc;
-      qs_l[2 * lane + 1] = q1 * qsc;
-      ks_l[2 * lane] = k0 * rk;
-      ks_l[2 * lane + 1] = k1 * rk;
+#pragma unroll
+      for (int i = 0; i < QE; ++i) {
+        qs_l[QE * lane + i] = qv[i] * qsc;
+        ks_l[QE * lane + i] = kv[i] * rk;
+      }
     }
     const float qk = sqk * qsc * rk;
     float gl, bt;
@@ -311,8 +326,9 @@ int recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
                   const int32_t *cu_seqlens, int32_t n_seqs, int32_t T,
                   int32_t Hk, int32_t Hv, int32_t K, int32_t V,
                   float scale, int l2norm_qk, void *stream, const char *name) {
-  if (K != KD || V != VD)
-    return fail(GDN_ERR_UNSUPPORTED, "%s: K=%d V=%d; only K=V=128 is built", name, K, V);
+  if ((K != 64 && K != 128 && K != 256) || V <= 0 || V % REC_VT)
+    return fail(GDN_ERR_UNSUPPORTED, "%s: K=%d V=%d; K must be 64, 128 or 256 and V a positive multiple of %d",
+                name, K, V, REC_VT);
   if (n_seqs < 0 || T < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk)
     return fail(GDN_ERR_INVALID_ARGUMENT, "%s: bad sizes n_seqs=%d T=%d Hk=%d Hv=%d", name, n_seqs, T, Hk, Hv);
   if (!valid_dtype(qkv_dtype) || !valid_dtype(gate.dt) || !valid_dtype(o_dtype))
@@ -330,18 +346,26 @@ int recurrent_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
                 static_cast<long long>(state_in_rows), static_cast<long long>(state_out_rows), n_seqs);
   if (q_stride_t < Hk * K || k_stride_t < Hk * K || v_stride_t < Hv * V)
     return fail(GDN_ERR_INVALID_ARGUMENT, "%s: token stride smaller than a row", name);
-  const int64_t n_blocks = static_cast<int64_t>(n_seqs) * Hv * (VD / REC_VT);
+  const int64_t n_blocks = static_cast<int64_t>(n_seqs) * Hv * (V / REC_VT);
   if (n_blocks > 0x7fffffff) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: grid too large", name);
 
   RecArgs a{q, k, v, q_stride_t, k_stride_t, v_stride_t, gate, state_in, state_in_idx, state_in_rows,
-            state_out, state_out_idx, state_out_rows, o, snapshots, cu_seqlens, n_seqs, T, Hk, Hv,
+            state_out, state_out_idx, state_out_rows, o, snapshots, cu_seqlens, n_seqs, T, Hk, Hv, V,
             cu_seqlens ? static_cast<int64_t>(T) : static_cast<int64_t>(n_seqs) * T,
             scale, l2norm_qk, qkv_dtype, o_dtype};
   const bool capped = n_blocks > REC_CAP_MIN_BLOCKS && (T == 1 || snapshots);
   a.head_major = capped;
   const unsigned lds = !capped ? 0u : T == 1 ? REC_CAP_LDS : REC_SNAP_CAP_LDS;
-  hipLaunchKernelGGL((recurrent_kernel<REC_VT, REC_NT>), dim3(static_cast<unsigned>(n_blocks)), dim3(REC_NT), lds,
-                     static_cast<hipStream_t>(stream), a);
+  const dim3 grid(static_cast<unsigned>(n_blocks)), block(REC_NT);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (K == KD_DEFAULT && V == VD_DEFAULT)
+    hipLaunchKernelGGL((recurrent_kernel<REC_VT, REC_NT, KD_DEFAULT, VD_DEFAULT>), grid, block, lds, st, a);
+  else if (K == 64)
+    hipLaunchKernelGGL((recurrent_kernel<REC_VT, REC_NT, 64, 0>), grid, block, lds, st, a);
+  else if (K == 128)
+    hipLaunchKernelGGL((recurrent_kernel<REC_VT, REC_NT, 128, 0>), grid, block, lds, st, a);
+  else
+    hipLaunchKernelGGL((recurrent_kernel<REC_VT, REC_NT, 256, 0>), grid, block, lds, st, a);
   return check_launch(name);
 }
 

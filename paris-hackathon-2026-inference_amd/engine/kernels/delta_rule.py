@@ -66,9 +66,11 @@ def chunk_gated_delta_rule(
 
     Shapes: query, key ``[B, T, Hk, K]``; value ``[B, T, Hv, V]``; g, beta
     ``[B, T, Hv]``; ``initial_state`` ``[N, Hv, K, V]`` fp32 (N = B, or the
-    number of sequences with ``cu_seqlens`` [N+1], B = 1).  K = V = 128;
-    q/k/v bf16 (MFMA chunk kernels), fp16 or fp32 (token recurrence);
-    ``chunk_size`` any positive value (computed with 64).
+    number of sequences with ``cu_seqlens`` [N+1], B = 1).  bf16 q/k/v with
+    K = V = 128 run the MFMA chunk kernels; fp16 or fp32 q/k/v, and K = 64 or
+    256 or V another multiple of 32, run the token recurrence (exact in the
+    inputs as given, one token after another); ``chunk_size`` any positive
+    value (computed with 64).
 
     Returns ``(core_attn_out [B, T, Hv, V] in query's dtype,
     last_recurrent_state [N, Hv, K, V] fp32 or None)`` as the reference does
@@ -203,8 +205,9 @@ def _chunk(query, key, value, gates, chunk_size, initial_state, output_final_sta
     lib = _lib.load()
     o = torch.empty((b, t, hv, dv), dtype=query.dtype, device=dev)
     name, gate_args = gates
-    if query.dtype != torch.bfloat16:
-        # fp32 / fp16 q, k, v: the token recurrence, fp32 math on the inputs as given
+    if query.dtype != torch.bfloat16 or dk != 128 or dv != 128:
+        # fp32 / fp16 q, k, v, or head dims the chunk kernels are not built for:
+        # the token recurrence, fp32 math on the inputs as given
         rec = {"gdn_chunk_fwd": "gdn_recurrent_fwd", "gdn_chunk_fwd_gated": "gdn_recurrent_fwd_gated"}[name]
         st = getattr(lib, rec)(
             _lib.ptr(qx), _lib.ptr(kx), _lib.ptr(vx), _lib.dtype_code(query, "query"), qs, ks, vs,

@@ -54,8 +54,13 @@ def _rec_call(lib, **over):
 
 
 def test_recurrent_rejects_unsupported_head_dim(lib):
-    assert _rec_call(lib, kd=64, vd=64) == 2
-    assert "K=64" in lib.gdn_last_error_string().decode()
+    # built: K in {64, 128, 256}, V a positive multiple of 32 (valid sizes are
+    # not called here: they would launch)
+    assert _rec_call(lib, kd=96, vd=128) == 2
+    assert "K=96" in lib.gdn_last_error_string().decode()
+    assert _rec_call(lib, kd=64, vd=48) == 2
+    assert _rec_call(lib, kd=128, vd=0) == 2
+    assert _rec_call(lib, kd=512, vd=128) == 2
 
 
 def test_recurrent_rejects_bad_gqa_and_nulls(lib):
@@ -153,7 +158,7 @@ def test_gated_entry_points_check_their_gate_arguments(lib):
     assert _rec_gated_call(lib, dt_bias=None) == 1
     assert _rec_gated_call(lib, ab_stride=16) == 1         # stride below Hv
     assert _rec_gated_call(lib, ab_dtype=7) == 1
-    assert _rec_gated_call(lib, kd=64, vd=64) == 2
+    assert _rec_gated_call(lib, kd=96, vd=64) == 2          # K not built
     # chunk variant: same gate checks ahead of its own (A_log, then workspace)
     chunk = dict(q=256, k=256, v=256, qkv_dtype=1, qs=4096, ks=4096, vs=4096, a=1, b=1, ab_dtype=1, ab_stride=32,
                  A_log=None, dt_bias=1, h0=None, h0_idx=None, h0_rows=0, hT=None, hT_idx=None, hT_rows=0,

@@ -137,6 +137,20 @@ def test_chunk_equals_recurrence_small_dims(d):
     assert np.abs(o1 - o2).max() < 1e-11 and gdn.state_rel_err(s2, s1) < 1e-11
 
 
+@pytest.mark.parametrize("dk,dv", [(64, 96), (32, 160), (256, 32)])
+def test_chunk_equals_recurrence_unequal_dims(dk, dv):
+    """Pins the oracle at the head dims the recurrence kernel also builds
+    (K 64 / 256, V a multiple of 32, K != V)."""
+    rng = np.random.default_rng(dk * 1000 + dv)
+    q, k, _, g, beta, _ = rand_inputs(1, 70, 1, 2, dk, rng=rng, h0_std=0)
+    v = rng.standard_normal((1, 70, 2, dv))
+    h0 = rng.standard_normal((1, 2, dk, dv)) * 0.1
+    o1, s1 = gdn.recurrent_gated_delta_rule(q, k, v, g, beta, h0)
+    o2, s2 = gdn.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=h0)
+    assert o1.shape == (1, 70, 2, dv) and s1.shape == (1, 2, dk, dv)
+    assert np.abs(o1 - o2).max() < 1e-10 and gdn.state_rel_err(s2, s1) < 1e-10
+
+
 def test_forward_substitution_is_the_inverse():
     c = 64
     lower = np.tril(RNG.standard_normal((3, c, c)) * 0.3, -1)
