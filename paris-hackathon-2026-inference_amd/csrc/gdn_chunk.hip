@@ -468,11 +468,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
     if (g4 == 0) nq_s[irow] = (a.l2norm ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
   }
   if (p == 0) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float x = __shfl_up(gv, off, 64);
-      if (lane >= off) gv += x;
-    }
+    gv = wave_incl_scan(gv);  // chunk-local cumsum of g
     gam_s[lane] = gv;
     beta_s[lane] = bv;
   }
@@ -1418,11 +1414,7 @@ __device__ __forceinline__ void loc_prep(const ChunkArgs &a, const LocIn &in, co
     if (g4 == 0) L.nq_s[irow] = (a.l2norm ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
   }
   if (p == 0) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float x = __shfl_up(gv, off, 64);
-      if (lane >= off) gv += x;
-    }
+    gv = wave_incl_scan(gv);  // chunk-local cumsum of g
     L.gam_s[lane] = gv;
     L.beta_s[lane] = bv;
   }

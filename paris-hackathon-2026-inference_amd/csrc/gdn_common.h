@@ -160,6 +160,26 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave on DPP (no LDS round
+// trip): shifts by 1, 2, 4, 8 within each row of 16 lanes (a lane whose
+// source lies before its row's start adds 0), then row 0's total into row 1
+// and row 2's into row 3 (row_bcast:15, rows 1 and 3 enabled), then the
+// total of lanes 0..31 into rows 2 and 3 (row_bcast:31).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_from(float v) {
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf, false));
+}
+__device__ __forceinline__ float wave_incl_scan(float x) {
+  x += dpp_from<0x111, 0xf>(x);  // row_shr:1
+  x += dpp_from<0x112, 0xf>(x);  // row_shr:2
+  x += dpp_from<0x114, 0xf>(x);  // row_shr:4
+  x += dpp_from<0x118, 0xf>(x);  // row_shr:8
+  x += dpp_from<0x142, 0xa>(x);  // row_bcast:15
+  x += dpp_from<0x143, 0xc>(x);  // row_bcast:31
+  return x;
+}
+
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
