@@ -21,9 +21,13 @@ namespace {
 
 constexpr int CPT = 8;         // channels per thread
 constexpr int CONV_NT = 256;   // threads per workgroup
-// Tokens per workgroup tile: 64 once that still gives every CU a
-// workgroup, else 32 (a 64-token tile halves the re-read 3-token halo and
-// keeps more loads in flight per thread; short inputs need the 32-token grid)
+// Tokens per workgroup tile: 32 when a 64-token grid would leave CUs
+// without a workgroup (short inputs), else the longest of 64, 56 and 48
+// whose busiest CU streams the fewest tokens, ceil(workgroups / CUs) x tile:
+// a long tile halves the re-read 3-token halo against 32 and keeps more loads
+// in flight per thread, and a grid that is not a whole number of rounds over
+// the CUs leaves some CUs one workgroup more than the rest (configuration 3,
+// 13,794 tokens: 864 workgroups of 64 tokens, 3.4 per CU; 988 of 56)
 constexpr int TILE_SHORT = 32, TILE_LONG = 64;
 constexpr int CONV_CUS = 256;
 
@@ -372,10 +376,23 @@ template <typename T, int SL>
 int launch_fwd(const ConvArgs &a, hipStream_t s) {
   const unsigned gx = (a.C / CPT + CONV_NT - 1) / CONV_NT;
   if (a.total > 0) {
-    if (gx * ((a.total + TILE_LONG - 1) / TILE_LONG) >= CONV_CUS)
-      launch_tiles<T, SL, TILE_LONG>(a, gx, s);
-    else
+    auto busiest = [&](int64_t tile) {  // tokens streamed by the CU with the most workgroups
+      const int64_t n = gx * ((a.total + tile - 1) / tile);
+      return (n + CONV_CUS - 1) / CONV_CUS * tile;
+    };
+    if (gx * ((a.total + TILE_LONG - 1) / TILE_LONG) < CONV_CUS) {
       launch_tiles<T, SL, TILE_SHORT>(a, gx, s);
+    } else {
+      int tile = TILE_LONG;
+      for (const int t : {56, 48})
+        if (busiest(t) < busiest(tile)) tile = t;
+      if (tile == 56)
+        launch_tiles<T, SL, 56>(a, gx, s);
+      else if (tile == 48)
+        launch_tiles<T, SL, 48>(a, gx, s);
+      else
+        launch_tiles<T, SL, TILE_LONG>(a, gx, s);
+    }
   }
   if (a.st_out)
     hipLaunchKernelGGL((conv_final_state_kernel<T, SL>), dim3((a.C + CONV_NT - 1) / CONV_NT, a.n_seqs),
