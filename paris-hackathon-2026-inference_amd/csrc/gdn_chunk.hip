@@ -1604,6 +1604,39 @@ __device__ __forceinline__ void loc_u(const LocLds &L, int q, int lane) {
 // chunk's rows are requested after barrier 6, when the current ones are in
 // LDS.  143 KiB of LDS: one workgroup per CU.
 constexpr int LOC_WAVES = 8;
+constexpr int LOC_LPT_MAX = 64 * LOC_WAVES;  // sequences ranked in the prologue, one per thread
+
+// Longest sequences first.  The per-pair workgroups run one per CU, each for
+// its sequence's whole length, and start in workgroup order as CUs free up;
+// in sequence order a long sequence whose pairs come late starts after a
+// short one has finished (configuration 3: 39 chunk steps on the busiest CU
+// against 32, its longest sequence).  The workgroup for slot n takes the
+// sequence whose length ranks n-th, decreasing, ties by index: each thread
+// ranks one sequence against all the lengths (from cu_seqlens, in LDS the
+// preparation does not use before barrier 1).  Returns n unchanged for more
+// than LOC_LPT_MAX sequences.
+__device__ __forceinline__ int loc_longest_first(const ChunkArgs &a, int n, int tid, int *lds) {
+  if (a.n_seqs > LOC_LPT_MAX) return n;
+  int *lens = lds, *sel = lds + LOC_LPT_MAX;
+  if (tid < a.n_seqs) {
+    int64_t s0;
+    int len;
+    seq_bounds(a, tid, &s0, &len);
+    lens[tid] = len;
+  }
+  __syncthreads();
+  if (tid < a.n_seqs) {
+    const int lm = lens[tid];
+    int r = 0;
+    for (int j = 0; j < a.n_seqs; ++j) {
+      const int lj = lens[j];
+      r += (lj > lm) || (lj == lm && j < tid);
+    }
+    if (r == n) *sel = tid;
+  }
+  __syncthreads();
+  return *sel;
+}
 
 template <bool BF16_OUT>
 __global__ __launch_bounds__(64 * LOC_WAVES) void chunk_local_kernel(ChunkArgs a) {
@@ -1626,6 +1659,7 @@ __global__ __launch_bounds__(64 * LOC_WAVES) void chunk_local_kernel(ChunkArgs a
     n = g / (a.Hv / ratio);
     h = (g % (a.Hv / ratio)) * ratio + m;
   }
+  if (a.cu && a.n_seqs > 1) n = __builtin_amdgcn_readfirstlane(loc_longest_first(a, n, tid, reinterpret_cast<int *>(s16k)));
   const int hk = h / ratio;
   int64_t s0;
   int slen;

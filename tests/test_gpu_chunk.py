@@ -433,3 +433,34 @@ def test_per_pair_kernel_varlen_on_a_slot_pool():
     assert torch.equal(pool[2].cpu(), pool0[2])  # the empty row passed its state through
     untouched = [i for i in range(12) if i not in (7, 2, 9, 0, 11, 5)]
     assert torch.equal(pool[untouched].cpu(), pool0[untouched])
+
+
+@pytest.mark.parametrize("n_seqs", [300, 520])
+def test_per_pair_kernel_many_varlen_sequences(n_seqs):
+    """Many packed sequences of 0..90 tokens (some empty) on the per-pair
+    kernel, final states out: with 300 the workgroups take the sequences
+    longest first (the workgroup for slot n ranks the lengths and takes the
+    n-th longest), with 520 (more than one per thread of the ranking) in
+    sequence order.  Every 9th sequence, the longest and the first empty ones
+    against the oracle (each sequence is independent)."""
+    from engine.kernels import _lib
+    rng = np.random.default_rng(n_seqs)
+    lens = rng.integers(0, 91, n_seqs)
+    lens[::37] = 0
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    total = int(cu[-1])
+    assert _lib.load().gdn_chunk_workspace_bytes(n_seqs, total, 32, 128, 128) == 0  # the per-pair kernel
+    c = configs.config2(seed=n_seqs, t=total)
+    print(f"per-pair kernel, {n_seqs} varlen sequences", flush=True)
+    o, s = chunk_gated_delta_rule(*(c[x].to(DEV) for x in ("q", "k", "v", "g", "beta")), output_final_state=True,
+                                  use_qk_l2norm_in_kernel=True, cu_seqlens=torch.from_numpy(cu).to(DEV))
+    empty = np.nonzero(lens == 0)[0]
+    check = sorted(set(range(0, n_seqs, 9)) | {int(np.argmax(lens))} | {int(i) for i in empty[:3]})
+    for i in check:
+        a, b = int(cu[i]), int(cu[i + 1])
+        if a == b:
+            assert torch.count_nonzero(s[i]).item() == 0, i  # zero initial state, no tokens
+            continue
+        o_ref, s_ref = gdn.chunk_gated_delta_rule(*(c[x][:, a:b].float().numpy() for x in ("q", "k", "v", "g", "beta")))
+        assert np.abs(np64(o[:, a:b]) - o_ref).max() < O_TOL, i
+        assert gdn.state_rel_err(np64(s[i:i + 1]), s_ref) < S_TOL, i
