@@ -1314,7 +1314,6 @@ enum { SC_SQ = 0, SC_SK = CK, SC_EL = 2 * CK };  // the scalar block: sq[64], sk
 struct LocIn {  // one chunk's inputs in prep thread tid's registers (tid < 256)
   u32x4 ku[4], vu[4];
   bf16x8 qf[4];
-  GateRaw graw;
 };
 
 struct LocLds {
@@ -1353,16 +1352,32 @@ __device__ __forceinline__ void loc_load(const ChunkArgs &a, LocIn &in, int64_t 
     const u32x2 x1 = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rq, off + 32, 0, 0));
     in.qf[s] = as_bf16x8(u32x4{x0.x, x0.y, x1.x, x1.y});
   }
-  in.graw = GateRaw{0u, 0u, 0.f, 0.f};
-  if (p == 0 && lane < len) {
+}
+
+// One chunk's gates, raw, into chain wave 4's registers (lane = position;
+// positions past the chunk's end read nothing), and from them the gates
+// and their chunk-local cumsum into LDS (gam_s, beta_s).  The chain wave
+// forms them for chunk k before barrier 1 of step k, in the time it waits
+// there, instead of the preparing wave 0 ahead of its own work.
+__device__ __forceinline__ GateRaw loc_gates_load(const ChunkArgs &a, int64_t t0, int len, int h, int lane) {
+  GateRaw g{0u, 0u, 0.f, 0.f};
+  if (lane < len) {
     const int64_t gi = (t0 + lane) * a.gate.stride + h;
-    in.graw.ga = load_bits(a.gate.g_or_a, gi, a.gate.A_log ? a.gate.dt : GDN_DTYPE_F32);
-    in.graw.gb = load_bits(a.gate.beta_or_b, gi, a.gate.dt);
+    g.ga = load_bits(a.gate.g_or_a, gi, a.gate.A_log ? a.gate.dt : GDN_DTYPE_F32);
+    g.gb = load_bits(a.gate.beta_or_b, gi, a.gate.dt);
   }
   if (a.gate.A_log) {
-    in.graw.a_log = a.gate.A_log[h];
-    in.graw.dt_bias = a.gate.dt_bias[h];
+    g.a_log = a.gate.A_log[h];
+    g.dt_bias = a.gate.dt_bias[h];
   }
+  return g;
+}
+__device__ __forceinline__ void loc_gates(const ChunkArgs &a, const GateRaw &g, int len, int lane, float *gam_s,
+                                          float *beta_s) {
+  float gv = 0.f, bv = 0.f;
+  if (lane < len) gates_from_raw(a.gate, g, &gv, &bv);
+  gam_s[lane] = wave_incl_scan(gv);  // chunk-local cumsum of g
+  beta_s[lane] = bv;
 }
 
 // Phase A of one chunk on waves 0-3 (thread tid < 256), from the registers of
@@ -1381,9 +1396,8 @@ __device__ __forceinline__ void loc_prep(const ChunkArgs &a, const LocIn &in, co
   f32x4 *txch = L.s16k + 8 * 64;    // [3 * 64] T[1][0], T[2][1], T[2][0], D layout by lane
   float(*dtr)[16 * 20] = reinterpret_cast<float(*)[16 * 20]>(L.s16k + 11 * 64);  // D -> row layout
 
-  float gv = 0.f, bv = 0.f;
-  if (p == 0 && lane < len) gates_from_raw(a.gate, in.graw, &gv, &bv);
-  // ---- K rows into LDS; K and Q row norms; chunk-local cumsum of g; the q fragments for the chain
+  // ---- K rows into LDS; K and Q row norms; the q fragments for the chain (the
+  // gates and their cumsum: chain wave 4, loc_gates, before the same barrier 1)
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int row = (tid >> 4) + 16 * it;
@@ -1412,11 +1426,6 @@ __device__ __forceinline__ void loc_prep(const ChunkArgs &a, const LocIn &in, co
     sq += __shfl_xor(sq, 16, 64);
     sq += __shfl_xor(sq, 32, 64);
     if (g4 == 0) L.nq_s[irow] = (a.l2norm ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
-  }
-  if (p == 0) {
-    gv = wave_incl_scan(gv);  // chunk-local cumsum of g
-    L.gam_s[lane] = gv;
-    L.beta_s[lane] = bv;
   }
   lds_barrier();  // (1)
 
@@ -1714,10 +1723,16 @@ __global__ __launch_bounds__(64 * LOC_WAVES) void chunk_local_kernel(ChunkArgs a
     asm volatile("" : "+v"(ln));  // per call: keeps LLVM from hoisting loc_u's LDS addresses into the loop
     if (k < nch) loc_u(Lu, cw, ln);
   };
+  // chunk k's gates by wave 4 (cw 0) before barrier 1 of step k; the raw
+  // values of chunk k + 1 requested after that barrier
+  GateRaw gnext{0u, 0u, 0.f, 0.f};
   // step 0: the preparation of chunk 0 alone
   if (nch > 0) {
+    if (cw == 0) loc_gates(a, loc_gates_load(a, s0, chunk_len(0), h, lane), chunk_len(0), lane, gam_s, beta_s);
+    lds_barrier();  // (1)
+    if (cw == 0 && nch > 1) gnext = loc_gates_load(a, s0 + CK, chunk_len(1), h, lane);
 #pragma unroll 1
-    for (int b = 0; b < 6; ++b) lds_barrier();  // (1) .. (6)
+    for (int b = 1; b < 6; ++b) lds_barrier();  // (2) .. (6)
     prep_share(0);
     lds_barrier();  // (7)
   }
@@ -1746,7 +1761,9 @@ __global__ __launch_bounds__(64 * LOC_WAVES) void chunk_local_kernel(ChunkArgs a
 #pragma unroll
         for (int j = 0; j < 2; ++j) vp[j][t] = mfma(w, sb[j][s], vp[j][t]);
       }
+    if (cw == 0 && k < nch) loc_gates(a, gnext, chunk_len(k), lane, gam_s, beta_s);
     lds_barrier();  // (1)
+    if (cw == 0 && k + 1 < nch) gnext = loc_gates_load(a, s0 + static_cast<int64_t>(k + 1) * CK, chunk_len(k + 1), h, lane);
     // interval 1: O^T = (S^T Q^T) diag(sq) + V'^T A^T, then S <- e^{gamma_63} S + K^T V''
     bf16x8 vb[2][2];
 #pragma unroll
