@@ -45,24 +45,31 @@ def raw_gates(gen, b, t, hv):
     return a, bb, A_log, dt_bias
 
 
-def test_chunk_from_projections_matches_oracle():
+@pytest.mark.parametrize("bsz,t", [(1, 200), (8, 130)])
+def test_chunk_from_projections_matches_oracle(bsz, t):
+    """Gates computed in the kernel from the raw projections: one sequence
+    (prep + scan) and B = 8 x T = 130 (256 (sequence, v-head) pairs: the
+    per-pair kernel, where a chain wave forms the gates), against the oracle
+    sequence by sequence."""
     from engine.kernels import chunk_gated_delta_rule_from_projections
     gen = torch.Generator().manual_seed(31)
-    t, hk, hv = 200, 16, 32
-    q = torch.randn(1, t, hk, 128, generator=gen).to(torch.bfloat16)
-    k = torch.randn(1, t, hk, 128, generator=gen).to(torch.bfloat16)
-    v = torch.randn(1, t, hv, 128, generator=gen).to(torch.bfloat16)
-    a, b, A_log, dt_bias = raw_gates(gen, 1, t, hv)
+    hk, hv = 16, 32
+    q = torch.randn(bsz, t, hk, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(bsz, t, hk, 128, generator=gen).to(torch.bfloat16)
+    v = torch.randn(bsz, t, hv, 128, generator=gen).to(torch.bfloat16)
+    a, b, A_log, dt_bias = raw_gates(gen, bsz, t, hv)
     a = a * 0.5 - 3.0  # moderate decays so the state carries across chunks
-    h0 = torch.randn(1, hv, 128, 128, generator=gen) * 0.1
+    h0 = torch.randn(bsz, hv, 128, 128, generator=gen) * 0.1
     o, s = chunk_gated_delta_rule_from_projections(
         q.to(DEV), k.to(DEV), v.to(DEV), a.to(torch.bfloat16).to(DEV), b.to(torch.bfloat16).to(DEV),
         A_log.to(DEV), dt_bias.to(DEV), initial_state=h0.to(DEV), output_final_state=True)
     g, beta = gdn.gdn_gates(np64(a.to(torch.bfloat16)), np64(b.to(torch.bfloat16)), np64(A_log), np64(dt_bias))
-    o_ref, s_ref = gdn.chunk_gated_delta_rule(np64(q), np64(k), np64(v), g, beta, initial_state=np64(h0))
-    err_o, err_s = np.abs(np64(o) - o_ref).max(), gdn.state_rel_err(np64(s), s_ref)
-    print(f"chunk gated: max|o-o_ref|={err_o:.3e} state rel={err_s:.3e}")
-    assert err_o < O_TOL and err_s < S_TOL
+    for i in range(bsz):
+        o_ref, s_ref = gdn.chunk_gated_delta_rule(np64(q[i:i + 1]), np64(k[i:i + 1]), np64(v[i:i + 1]),
+                                                  g[i:i + 1], beta[i:i + 1], initial_state=np64(h0[i:i + 1]))
+        err_o, err_s = np.abs(np64(o[i:i + 1]) - o_ref).max(), gdn.state_rel_err(np64(s[i:i + 1]), s_ref)
+        print(f"chunk gated B={bsz} row {i}: max|o-o_ref|={err_o:.3e} state rel={err_s:.3e}")
+        assert err_o < O_TOL and err_s < S_TOL, i
 
 
 def test_recurrent_from_projections_matches_oracle_on_a_slot_pool():
