@@ -464,3 +464,38 @@ def test_per_pair_kernel_many_varlen_sequences(n_seqs):
         o_ref, s_ref = gdn.chunk_gated_delta_rule(*(c[x][:, a:b].float().numpy() for x in ("q", "k", "v", "g", "beta")))
         assert np.abs(np64(o[:, a:b]) - o_ref).max() < O_TOL, i
         assert gdn.state_rel_err(np64(s[i:i + 1]), s_ref) < S_TOL, i
+
+
+@pytest.mark.parametrize("b,t", [(1, 200), (2, 150), (8, 130)])
+def test_fp32_output_through_the_c_abi(b, t):
+    """o in fp32 from bf16 q/k/v (the C ABI's o_dtype; the Python entry
+    returns o in q's dtype): the prep + scan path (B = 1), the persistent scan
+    (B = 2) and the per-pair kernel (B = 8 x 32 v-heads), against the oracle,
+    and rounded to bf16 equal to the bf16-output call."""
+    from engine.kernels import _lib
+    lib = _lib.load()
+    c = configs.config2(t=b * t, seed=90 + b)
+    x = {k: c[k].reshape(b, t, *c[k].shape[2:]).to(DEV) for k in ("q", "k", "v", "g", "beta")}
+    hk, hv = x["q"].shape[2], x["v"].shape[2]
+    g32, beta32 = x["g"].float().contiguous(), x["beta"].float().contiguous()
+    ws_bytes = int(lib.gdn_chunk_workspace_bytes(b, b * t, hv, 128, 128))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
+    outs = {}
+    for odt in (torch.float32, torch.bfloat16):
+        o = torch.empty(b, t, hv, 128, dtype=odt, device=DEV)
+        hT = torch.empty(b, hv, 128, 128, dtype=torch.float32, device=DEV)
+        st = lib.gdn_chunk_fwd(
+            _lib.ptr(x["q"]), _lib.ptr(x["k"]), _lib.ptr(x["v"]), _lib.dtype_code(x["q"], "q"),
+            hk * 128, hk * 128, hv * 128, _lib.ptr(g32), _lib.ptr(beta32), _lib.dtype_code(beta32, "beta"),
+            None, None, 0, _lib.ptr(hT), None, b, _lib.ptr(o), _lib.dtype_code(o, "o"),
+            None, b, t, hk, hv, 128, 128, 128 ** -0.5, 1, _lib.ptr(ws), ws_bytes, _lib.stream_of(x["q"]))
+        _lib.check(st, "gdn_chunk_fwd")
+        outs[odt] = (o, hT)
+    o32, s32 = outs[torch.float32]
+    assert torch.equal(o32.to(torch.bfloat16), outs[torch.bfloat16][0])
+    assert torch.equal(s32, outs[torch.bfloat16][1])
+    for i in range(b):
+        o_ref, s_ref = gdn.chunk_gated_delta_rule(*(c[k].reshape(b, t, *c[k].shape[2:])[i:i + 1].float().numpy()
+                                                    for k in ("q", "k", "v", "g", "beta")))
+        assert np.abs(np64(o32[i:i + 1]) - o_ref).max() < O_TOL, i
+        assert gdn.state_rel_err(np64(s32[i:i + 1]), s_ref) < S_TOL, i
