@@ -499,3 +499,18 @@ def test_fp32_output_through_the_c_abi(b, t):
                                                     for k in ("q", "k", "v", "g", "beta")))
         assert np.abs(np64(o32[i:i + 1]) - o_ref).max() < O_TOL, i
         assert gdn.state_rel_err(np64(s32[i:i + 1]), s_ref) < S_TOL, i
+
+
+def test_per_pair_kernel_repeated_qk_equals_native():
+    """The per-pair kernel with q/k repeated to the 32 v-heads (HF's layout:
+    one k-head per v-head) gives the bits of native GQA (16 k-heads), B = 8 x
+    T = 130, with an initial state and final states out."""
+    b, t = 8, 130
+    c = configs.config2(t=b * t, seed=97)
+    x = {k: c[k].reshape(b, t, *c[k].shape[2:]).to(DEV) for k in ("q", "k", "v", "g", "beta")}
+    h0 = torch.randn(b, 32, 128, 128, generator=torch.Generator().manual_seed(98)).to(DEV) * 0.1
+    o1, s1 = chunk_gated_delta_rule(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=h0,
+                                    output_final_state=True, use_qk_l2norm_in_kernel=True)
+    o2, s2 = chunk_gated_delta_rule(x["q"].repeat_interleave(2, 2), x["k"].repeat_interleave(2, 2), x["v"], x["g"],
+                                    x["beta"], initial_state=h0, output_final_state=True, use_qk_l2norm_in_kernel=True)
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
