@@ -73,3 +73,32 @@ def test_chunk_prefill_graph_replays_match_eager(t):
         torch.cuda.synchronize()
         assert torch.equal(o_graph, o_eager)
         assert torch.equal(s_graph, s_eager)
+
+
+@pytest.mark.parametrize("lens", [[1402, 1130, 590, 319, 404, 422, 421, 1909, 1501, 245, 2033, 1583, 810, 335, 401, 289],
+                                  [700, 0, 1300]])
+def test_varlen_prefill_graph_replays_match_eager(lens):
+    """Packed sequences from a graph: configuration 3's lengths (512 pairs:
+    the per-pair kernel, its workgroups ranking the lengths in the kernel) and
+    three sequences with an empty one (the persistent scan, with the chunk
+    table built on the device)."""
+    import numpy as np
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=DEV)
+    c = configs.config2(seed=13, t=int(sum(lens)))
+    q, k, v, g, beta = (c[x].to(DEV) for x in ("q", "k", "v", "g", "beta"))
+    h0 = torch.randn(len(lens), 32, 128, 128, generator=torch.Generator().manual_seed(5)).mul(0.1).to(DEV)
+
+    def run():
+        return chunk_gated_delta_rule(q, k, v, g, beta, initial_state=h0, output_final_state=True,
+                                      use_qk_l2norm_in_kernel=True, cu_seqlens=cu)
+
+    o_eager, s_eager = (t.clone() for t in run())
+    graph, (o_graph, s_graph) = capture(run)
+    for _ in range(3):
+        torch.cuda.synchronize()
+        scratch = torch.randn(1 << 20, device=DEV)  # unrelated eager work
+        del scratch
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o_graph, o_eager)
+        assert torch.equal(s_graph, s_eager)
