@@ -514,3 +514,32 @@ def test_per_pair_kernel_repeated_qk_equals_native():
     o2, s2 = chunk_gated_delta_rule(x["q"].repeat_interleave(2, 2), x["k"].repeat_interleave(2, 2), x["v"], x["g"],
                                     x["beta"], initial_state=h0, output_final_state=True, use_qk_l2norm_in_kernel=True)
     assert torch.equal(o1, o2) and torch.equal(s1, s2)
+
+
+@pytest.mark.parametrize("hk", [8, 4])
+@pytest.mark.parametrize("b,t", [(1, 200), (8, 130)])
+def test_gqa_ratios_other_than_two(hk, b, t):
+    """32 v-heads over 8 or 4 k-heads (4 or 8 v-heads per k-head) on the
+    prep + scan path (B = 1) and the per-pair kernel (B = 8 x 32 pairs), and
+    the decode recurrence, against the oracle (which repeats the k-heads)."""
+    from engine.kernels import fused_recurrent_gated_delta_rule
+    gen = torch.Generator().manual_seed(60 + hk + b)
+    q = torch.randn(b, t, hk, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(b, t, hk, 128, generator=gen).to(torch.bfloat16)
+    v = torch.randn(b, t, 32, 128, generator=gen).to(torch.bfloat16)
+    g = -torch.nn.functional.softplus(torch.randn(b, t, 32, generator=gen)) * 0.3
+    beta = torch.sigmoid(torch.randn(b, t, 32, generator=gen))
+    h0 = torch.randn(b, 32, 128, 128, generator=gen) * 0.1
+    o, s = chunk_gated_delta_rule(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), beta.to(DEV), initial_state=h0.to(DEV),
+                                  output_final_state=True, use_qk_l2norm_in_kernel=True)
+    od, sd = fused_recurrent_gated_delta_rule(q[:, :1].to(DEV), k[:, :1].to(DEV), v[:, :1].to(DEV), g[:, :1].to(DEV),
+                                              beta[:, :1].to(DEV), initial_state=h0.to(DEV), output_final_state=True,
+                                              use_qk_l2norm_in_kernel=True)
+    for i in range(b):
+        args = [np64(x[i:i + 1]) for x in (q, k, v, g, beta)]
+        o_ref, s_ref = gdn.chunk_gated_delta_rule(*args, initial_state=np64(h0[i:i + 1]))
+        assert np.abs(np64(o[i:i + 1]) - o_ref).max() < O_TOL, i
+        assert gdn.state_rel_err(np64(s[i:i + 1]), s_ref) < S_TOL, i
+        od_ref, sd_ref = gdn.recurrent_gated_delta_rule(*(x[:, :1] for x in args), initial_state=np64(h0[i:i + 1]))
+        assert np.abs(np64(od[i:i + 1]) - od_ref).max() < O_TOL, i
+        assert gdn.state_rel_err(np64(sd[i:i + 1]), sd_ref) < S_TOL, i
