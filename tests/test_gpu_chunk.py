@@ -516,20 +516,21 @@ def test_per_pair_kernel_repeated_qk_equals_native():
     assert torch.equal(o1, o2) and torch.equal(s1, s2)
 
 
-@pytest.mark.parametrize("hk", [8, 4])
+@pytest.mark.parametrize("hk,hv", [(8, 32), (4, 32), (16, 48), (8, 16)])
 @pytest.mark.parametrize("b,t", [(1, 200), (8, 130)])
-def test_gqa_ratios_other_than_two(hk, b, t):
-    """32 v-heads over 8 or 4 k-heads (4 or 8 v-heads per k-head) on the
-    prep + scan path (B = 1) and the per-pair kernel (B = 8 x 32 pairs), and
-    the decode recurrence, against the oracle (which repeats the k-heads)."""
+def test_gqa_ratios_other_than_two(hk, hv, b, t):
+    """v-heads over k-heads at ratios 4, 8 and 3 and at 16 v-heads, on the
+    prep + scan path (B = 1), at B = 8 on the per-pair kernel (256 or 384
+    pairs) or the persistent scan (128 pairs), and the decode recurrence,
+    against the oracle (which repeats the k-heads)."""
     from engine.kernels import fused_recurrent_gated_delta_rule
-    gen = torch.Generator().manual_seed(60 + hk + b)
+    gen = torch.Generator().manual_seed(60 + hk + hv + b)
     q = torch.randn(b, t, hk, 128, generator=gen).to(torch.bfloat16)
     k = torch.randn(b, t, hk, 128, generator=gen).to(torch.bfloat16)
-    v = torch.randn(b, t, 32, 128, generator=gen).to(torch.bfloat16)
-    g = -torch.nn.functional.softplus(torch.randn(b, t, 32, generator=gen)) * 0.3
-    beta = torch.sigmoid(torch.randn(b, t, 32, generator=gen))
-    h0 = torch.randn(b, 32, 128, 128, generator=gen) * 0.1
+    v = torch.randn(b, t, hv, 128, generator=gen).to(torch.bfloat16)
+    g = -torch.nn.functional.softplus(torch.randn(b, t, hv, generator=gen)) * 0.3
+    beta = torch.sigmoid(torch.randn(b, t, hv, generator=gen))
+    h0 = torch.randn(b, hv, 128, 128, generator=gen) * 0.1
     o, s = chunk_gated_delta_rule(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), beta.to(DEV), initial_state=h0.to(DEV),
                                   output_final_state=True, use_qk_l2norm_in_kernel=True)
     od, sd = fused_recurrent_gated_delta_rule(q[:, :1].to(DEV), k[:, :1].to(DEV), v[:, :1].to(DEV), g[:, :1].to(DEV),
