@@ -158,15 +158,16 @@ def test_prefill_then_decode_continuation():
     assert torch.allclose(y_cat, y_full, atol=1e-5)
 
 
-def test_tile_lengths_agree():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_tile_lengths_agree(dtype):
     """The tile length follows the input's length (64, 56, 48 or 32 tokens:
     13,794 tokens run 56-token tiles, 5,000 run 48, 4,096 run 64 and 4,000
     run 32): the same tokens give the same bits whatever the tiling (and
-    match the oracle)."""
+    match the oracle), in each activation dtype."""
     gen = torch.Generator().manual_seed(12)
     c = configs.CONV_DIM
-    x = torch.randn(1, 13794, c, generator=gen).to(torch.bfloat16)
-    w = torch.randn(c, 4, generator=gen).to(torch.bfloat16)
+    x = torch.randn(1, 13794, c, generator=gen).to(dtype)
+    w = torch.randn(c, 4, generator=gen).to(dtype)
     xd, wd = x.to(DEV), w.to(DEV)
     y_short = causal_conv1d_fn(xd[:, :4000].transpose(1, 2), wd, None, activation="silu")
     for t in (13794, 5000, 4096):
