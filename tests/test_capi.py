@@ -163,7 +163,7 @@ def test_gated_entry_points_check_their_gate_arguments(lib):
     chunk = dict(q=256, k=256, v=256, qkv_dtype=1, qs=4096, ks=4096, vs=4096, a=1, b=1, ab_dtype=1, ab_stride=32,
                  A_log=None, dt_bias=1, h0=None, h0_idx=None, h0_rows=0, hT=None, hT_idx=None, hT_rows=0,
                  o=1, o_dtype=1,
-                 cu=None, n=1, t=64, hk=16, hv=32, kd=128, vd=128, scale=0.1, l2=1,
+                 cu=None, n=1, t=128, hk=16, hv=32, kd=128, vd=128, scale=0.1, l2=1,  # 2 chunks, 32 pairs: prep + scan
                  ws=None, ws_bytes=0, stream=None)
     assert lib.gdn_chunk_fwd_gated(*chunk.values()) == 1
     chunk.update(A_log=1)
