@@ -181,9 +181,10 @@ int gdn_chunk_fwd_gated(const void *q, const void *k, const void *v, int qkv_dty
  * `n_seqs` sequences (an upper bound that needs no knowledge of the lengths).
  * 0 when n_seqs * Hv >= 160: such a batch runs one workgroup per (sequence,
  * v-head) that keeps every chunk operand in LDS, and the workspace pointer
- * may then be NULL.  Dense batches (no cu_seqlens) of one 64-token chunk per
- * sequence, or of two at 96 pairs or more, run that kernel too and leave
- * the workspace they are given unused. */
+ * may then be NULL.  Batches whose longest sequence has one 64-token chunk,
+ * or two at 96 pairs or more (with cu_seqlens: whose total tokens fit one
+ * or two chunks), run that kernel too and leave the workspace they are
+ * given unused. */
 size_t gdn_chunk_workspace_bytes(int32_t n_seqs, int64_t total_tokens,
                                  int32_t Hv, int32_t K, int32_t V);
 

@@ -1855,10 +1855,11 @@ constexpr int SEG_CHUNKS = 64;
 // against 495, B = 2 x T = 4096 242 against 477: the local kernel from 5
 // sequences of 32 v-heads.
 constexpr int LOC_MIN_PAIRS = 160;
-// Short dense batches (no cu_seqlens, so every sequence has the same chunk
-// count) take the local kernel below that as well: one chunk per sequence
-// at any batch, two from LOC_SHORT2_PAIRS pairs, where prep + scan's fixed
-// latency outweighs a chunk step.  Measured from graphs (10 calls per
+// Short batches take the local kernel below that as well: one chunk per
+// sequence at any batch, two from LOC_SHORT2_PAIRS pairs, where prep + scan's
+// fixed latency outweighs a chunk step.  The chunk count is exact for a dense
+// batch (no cu_seqlens); with cu_seqlens its bound, the total tokens' chunks
+// (one sequence can hold them all), is used.  Measured from graphs (10 calls per
 // replay, Hv = 32), local against prep + scan: T = 64 at B = 1 / 2 / 3 / 4
 // 14.1 / 14.5 / 15.3 / 15.9 against 15.3 / 17.1 / 19.5 / 22.0 us; T = 128
 // 20.5 / 21.0 / 21.5 / 21.9 against 16.5 / 19.4 / 23.7 / 26.7; T = 256
@@ -1946,9 +1947,9 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
   // several sequences: the persistent scan once its (v-head, column tile)
   // workgroups fill the CUs without spreading the sequences over the grid
   // (sequence, v-head) pairs that fill the CUs: the local kernel, one workgroup per pair
-  const int64_t pairs = static_cast<int64_t>(n_seqs) * Hv, dense_chunks = (T + CK - 1) / CK;
-  const bool local = pairs >= LOC_MIN_PAIRS ||
-                     (!cu_seqlens && (dense_chunks == 1 || (dense_chunks == 2 && pairs >= LOC_SHORT2_PAIRS)));
+  const int64_t pairs = static_cast<int64_t>(n_seqs) * Hv;
+  const int64_t longest = cu_seqlens ? (total + CK - 1) / CK : (T + CK - 1) / CK;  // chunks, or their bound
+  const bool local = pairs >= LOC_MIN_PAIRS || longest == 1 || (longest == 2 && pairs >= LOC_SHORT2_PAIRS);
   const bool persist = n_seqs > 1 && static_cast<int64_t>(Hv) * (DV / SCAN_COLS) >= SCAN_PERSIST_BLOCKS;
   const int64_t seg = std::min<int64_t>(nc, SEG_CHUNKS);
   const WsLayout l = ws_layout(n_seqs, seg, Hv, nc > SEG_CHUNKS);

@@ -544,3 +544,22 @@ def test_gqa_ratios_other_than_two(hk, hv, b, t):
         od_ref, sd_ref = gdn.recurrent_gated_delta_rule(*(x[:, :1] for x in args), initial_state=np64(h0[i:i + 1]))
         assert np.abs(np64(od[i:i + 1]) - od_ref).max() < O_TOL, i
         assert gdn.state_rel_err(np64(sd[i:i + 1]), sd_ref) < S_TOL, i
+
+
+@pytest.mark.parametrize("lens", [[0, 17, 30, 0, 12], [40, 50, 0, 30]])
+def test_short_packed_batches_on_the_per_pair_kernel(lens):
+    """Packed batches whose total tokens fit one chunk (any pair count) or
+    two chunks at 96 pairs or more run the per-pair kernel, empty sequences
+    included (an empty one keeps its initial state), against the oracle."""
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32)
+    c = configs.config2(seed=57, t=int(cu[-1]))
+    h0 = torch.randn(len(lens), 32, 128, 128, generator=torch.Generator().manual_seed(2)) * 0.1
+    o_ref, s_ref = gdn.chunk_gated_delta_rule_varlen(*(c[x].float().numpy() for x in ("q", "k", "v", "g", "beta")),
+                                                     cu.numpy(), h0.numpy())
+    o, s = chunk_gated_delta_rule(*(c[x].to(DEV) for x in ("q", "k", "v", "g", "beta")), initial_state=h0.to(DEV),
+                                  output_final_state=True, use_qk_l2norm_in_kernel=True, cu_seqlens=cu.to(DEV))
+    assert np.abs(np64(o) - o_ref).max() < O_TOL
+    assert gdn.state_rel_err(np64(s), s_ref) < S_TOL
+    for i, n in enumerate(lens):
+        if n == 0:
+            assert torch.equal(s[i].cpu(), h0[i]), i
