@@ -6,7 +6,13 @@
 //   U = T (beta V),  W = T (beta e^gamma K~)
 //   V' = U - W S ;  O = (e^gamma Q~) S + lower(Q~K~^T * Gamma) V'
 //   S <- e^{gamma_63} S + (e^{gamma_63 - gamma} K~)^T V'
-// runs as up to three launches:
+// runs on one of two paths.  Batches of 160 or more (sequence, v-head) pairs,
+// and batches whose longest sequence has one chunk (or two, from 96 pairs),
+// take chunk_local_kernel: one 8-wave workgroup per pair walks its
+// sequence's chunks, 4 waves preparing chunk k while 4 run chunk k - 1's
+// state chain, every operand kept in LDS (no workspace); with cu_seqlens the
+// workgroups take the sequences longest first.  Otherwise up to three
+// launches:
 //   chunk_table_kernel  chunk -> sequence table (only with cu_seqlens)
 //   chunk_prep_kernel   one workgroup per (chunk, v-head), all in parallel:
 //                       K K^T and K Q^T on MFMA from the raw bf16 rows (exact
@@ -16,9 +22,11 @@
 //                       substitution on the 16x16 diagonal blocks and fp32 MFMA
 //                       below them; W = T' K and U = T'' V on MFMA with T', T''
 //                       split into bf16 hi + lo parts and K, V read transposed
-//                       (ds_read_b64_tr_b16).  Every operand the scan needs is
-//                       written pre-swizzled: one 1 KiB block per (MFMA, wave),
-//                       lane l's 16 bytes at offset 16 l.
+//                       (ds_read_b64_tr_b16).  -W, U, the A blocks and the
+//                       scalars are written pre-swizzled for the scan: one
+//                       1 KiB block per (MFMA, wave), lane l's 16 bytes at
+//                       offset 16 l (the scan reads q and k rows from the
+//                       inputs themselves).
 //   chunk_scan_kernel   one workgroup per (sequence, v-head, 16 state
 //                       columns), serial over the chunks: four compute waves,
 //                       each owning 16 chunk positions and 32 state rows (its
