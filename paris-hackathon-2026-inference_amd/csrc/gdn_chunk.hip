@@ -1615,11 +1615,13 @@ __device__ __forceinline__ void loc_u(const LocLds &L, int q, int lane) {
 // prepare chunk k (loc_prep, 7 barriers) while waves 4-7 run chunk k - 1's
 // chain, fitted between the same barriers: V' = U - W S before barrier 1,
 // the output and the state update between barriers 1 and 2 (the solve's
-// interval, the longest).  The operands the preparation writes before
-// barrier 2 (q fragments, A blocks, scalars) are double-buffered; -W, U and
-// K^T are written after barrier 6, when the chain has read them.  The next
-// chunk's rows are requested after barrier 6, when the current ones are in
-// LDS.  143 KiB of LDS: one workgroup per CU.
+// interval, the longest); between barriers 6 and 7 they form chunk k's U
+// for their column tiles, and wave 4 forms chunk k + 1's gates before the
+// next barrier 1.  The operands the preparation writes before barrier 2
+// (q fragments, A blocks, scalars) are double-buffered; -W, U and K^T are
+// written after barrier 6, when the chain has read them.  The next chunk's
+// rows are requested after barrier 6, when the current ones are in LDS.
+// 159 KiB of LDS: one workgroup per CU.
 constexpr int LOC_WAVES = 8;
 constexpr int LOC_LPT_MAX = 64 * LOC_WAVES;  // sequences ranked in the prologue, one per thread
 
