@@ -1965,6 +1965,7 @@ int chunk_fwd(const void *q, const void *k, const void *v, int qkv_dtype,
   const WsLayout l = ws_layout(n_seqs, seg, Hv, nc > SEG_CHUNKS);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (local) {  // one workgroup per (sequence, v-head); no workspace
+    if (pairs > 0x7fffffff) return fail(GDN_ERR_INVALID_ARGUMENT, "%s: grid too large", name);
     ChunkArgs a{static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
                 q_stride_t, k_stride_t, v_stride_t, gate, h0, h0_idx, h0_rows, hT, hT_idx, hT_rows, o, o_dtype,
                 cu_seqlens, n_seqs, T, Hk, Hv, total, scale, l2norm_qk, static_cast<int>(std::min<int64_t>(nc, 0x7fffffff)),
