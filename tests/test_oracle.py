@@ -151,6 +151,35 @@ def test_chunk_equals_recurrence_unequal_dims(dk, dv):
     assert np.abs(o1 - o2).max() < 1e-10 and gdn.state_rel_err(s2, s1) < 1e-10
 
 
+def test_chunk_equals_recurrence_at_extreme_gates():
+    """g in {0, -40, ordinary} (e^{-40} = 4e-18; a chunk's cumsum reaches
+    -2560 and its exponentials underflow) and beta in {0, 1, ordinary}: the
+    chunk form exps only non-positive cumsum differences, so it stays finite
+    and equal to the recurrence (the GPU tests' comparator at these gates)."""
+    rng = np.random.default_rng(77)
+    q, k, v, g, beta, h0 = rand_inputs(1, 150, 2, 4, 16, rng=rng)
+    pick = rng.integers(0, 3, g.shape)
+    g = np.where(pick == 0, 0.0, np.where(pick == 1, -40.0, g))
+    pick = rng.integers(0, 3, beta.shape)
+    beta = np.where(pick == 0, 0.0, np.where(pick == 1, 1.0, beta))
+    o1, s1 = gdn.recurrent_gated_delta_rule(q, k, v, g, beta, h0)
+    o2, s2 = gdn.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=h0)
+    assert np.isfinite(o2).all() and np.isfinite(s2).all()
+    assert np.abs(o1 - o2).max() < 1e-11 and gdn.state_rel_err(s2, s1) < 1e-11
+
+
+def test_full_decay_forgets_the_state():
+    """g = -40 on every token: the state carried into a token is ~4e-18 of
+    itself, so o_t = beta_t (q~_t . k~_t) v_t to that precision."""
+    q, k, v, g, beta, h0 = rand_inputs(1, 70, 2, 4, 16)
+    g[:] = -40.0
+    o, _ = gdn.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=h0)
+    qn = gdn.expand_heads(gdn.l2norm(q), 4) * 16 ** -0.5
+    kn = gdn.expand_heads(gdn.l2norm(k), 4)
+    expect = (beta * (qn * kn).sum(-1))[..., None] * v
+    assert np.allclose(o, expect, rtol=1e-12, atol=1e-14)
+
+
 def test_forward_substitution_is_the_inverse():
     c = 64
     lower = np.tril(RNG.standard_normal((3, c, c)) * 0.3, -1)
