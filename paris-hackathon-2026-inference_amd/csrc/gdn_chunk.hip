@@ -87,9 +87,6 @@ __device__ __forceinline__ int64_t uniform64(int64_t x) {
   const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(x) >> 32));
   return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
-__device__ __forceinline__ uint16_t bf16_rne(float x) {  // hardware round-to-nearest-even
-  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
-}
 __device__ __forceinline__ bf16x8 pack_hi(f32x4 a, f32x4 b) {
   bf16x8 r;
 #pragma unroll
