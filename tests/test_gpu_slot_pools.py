@@ -20,7 +20,6 @@ path), states relative error <= 1e-2, conv windows max abs error <= 2e-2.
 """
 import types
 
-import numpy as np
 import pytest
 import torch
 
