@@ -1334,7 +1334,9 @@ struct LocLds {
   f32x4 *tx;        // [4][4][64] T's rows by position tile (row layout), for the W and U products
 };
 
-__device__ __forceinline__ void loc_load(const ChunkArgs &a, LocIn &in, int64_t t0, int len, int h, int hk, int tid) {
+// One chunk's rows into `in`: part 0 K and Q, part 1 V, part 2 all three.
+__device__ __forceinline__ void loc_load(const ChunkArgs &a, LocIn &in, int64_t t0, int len, int h, int hk, int tid,
+                                         int part = 2) {
   const int lane = tid & 63, p = tid >> 6, g4 = lane >> 4, irow = 16 * p + (lane & 15), seg = tid & 15;
   // buffer ranges end at the chunk's last row: rows past it read as zero
   auto rows_rsrc = [&](const uint16_t *base, int64_t stride, int head) {
@@ -1344,12 +1346,21 @@ __device__ __forceinline__ void loc_load(const ChunkArgs &a, LocIn &in, int64_t 
   };
   const auto rk = rows_rsrc(a.k, a.ks, hk), rv = rows_rsrc(a.v, a.vs, h), rq = rows_rsrc(a.q, a.qs, hk);
   const int ks2 = static_cast<int>(a.ks * 2), vs2 = static_cast<int>(a.vs * 2), qs2 = static_cast<int>(a.qs * 2);
+  if (part != 1) {
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int row = (tid >> 4) + 16 * it;
-    in.ku[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, row * ks2 + seg * 16, 0, 0));
-    in.vu[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, row * vs2 + seg * 16, 0, 0));
+    for (int it = 0; it < 4; ++it) {
+      const int row = (tid >> 4) + 16 * it;
+      in.ku[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, row * ks2 + seg * 16, 0, 0));
+    }
   }
+  if (part != 0) {
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int row = (tid >> 4) + 16 * it;
+      in.vu[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, row * vs2 + seg * 16, 0, 0));
+    }
+  }
+  if (part == 1) return;
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const int off = irow * qs2 + (32 * s + 4 * g4) * 2;
@@ -1387,11 +1398,15 @@ __device__ __forceinline__ void loc_gates(const ChunkArgs &a, const GateRaw &g, 
 
 // Phase A of one chunk on waves 0-3 (thread tid < 256), from the registers of
 // loc_load into the LDS operands of the chain.
-// after_v() runs once the chunk's inputs in `in` are consumed (after barrier
-// 6): the caller may request the next chunk's into it there.
-template <class AfterV>
+// after_kq() runs once the chunk's K and Q rows in `in` are consumed (after
+// barrier 1) and after_v() once its V rows are (in LDS, before barrier 6):
+// the caller requests the next chunk's rows into `in` there, so that no
+// load is issued in the interval after barrier 6 (measured: B = 16 x
+// T = 1038 and configuration 3's prefill ~1% faster than with all the
+// loads after barrier 6).
+template <class AfterKQ, class AfterV>
 __device__ __forceinline__ void loc_prep(const ChunkArgs &a, const LocIn &in, const LocLds &L, int len, int tid,
-                                         const AfterV &after_v) {
+                                         const AfterKQ &after_kq, const AfterV &after_v) {
   const int lane = tid & 63, p = tid >> 6, g4 = lane >> 4, r16 = lane & 15, seg = tid & 15;
   const int irow = 16 * p + r16;
   uint16_t *kn = L.kn;
@@ -1433,6 +1448,7 @@ __device__ __forceinline__ void loc_prep(const ChunkArgs &a, const LocIn &in, co
     if (g4 == 0) L.nq_s[irow] = (a.l2norm ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
   }
   lds_barrier();  // (1)
+  after_kq();
 
   if (p == 0) {  // per-position scalars of the chain, W's column scale
     const float gl = L.gam_s[CK - 1], gm = L.gam_s[lane], nkl = L.nk_s[lane];
@@ -1540,8 +1556,8 @@ __device__ __forceinline__ void loc_prep(const ChunkArgs &a, const LocIn &in, co
 #pragma unroll
   for (int it = 0; it < 4; ++it)
     *reinterpret_cast<u32x4 *>(vn + nsw((tid >> 4) + 16 * it, seg * 8)) = in.vu[it];
-  lds_barrier();  // (6)
   after_v();
+  lds_barrier();  // (6)
 
   // ---- -W = -(T diag(colw) K), as W^T tiles K^T (T diag(colw))^T, for the
   // column tiles 2p and 2p + 1 over every position tile (T's rows from L.tx):
@@ -1617,7 +1633,8 @@ __device__ __forceinline__ void loc_u(const LocLds &L, int q, int lane) {
 // next barrier 1.  The operands the preparation writes before barrier 2
 // (q fragments, A blocks, scalars) are double-buffered; -W, U and K^T are
 // written after barrier 6, when the chain has read them.  The next chunk's
-// rows are requested after barrier 6, when the current ones are in LDS.
+// K and Q rows are requested after barrier 1 and its V rows before barrier
+// 6, each once the current ones are in LDS.
 // 159 KiB of LDS: one workgroup per CU.
 constexpr int LOC_WAVES = 8;
 constexpr int LOC_LPT_MAX = 64 * LOC_WAVES;  // sequences ranked in the prologue, one per thread
@@ -1695,7 +1712,9 @@ __global__ __launch_bounds__(64 * LOC_WAVES) void chunk_local_kernel(ChunkArgs a
       asm volatile("" : "+v"(tk));
       const LocLds L{kn, s16k, ktf, qp2[k & 1], wb, ub, ab2[k & 1], sc2[k & 1], gam_s, beta_s, nk_s, nq_s, colw_s, tx};
       loc_prep(a, in, L, chunk_len(k), tk, [&] {
-        if (k + 1 < nch) loc_load(a, in, s0 + static_cast<int64_t>(k + 1) * CK, chunk_len(k + 1), h, hk, tk);
+        if (k + 1 < nch) loc_load(a, in, s0 + static_cast<int64_t>(k + 1) * CK, chunk_len(k + 1), h, hk, tk, 0);
+      }, [&] {
+        if (k + 1 < nch) loc_load(a, in, s0 + static_cast<int64_t>(k + 1) * CK, chunk_len(k + 1), h, hk, tk, 1);
       });
     }
     if (nch > 0)  // step nch: the chain's last chunk
